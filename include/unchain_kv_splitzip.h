@@ -1,0 +1,153 @@
+/*
+ * C ABI of libunchain_kv_splitzip_cuda.so, the MI355X (gfx950) splitzip bf16
+ * KV-cache codec.
+ *
+ * Every pointer, size and stream is passed as unsigned long long (a hipStream_t
+ * for the stream; 0 is the null stream); every call only enqueues work on that
+ * stream and returns without synchronising. Return convention (all functions
+ * returning long long):
+ *   > 0  bytes encoded / bytes written;
+ *     0  declined: a precondition failed and nothing was launched (the caller
+ *        falls back to another codec);
+ *   < 0  a launch failed; the message is in kvq_splitzip_last_error().
+ * Top-16 overflow is in-band: byte 0 of the payload is 255 once the stream has
+ * run the encode.
+ *
+ * The first eight entry points have the names, argument order and meaning of the
+ * reference library (native/unchain_kv/kvq_splitzip_cuda.cu); their comments cite
+ * the function each one replaces. The rest are additions.
+ */
+#ifndef UNCHAIN_KV_SPLITZIP_H_
+#define UNCHAIN_KV_SPLITZIP_H_
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Replaces kvq_splitzip_last_error (kvq_splitzip_cuda.cu:288): message of the last
+ * failed call on this host thread. */
+const char* kvq_splitzip_last_error(void);
+
+/* Replaces kvq_splitzip_bf16_encode_mode (kvq_splitzip_cuda.cu:292). Palette encode
+ * of `count` contiguous bf16 words at src into dst: bits 6 -> mode 3 (64-entry
+ * palette), bits 5 -> mode 4 (32-entry). Returns the encoded size; 0 if bits is not
+ * 5/6, if the encoded size is not below 2*count, or if capacity is smaller than
+ * align4(encoded) + 1032 (scratch after the payload). The palette is ascending. */
+long long kvq_splitzip_bf16_encode_mode(unsigned long long src_ptr, unsigned long long dst_ptr,
+                                        unsigned long long count, unsigned long long capacity,
+                                        unsigned long long stream_ptr, int bits);
+
+/* Replaces kvq_splitzip_bf16_encode (kvq_splitzip_cuda.cu:335): encode_mode, bits 6. */
+long long kvq_splitzip_bf16_encode(unsigned long long src_ptr, unsigned long long dst_ptr,
+                                   unsigned long long count, unsigned long long capacity,
+                                   unsigned long long stream_ptr);
+
+/* Replaces kvq_splitzip_bf16_decode_fixed6_blocks (kvq_splitzip_cuda.cu:344). Decodes a
+ * mode-3 payload of count_words = 2*block_count*block_words words and writes word i
+ * to dst[p*plane_stride + blk*block_stride + within] (p = K/V plane, blk =
+ * block_ids[j] or block_start + j when block_ids_ptr is 0). encoded_bytes must be
+ * 65 + n + 3*ceil(n/4). Returns 2*count_words; a payload whose byte 0 is not 3 is
+ * left unapplied. */
+long long kvq_splitzip_bf16_decode_fixed6_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long block_ids_ptr, unsigned long long stream_ptr);
+
+/* Replaces kvq_splitzip_bf16_decode_fixed6 (kvq_splitzip_cuda.cu:370): contiguous
+ * block run starting at block_start. */
+long long kvq_splitzip_bf16_decode_fixed6(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long stream_ptr);
+
+/* Replaces kvq_splitzip_bf16_encode_top16 (kvq_splitzip_cuda.cu:381). Top-16 encode
+ * (mode 5) of `count` contiguous bf16 words; the K/V split is at count/2. tables_ptr
+ * is the 544-byte device table. Returns E = 5 + n + ceil(n/2) + 5*ceil(n/200); 0 if
+ * count is 0 or above 2^32-1, if E >= 2*count, or if capacity < align4(E) + 8.
+ * When capacity leaves room past the payload (16-byte aligned, 260 bytes per
+ * 4096-word tile) the tiles are encoded in parallel using it as workspace;
+ * otherwise one workgroup encodes the tiles in order. Escapes are written in
+ * ascending position order and unused escape slots are zeroed. */
+long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr, unsigned long long dst_ptr,
+                                         unsigned long long count, unsigned long long capacity,
+                                         unsigned long long tables_ptr,
+                                         unsigned long long stream_ptr);
+
+/* Replaces kvq_splitzip_bf16_decode_top16_blocks (kvq_splitzip_cuda.cu:416). Decodes a
+ * mode-5 payload and scatters it like decode_fixed6_blocks; escapes are applied in
+ * any order. encoded_bytes must equal E(count_words). Returns 2*count_words; a
+ * payload whose byte 0 is not 5 is left unapplied. */
+long long kvq_splitzip_bf16_decode_top16_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long block_ids_ptr, unsigned long long tables_ptr,
+    unsigned long long stream_ptr);
+
+/* Replaces kvq_splitzip_bf16_decode_top16 (kvq_splitzip_cuda.cu:453): contiguous run. */
+long long kvq_splitzip_bf16_decode_top16(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long tables_ptr, unsigned long long stream_ptr);
+
+/* ------------------------------------------------------------------------------
+ * Additions: every request of one paged layer in one launch.
+ *
+ * The reference gathers each request's blocks with torch.index_select into a packed
+ * copy and then encodes that copy (src/unchain_kv/vllm_connector.py:2827-2869,
+ * 3105); these entry points read the blocks in place through the block table and
+ * handle all requests of a layer per launch (up to 64 payloads per launch, more in
+ * several launches).
+ *
+ * Payload r consists of blocks block_ids[block_offsets[r] .. block_offsets[r+1]) of
+ * the layer `kv` (words at kv[p*plane_stride + id*block_stride + w], w <
+ * block_words); its n_r = 2*blocks_r*block_words words are ordered K then V, block
+ * table order, then within the block, exactly as kv_layer[:, ids].contiguous().
+ * block_offsets, out_offsets, src_offsets and encoded_bytes are HOST arrays;
+ * block_ids is a DEVICE int64 array.
+ * ---------------------------------------------------------------------------- */
+
+/* Workspace bytes that kvq_splitzip_bf16_encode_top16_paged needs for this batch
+ * (no counterpart in the reference). */
+unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count);
+
+/* Gather + Top-16 encode (no counterpart in the reference; it replaces the
+ * index_select + kvq_splitzip_bf16_encode_top16 pair per request). Payload r goes to
+ * out + out_offsets[r]; payloads must not overlap and must fit in out_capacity.
+ * workspace must hold kvq_splitzip_top16_paged_workspace_bytes() bytes. Returns the
+ * sum of the encoded sizes, or 0 when a precondition fails. */
+long long kvq_splitzip_bf16_encode_top16_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long stream_ptr);
+
+/* Top-16 decode + scatter of a batch (no counterpart in the reference; it replaces one
+ * kvq_splitzip_bf16_decode_top16_blocks call per request). Payload r is read from
+ * src + src_offsets[r] and must be encoded_bytes[r] = E(n_r) long; it is written into
+ * the blocks of block table r. Returns the total raw bytes (sum of 2*n_r). */
+long long kvq_splitzip_bf16_decode_top16_paged(
+    unsigned long long src_ptr, const unsigned long long* src_offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long tables_ptr,
+    unsigned long long stream_ptr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UNCHAIN_KV_SPLITZIP_H_ */

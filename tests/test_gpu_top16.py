@@ -1,0 +1,331 @@
+"""GPU parity of the HIP Top-16 codec against the CPU oracle.
+
+Encode output must be byte-identical to the oracle's canonical payload
+(escapes ascending, unused slots zeroed); decode + scatter must reproduce the
+source bf16 words exactly, for payloads from the oracle (canonical) and for
+payloads with shuffled escapes and garbage padding (the byte streams the
+reference's atomic-ordered encoder produces).
+"""
+
+import random
+
+import numpy as np
+import pytest
+
+import oracle
+from unchainkv_amd import codec_format
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sz():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU visible")
+    from unchainkv_amd import splitzip_cuda
+
+    assert splitzip_cuda.available(), splitzip_cuda.load_error()
+    return splitzip_cuda
+
+
+def u16(t) -> np.ndarray:
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+
+
+def bf16(words: np.ndarray, device="cuda"):
+    return torch.from_numpy(np.ascontiguousarray(words).view(np.int16).copy()).to(device).view(
+        torch.bfloat16)
+
+
+def random_words(rng, n, books, escape_rate):
+    half = n // 2
+    k_book = np.frombuffer(books[:16], dtype=np.uint8)
+    v_book = np.frombuffer(books[16:], dtype=np.uint8)
+    outside = np.array(sorted(set(range(256)) - set(books)), dtype=np.uint16)
+    exps = np.empty(n, dtype=np.uint16)
+    exps[:half] = k_book[rng.integers(0, 16, half)]
+    exps[half:] = v_book[rng.integers(0, 16, n - half)]
+    esc = rng.random(n) < escape_rate
+    exps[esc] = outside[rng.integers(0, outside.size, int(esc.sum()))]
+    low = rng.integers(0, 128, n).astype(np.uint16)
+    sign = rng.integers(0, 2, n).astype(np.uint16) << 15
+    return (sign | (exps << 7) | low).astype(np.uint16)
+
+
+def say(*parts):
+    print("[case]", *parts, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# known answers
+
+def test_kat256_encode_and_decode(sz, golden_dir, codebooks):
+    import json
+
+    kat = json.loads((golden_dir / "kat_top16_256.json").read_text())
+    payload = bytes.fromhex(kat["payload_hex"])
+    words = np.frombuffer(bytes.fromhex(kat["raw_hex"]), "<u2").copy()
+    say("kat256 encode")
+    source = bf16(words)
+    out = torch.empty(512, dtype=torch.uint8, device="cuda")
+    size = sz.encode_top16(source, out, 0)
+    torch.cuda.synchronize()
+    assert size == len(payload)
+    assert bytes(out[:size].cpu().numpy()) == payload
+    say("kat256 decode")
+    comp = torch.tensor(list(payload), dtype=torch.uint8, device="cuda")
+    target = torch.zeros((2, 16, 8), dtype=torch.bfloat16, device="cuda")
+    copied = sz.decode_top16(comp, target, list(range(16)), 512, 0)
+    torch.cuda.synchronize()
+    assert copied == 512
+    assert np.array_equal(u16(target), words)
+
+
+@pytest.mark.parametrize("block_count,target_blocks,block_ids", [
+    (1, 4, [3]), (128, 256, list(range(0, 256, 2)))])
+def test_reference_roundtrip_inputs(sz, codebooks, block_count, target_blocks, block_ids):
+    """tests/test_splitzip_cuda.py:137-185 of the reference, plus byte parity."""
+    say("reference roundtrip", block_count)
+    count = 2 * block_count * 2048
+    index = torch.arange(count, dtype=torch.int32, device="cuda")
+    books = torch.tensor(list(codebooks[:32]), device="cuda").reshape(2, 16)
+    plane = torch.div(index, count // 2, rounding_mode="floor")
+    exponent = books[plane.long(), torch.remainder(index, 16).long()]
+    exponent[::400] = 100
+    words = torch.bitwise_or(
+        torch.bitwise_left_shift(torch.remainder(index, 2), 15),
+        torch.bitwise_or(torch.bitwise_left_shift(exponent.to(torch.int32), 7),
+                         torch.remainder(index, 128))).to(torch.int16)
+    source = words.view(torch.bfloat16).reshape(2, block_count, 2048)
+    raw_bytes = source.numel() * source.element_size()
+    encoded = torch.empty(raw_bytes, dtype=torch.uint8, device="cuda")
+    size = sz.encode_top16(source, encoded, 0)
+    target = torch.zeros((2, target_blocks, 2048), dtype=torch.bfloat16, device="cuda")
+    copied = sz.decode_top16(encoded[:size], target, block_ids, raw_bytes, 0)
+    torch.cuda.synchronize()
+    assert raw_bytes / size >= 1.30
+    assert int(encoded[0].item()) == 5
+    assert copied == raw_bytes
+    assert torch.equal(target[:, block_ids].view(torch.int16), source.view(torch.int16))
+    ref = oracle.top16_encode(u16(source), oracle.top16_tables(codebooks[:32]))
+    assert bytes(encoded[:size].cpu().numpy()) == bytes(ref)
+
+
+# ---------------------------------------------------------------------------
+# drop-in entry points: sizes, misalignment, capacity modes
+
+@pytest.mark.parametrize("n", [22, 23, 255, 256, 1000, 4096, 8192, 8202, 65536, 200_000])
+@pytest.mark.parametrize("shift", [0, 3, 11])
+@pytest.mark.parametrize("roomy", [True, False])
+def test_dropin_encode_matches_oracle(sz, codebooks, n, shift, roomy):
+    say("dropin encode", n, shift, roomy)
+    rng = np.random.default_rng(n + 17 * shift)
+    books = codebooks[7 * 32:8 * 32]
+    words = random_words(rng, n, books, 0.003)
+    ref = oracle.top16_encode(words, oracle.top16_tables(books))
+    size = codec_format.top16_encoded_size(n)
+    capacity = 2 * n if roomy else ((size + 3) & ~3) + 8
+    if ref is None or capacity < ((size + 3) & ~3) + 8:
+        pytest.skip("the reference declines this size")
+    backing = torch.full((capacity + shift + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    out = backing[shift:shift + capacity]
+    source = bf16(words)
+    got = sz.encode_top16(source, out, 7)
+    torch.cuda.synchronize()
+    assert got == size
+    assert bytes(out[:size].cpu().numpy()) == bytes(ref)
+    # nothing before the payload was touched
+    assert bytes(backing[:shift].cpu().numpy()) == b"\xa5" * shift
+
+
+def test_dropin_encode_unaligned_source(sz, codebooks):
+    say("dropin encode unaligned source")
+    rng = np.random.default_rng(5)
+    n = 9000
+    books = codebooks[:32]
+    words = random_words(rng, n + 1, books, 0.002)
+    backing = bf16(words)
+    source = backing[1:]  # 2-byte offset: not 16-byte aligned
+    out = torch.empty(2 * n, dtype=torch.uint8, device="cuda")
+    got = sz.encode_top16(source, out, 0)
+    torch.cuda.synchronize()
+    ref = oracle.top16_encode(words[1:], oracle.top16_tables(books))
+    assert bytes(out[:got].cpu().numpy()) == bytes(ref)
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.004, 0.02])
+@pytest.mark.parametrize("bw,blocks,pool", [(2048, 8, 40), (16384, 3, 12), (48, 50, 120), (40, 30, 90)])
+def test_dropin_decode_scatter_matches_oracle(sz, codebooks, rate, bw, blocks, pool):
+    say("dropin decode", rate, bw, blocks)
+    rng = np.random.default_rng(bw + blocks)
+    books = codebooks[11 * 32:12 * 32]
+    n = 2 * blocks * bw
+    words = random_words(rng, n, books, rate)
+    tables = oracle.top16_tables(books)
+    payload = oracle.top16_encode(words, tables)
+    ids = sorted(rng.choice(pool, blocks, replace=False).tolist(), key=lambda _: rng.random())
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    marker = torch.full_like(target, 1.5)
+    target.copy_(marker)
+    comp = torch.from_numpy(payload.copy()).cuda()
+    copied = sz.decode_top16(comp, target, ids, 2 * n, -1, codebooks=books)
+    torch.cuda.synchronize()
+    assert copied == 2 * n
+    expected = np.full((2, pool, bw), u16(marker)[0], np.uint16)
+    if payload[0] == 5:
+        oracle.scatter(oracle.top16_decode(payload, n, tables), expected.reshape(-1), blocks, bw,
+                       pool * bw, bw, ids=ids)
+    assert np.array_equal(u16(target), expected.reshape(-1))
+
+
+def test_decode_accepts_shuffled_escapes_and_garbage_padding(sz, codebooks):
+    say("decode shuffled escapes")
+    rng = np.random.default_rng(21)
+    bw, blocks, pool = 1024, 16, 40
+    n = 2 * blocks * bw
+    books = codebooks[2 * 32:3 * 32]
+    tables = oracle.top16_tables(books)
+    words = random_words(rng, n, books, 0.004)
+    payload = bytearray(oracle.top16_encode(words, tables))
+    count = int.from_bytes(payload[1:5], "little")
+    lo, hi = codec_format.top16_sections(n)["escapes"]
+    slots = [bytes(payload[lo + 5 * s: lo + 5 * s + 5]) for s in range(count)]
+    random.Random(3).shuffle(slots)
+    payload[lo:lo + 5 * count] = b"".join(slots)
+    payload[lo + 5 * count:hi] = bytes(rng.integers(0, 256, hi - lo - 5 * count, dtype=np.uint8))
+    ids = rng.permutation(pool)[:blocks].tolist()
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    comp = torch.tensor(list(payload), dtype=torch.uint8, device="cuda")
+    assert sz.decode_top16(comp, target, ids, 2 * n, -1, codebooks=books) == 2 * n
+    torch.cuda.synchronize()
+    got = u16(target).reshape(2, pool, bw)[:, ids].reshape(-1)
+    assert np.array_equal(got, words)
+
+
+def test_decode_leaves_overflowed_payload_unapplied(sz, codebooks):
+    say("decode mode 255")
+    n = 2 * 4 * 512
+    payload = torch.zeros(codec_format.top16_encoded_size(n), dtype=torch.uint8, device="cuda")
+    payload[0] = 255
+    target = torch.full((2, 8, 512), 2.0, dtype=torch.bfloat16, device="cuda")
+    assert sz.decode_top16(payload, target, [1, 5, 2, 7], 2 * n, 0) == 2 * n
+    torch.cuda.synchronize()
+    assert torch.all(target == 2.0)
+
+
+# ---------------------------------------------------------------------------
+# escape-heavy tiles (finalize re-scan path) and overflow
+
+def test_tile_with_many_escapes_and_overflow(sz, codebooks):
+    books = codebooks[4 * 32:5 * 32]
+    tables = oracle.top16_tables(books)
+    rng = np.random.default_rng(8)
+    n = 2 * 8 * 4096  # 16 tiles, cap 328
+    words = random_words(rng, n, books, 0.0)
+    outside = sorted(set(range(256)) - set(books))
+    # 200 escapes packed into tile 3 (more than the 64 staged per tile), 50 elsewhere
+    for pos in list(range(3 * 4096 + 100, 3 * 4096 + 300)) + rng.choice(n, 50, replace=False).tolist():
+        words[pos] = (words[pos] & 0x807F) | (outside[pos % len(outside)] << 7)
+    for label, w in (("dense tile", words), ("overflow", random_words(rng, n, books, 0.01))):
+        say("escape-heavy", label)
+        ref = oracle.top16_encode(w, tables)
+        out = torch.empty(2 * n, dtype=torch.uint8, device="cuda")
+        size = sz.encode_top16(bf16(w), out, -1, codebooks=books)
+        torch.cuda.synchronize()
+        assert bytes(out[:size].cpu().numpy()) == bytes(ref)
+    assert ref[0] == 255
+
+
+# ---------------------------------------------------------------------------
+# batched paged entry points
+
+@pytest.mark.parametrize("bw,pool,requests,rate,offset", [
+    (16384, 64, [8, 16, 3], 0.0005, 0),     # Llama-3-8B block (8 heads x 128 x 16)
+    (2048, 300, [8, 40, 17, 64], 0.001, 0),  # 70B TP8 share (1 head)
+    (8192, 80, [64], 0.002, 0),             # Llama-3.2-1B block
+    (48, 400, [50, 7, 99], 0.003, 0),       # small block, several blocks per tile
+    (40, 300, [60, 5], 0.003, 0),           # block words not a multiple of 16: generic path
+    (2048, 100, [10, 20], 0.001, 1),        # KV view at a 2-byte offset: generic path
+])
+def test_paged_encode_decode_matches_oracle(sz, codebooks, bw, pool, requests, rate, offset):
+    say("paged", bw, pool, requests, rate, offset)
+    rng = np.random.default_rng(bw * 3 + pool)
+    books = codebooks[9 * 32:10 * 32]
+    tables = oracle.top16_tables(books)
+    words = random_words(rng, 2 * pool * bw + offset, books, rate)
+    backing = bf16(words)
+    kv = backing[offset:].view(2, pool, bw)
+    kv_host = words[offset:].reshape(2, pool, bw)
+    perm = rng.permutation(pool).tolist()
+    block_tables, at = [], 0
+    for r in requests:
+        block_tables.append(perm[at:at + r])
+        at += r
+    batch = sz.PagedBatch(block_tables, bw, "cuda")
+    out = batch.new_payload_buffer()
+    out.fill_(0x5A)
+    ws = batch.new_workspace()
+    # with offset=1 the layer starts 2 bytes past a 16-byte boundary and the
+    # library takes its generic (any alignment) kernels
+    total = sz.encode_top16_paged(kv, batch, out, ws, codebooks=books)
+    torch.cuda.synchronize()
+    assert total == batch.total_encoded_bytes
+    host = out.cpu().numpy()
+    for r, t in enumerate(block_tables):
+        ref = oracle.top16_encode(kv_host[:, t].reshape(-1), tables)
+        got = host[batch.out_offsets[r]:batch.out_offsets[r] + batch.encoded_bytes[r]]
+        assert bytes(got) == bytes(ref), f"payload {r}"
+    # receiver with an independent block table
+    rperm = rng.permutation(pool).tolist()
+    recv_tables, at = [], 0
+    for r in requests:
+        recv_tables.append(rperm[at:at + r])
+        at += r
+    recv_batch = sz.PagedBatch(recv_tables, bw, "cuda")
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    copied = sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, target,
+                                   recv_batch, codebooks=books)
+    torch.cuda.synchronize()
+    assert copied == batch.total_raw_bytes
+    got = u16(target).reshape(2, pool, bw)
+    for src_t, dst_t in zip(block_tables, recv_tables):
+        assert np.array_equal(got[:, dst_t], kv_host[:, src_t])
+    used = {b for t in recv_tables for b in t}
+    free = [b for b in range(pool) if b not in used]
+    assert not got[:, free].any()
+
+
+def test_paged_full_size_llama3_8b_layer(sz):
+    """One full layer of the Llama-3-8B paged encode workload (8 requests x 4096
+    tokens from a 4096-block pool): byte parity of every payload with the oracle
+    and an exact round trip into an independent receiver table."""
+    from unchainkv_amd import workloads
+
+    shape = workloads.LLAMA3_8B
+    say("full-size llama3-8b layer")
+    kv = workloads.make_kv_layer(torch, shape, 4096, seed=1, layer=5, device="cuda")
+    tables = workloads.random_block_tables(torch, 4096, [256] * 8, seed=1)
+    books = workloads.fit_codebook(torch, kv, tables)
+    batch = sz.PagedBatch(tables, shape.block_words, "cuda")
+    out = batch.new_payload_buffer()
+    ws = batch.new_workspace()
+    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books) == batch.total_encoded_bytes
+    recv_tables = workloads.random_block_tables(torch, 4096, [256] * 8, seed=2)
+    recv_batch = sz.PagedBatch(recv_tables, shape.block_words, "cuda")
+    target = torch.zeros_like(kv)
+    assert sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, target, recv_batch,
+                                 codebooks=books) == batch.total_raw_bytes
+    torch.cuda.synchronize()
+    src_ids = torch.tensor([b for t in tables for b in t], device="cuda")
+    dst_ids = torch.tensor([b for t in recv_tables for b in t], device="cuda")
+    assert torch.equal(kv.view(torch.int16)[:, src_ids], target.view(torch.int16)[:, dst_ids])
+    host = out.cpu().numpy()
+    kv_host = u16(kv).reshape(2, 4096, -1)
+    ref = oracle.encode_paged_batch(kv_host, 4096 * shape.block_words, shape.block_words,
+                                    shape.block_words, tables, batch.out_offsets, batch.out_bytes,
+                                    oracle.top16_tables(books), threads=oracle.default_threads())
+    for r in range(8):
+        a, b = batch.out_offsets[r], batch.out_offsets[r] + batch.encoded_bytes[r]
+        assert host[a] == 5
+        assert bytes(host[a:b]) == bytes(ref[a:b]), f"payload {r}"

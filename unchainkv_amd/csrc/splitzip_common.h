@@ -1,0 +1,187 @@
+// Shared device helpers for the splitzip bf16 codec kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace unchainkv {
+
+// Error reporting shared by every C entry point: the message is kept per host
+// thread and returned by kvq_splitzip_last_error().
+long long fail(const char* what, hipError_t status);
+long long fail_msg(const std::string& msg);
+
+constexpr int kThreads = 256;                         // 4 waves of 64
+constexpr int kWave = 64;
+constexpr int kWordsPerLane = 16;                     // 32 B of bf16 per lane
+constexpr int kTileWords = kThreads * kWordsPerLane;  // 4096 words per workgroup tile
+constexpr int kTileShift = 12;
+static_assert((1 << kTileShift) == kTileWords, "tile size");
+
+// Escapes staged per tile by the encode kernel; tiles with more are re-scanned
+// by the finalize kernel.
+constexpr int kStageSlots = 64;
+// Payload descriptors passed by value in the kernel arguments.
+constexpr int kMaxPayloads = 64;
+
+struct PayloadDesc {
+  unsigned long long buf_offset;  // byte offset of the payload inside the payload buffer
+  unsigned long long ids_offset;  // first block id of this payload inside `ids`
+  unsigned int block_count;       // blocks per plane
+  unsigned int tile_begin;        // first tile of this payload within the launch
+};
+
+// One launch covers up to kMaxPayloads payloads of one paged layer (or one
+// contiguous payload). Word i of a payload lives at
+//   kv[p * plane_stride + block(j) * block_stride + within]
+// with p = i / plane_words, j = (i % plane_words) / block_words, within =
+// i % block_words, block(j) = ids[ids_offset + j] or block_start + j, and
+// plane_words = block_count * block_words. `linear` payloads are contiguous
+// (word i at kv[i]) with the K/V split at n / 2 for any n.
+struct LaunchArgs {
+  uint16_t* kv;
+  const long long* ids;
+  unsigned char* buf;
+  const unsigned char* tables;  // 544 B: [p*256+exp] -> code, then 2 x 16 codebook bytes
+  unsigned int* workspace;      // encode: per-tile escape counts, then staged escapes
+  unsigned long long plane_stride;
+  unsigned long long block_stride;
+  unsigned long long block_words;
+  unsigned long long block_start;
+  unsigned long long linear_words;  // n of a linear payload, else 0
+  unsigned int payload_count;
+  unsigned int total_tiles;
+  unsigned int tiles_per_plane_mode;  // 1: tiles never cross a plane (fast path); 0: one range [0, n)
+  unsigned int pad;
+  PayloadDesc p[kMaxPayloads];
+};
+
+// ---------------------------------------------------------------------------
+// launch-shape helpers
+
+// Workgroups are handed to the 8 XCDs round-robin; remap so each XCD walks a
+// contiguous run of tiles (neighbouring tiles share partial cache lines).
+__device__ __forceinline__ unsigned int xcd_remap(unsigned int wg, unsigned int count) {
+  unsigned int q = count >> 3, rem = count & 7, xcd = wg & 7, local = wg >> 3;
+  return xcd * q + min(xcd, rem) + local;
+}
+
+__device__ __forceinline__ unsigned int find_payload(const LaunchArgs& a, unsigned int tile) {
+  unsigned int r = 0;
+  for (unsigned int k = 1; k < a.payload_count; ++k)
+    if (a.p[k].tile_begin <= tile) r = k;
+  return r;
+}
+
+__device__ __forceinline__ unsigned long long payload_words(const LaunchArgs& a,
+                                                            const PayloadDesc& d) {
+  return a.linear_words ? a.linear_words : 2ull * d.block_count * a.block_words;
+}
+
+// Tiles of payload d: planes are tiled separately when tiles_per_plane_mode is set
+// (so a tile never crosses the K/V split), else [0, n) is tiled as one range.
+__device__ __forceinline__ unsigned int tiles_per_plane(const LaunchArgs& a,
+                                                        unsigned long long plane_words) {
+  return (unsigned int)((plane_words + kTileWords - 1) >> kTileShift);
+}
+
+__device__ __forceinline__ void tile_range(const LaunchArgs& a, const PayloadDesc& d,
+                                           unsigned int local_tile, unsigned long long n,
+                                           unsigned long long& start, unsigned long long& end) {
+  if (a.tiles_per_plane_mode) {
+    unsigned long long plane_words = n >> 1;
+    unsigned int tpp = tiles_per_plane(a, plane_words);
+    unsigned int plane = local_tile >= tpp ? 1u : 0u;
+    start = plane * plane_words + (unsigned long long)(local_tile - plane * tpp) * kTileWords;
+    unsigned long long stop = (plane + 1ull) * plane_words;
+    end = start + kTileWords < stop ? start + kTileWords : stop;
+  } else {
+    start = (unsigned long long)local_tile * kTileWords;
+    end = start + kTileWords < n ? start + kTileWords : n;
+  }
+}
+
+__device__ __forceinline__ unsigned int payload_tiles(const LaunchArgs& a, unsigned long long n) {
+  if (a.tiles_per_plane_mode) return 2u * tiles_per_plane(a, n >> 1);
+  return (unsigned int)((n + kTileWords - 1) >> kTileShift);
+}
+
+// Element offset of payload word i in the KV cache (any geometry).
+__device__ __forceinline__ unsigned long long word_offset(const LaunchArgs& a,
+                                                          const PayloadDesc& d,
+                                                          unsigned long long i) {
+  if (a.linear_words) return i;
+  unsigned long long plane_words = (unsigned long long)d.block_count * a.block_words;
+  unsigned long long plane = i / plane_words;
+  unsigned long long in_plane = i - plane * plane_words;
+  unsigned long long j = in_plane / a.block_words;
+  unsigned long long within = in_plane - j * a.block_words;
+  unsigned long long blk =
+      a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+  return plane * a.plane_stride + blk * a.block_stride + within;
+}
+
+// ---------------------------------------------------------------------------
+// byte-window helpers: c[] holds consecutive little-endian dwords; take 4 (or 2)
+// dwords starting at byte offset off (wave-uniform, 0 <= off < 16 or < 8).
+
+__device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t r) {
+  return (uint32_t)((((uint64_t)hi << 32) | lo) >> (8 * r));
+}
+
+template <int Q>
+__device__ __forceinline__ void window4_q(const uint32_t (&c)[8], uint32_t r, uint32_t (&o)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = funnel(c[Q + k], c[Q + k + 1], r);
+}
+
+__device__ __forceinline__ void window4(const uint32_t (&c)[8], uint32_t off, uint32_t (&o)[4]) {
+  uint32_t r = off & 3;
+  switch (off >> 2) {
+    case 0: window4_q<0>(c, r, o); break;
+    case 1: window4_q<1>(c, r, o); break;
+    case 2: window4_q<2>(c, r, o); break;
+    default: window4_q<3>(c, r, o); break;
+  }
+}
+
+__device__ __forceinline__ void window2(const uint32_t (&c)[4], uint32_t off, uint32_t (&o)[2]) {
+  uint32_t r = off & 3;
+  if (off >> 2) {
+    o[0] = funnel(c[1], c[2], r);
+    o[1] = funnel(c[2], c[3], r);
+  } else {
+    o[0] = funnel(c[0], c[1], r);
+    o[1] = funnel(c[1], c[2], r);
+  }
+}
+
+__device__ __forceinline__ uint32_t shfl_next(uint32_t v) {
+  // value of the next lane in the wave (lane 63 receives its own value)
+  return (uint32_t)__shfl_down((int)v, 1, kWave);
+}
+
+__device__ __forceinline__ uint32_t byte_of(const uint32_t* v, int k) {
+  return (v[k >> 2] >> (8 * (k & 3))) & 0xFF;
+}
+
+// Writes `count` bytes of v (starting at byte `first` of the dword array) to dst.
+__device__ __forceinline__ void store_bytes(unsigned char* dst, const uint32_t* v, int first,
+                                            int count) {
+  for (int k = 0; k < count; ++k) dst[k] = (unsigned char)byte_of(v, first + k);
+}
+
+// Wave-wide inclusive prefix sum.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    uint32_t t = (uint32_t)__shfl_up((int)v, d, kWave);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+}  // namespace unchainkv

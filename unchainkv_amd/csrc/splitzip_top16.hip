@@ -1,0 +1,942 @@
+// Top-16 palette codec for bf16 KV cache (payload mode 5), gfx950.
+//
+// Wire format of one payload of n bf16 words (n = 2 * blocks * block_words for a
+// paged layer; K plane first, then V), identical to the reference's
+// (native/unchain_kv/kvq_splitzip_cuda.cu:146-208):
+//   [0]                 5, or 255 when the escapes overflow the capacity
+//   [1..4]              u32 LE escape count, clamped to cap = ceil(n / 200)
+//   [5, 5+n)            body: (w & 0x7F) | ((w >> 8) & 0x80)  (mantissa + sign)
+//   [5+n, 5+n+n/2)      codes: 4-bit codebook index, even word in the low nibble
+//   [.., +5*cap)        escapes: {u32 LE position, u8 exponent}, code 0 in codes
+// The code of word i is tables[p * 256 + exponent(i)] with p = (i >= n / 2);
+// 255 there means "escape". Escapes are emitted in ascending position order and
+// unused slots are zeroed, which is one of the byte streams the reference
+// encoder can produce (its order is set by a global atomicAdd) and makes the
+// payload deterministic.
+//
+// Kernels (all launched on the caller's stream, no host synchronisation):
+//   top16_encode_kernel<fast, sequential>  gather through the block table +
+//       encode one 4096-word tile per workgroup; escapes are counted per tile and
+//       up to kStageSlots of them staged in the workspace.
+//   top16_encode_finalize                  per payload: scan tile counts, place
+//       escapes in ascending order, zero unused slots, write the header.
+//   top16_decode_kernel                    decode + scatter one tile per workgroup.
+//   top16_decode_generic                   any geometry, one word per thread.
+//   top16_patch_escapes                    apply escapes (any order) after decode.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "splitzip_common.h"
+
+namespace unchainkv {
+
+thread_local std::string g_last_error;
+
+long long fail(const char* what, hipError_t status) {
+  g_last_error = std::string(what) + ": " + hipGetErrorString(status);
+  return -1;
+}
+
+long long fail_msg(const std::string& msg) {
+  g_last_error = msg;
+  return -1;
+}
+
+namespace {
+
+constexpr int kFinGroups = 8;     // finalize workgroups per payload
+constexpr int kFinChunk = 4096;   // tiles scanned per finalize pass (LDS resident)
+constexpr int kPatchGroups = 8;   // escape-patch workgroups per payload
+
+__host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
+  return (n + 199) / 200;
+}
+
+__host__ __device__ inline unsigned long long encoded_size(unsigned long long n) {
+  return 5 + n + (n + 1) / 2 + 5 * escape_capacity(n);
+}
+
+// q = x / d for x, d < 2^32 via m = floor(2^64 / d) + 1 (exact for every 32-bit x).
+struct Divider {
+  unsigned long long m;
+  unsigned int d;
+};
+
+inline Divider make_divider(unsigned int d) {
+  Divider r;
+  r.d = d;
+  r.m = d <= 1 ? 0 : (~0ull / d) + 1;
+  return r;
+}
+
+__device__ __forceinline__ unsigned int div_u32(unsigned int x, unsigned long long m,
+                                                unsigned int d) {
+  return d <= 1 ? x : (unsigned int)__umul64hi((unsigned long long)x, m);
+}
+
+__device__ __forceinline__ void put_entry(unsigned char* entries, unsigned long long slot,
+                                          unsigned int pos, unsigned int exponent) {
+  unsigned char* e = entries + slot * 5;
+  e[0] = (unsigned char)pos;
+  e[1] = (unsigned char)(pos >> 8);
+  e[2] = (unsigned char)(pos >> 16);
+  e[3] = (unsigned char)(pos >> 24);
+  e[4] = (unsigned char)exponent;
+}
+
+__device__ __forceinline__ void write_header(unsigned char* payload, unsigned long long n,
+                                             unsigned long long escapes) {
+  unsigned long long cap = escape_capacity(n);
+  unsigned long long count = escapes > cap ? cap : escapes;
+  payload[0] = escapes > cap ? 255 : 5;
+  payload[1] = (unsigned char)count;
+  payload[2] = (unsigned char)(count >> 8);
+  payload[3] = (unsigned char)(count >> 16);
+  payload[4] = (unsigned char)(count >> 24);
+}
+
+// Workgroup-cooperative zeroing of [p, p + len).
+__device__ void zero_fill(unsigned char* p, unsigned long long len) {
+  const unsigned int tid = threadIdx.x;
+  unsigned long long head = (16 - ((uintptr_t)p & 15)) & 15;
+  if (head > len) head = len;
+  if (tid < head) p[tid] = 0;
+  unsigned char* q = p + head;
+  unsigned long long rest = len - head;
+  unsigned long long vecs = rest >> 4;
+  for (unsigned long long k = tid; k < vecs; k += kThreads)
+    reinterpret_cast<uint4*>(q)[k] = make_uint4(0, 0, 0, 0);
+  unsigned long long tail = rest & 15;
+  if (tid < tail) q[(vecs << 4) + tid] = 0;
+}
+
+// Exclusive scan of one value per thread across the workgroup; returns the
+// exclusive prefix and sets total. Uses s_wave[4]; contains barriers.
+__device__ __forceinline__ unsigned int block_exclusive_sum(unsigned int v, unsigned int* s_wave,
+                                                            unsigned int& total) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  unsigned int incl = wave_inclusive_sum(v);
+  if (lane == kWave - 1) s_wave[wave] = incl;
+  __syncthreads();
+  unsigned int before = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < kThreads / kWave; ++k) {
+    unsigned int t = s_wave[k];
+    if (k < wave) before += t;
+    total += t;
+  }
+  __syncthreads();
+  return before + incl - v;
+}
+
+// ---------------------------------------------------------------------------
+// misaligned stores/loads of per-lane byte runs
+
+// Each active lane owns 16 bytes for [dst, dst + 16); the active lanes of a wave
+// cover one contiguous range and share the misalignment s = dst & 15. Interior
+// 16-byte aligned chunks are written whole (own tail + next lane's head);
+// the wave's edges are written bytewise.
+__device__ __forceinline__ void store16_run(unsigned char* dst, const uint32_t (&v)[4],
+                                            bool active, bool first, bool last) {
+  const uint32_t s = (uint32_t)((uintptr_t)dst & 15);
+  if (s == 0) {
+    if (active) *reinterpret_cast<uint4*>(dst) = make_uint4(v[0], v[1], v[2], v[3]);
+    return;
+  }
+  uint32_t c[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    c[k] = v[k];
+    c[k + 4] = shfl_next(v[k]);
+  }
+  if (!active) return;
+  unsigned char* x = dst - s + 16;
+  if (first) store_bytes(dst, v, 0, 16 - s);
+  if (last) {
+    store_bytes(x, v, 16 - s, s);
+  } else {
+    uint32_t o[4];
+    window4(c, 16 - s, o);
+    *reinterpret_cast<uint4*>(x) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// Same for 8-byte runs.
+__device__ __forceinline__ void store8_run(unsigned char* dst, const uint32_t (&v)[2],
+                                           bool active, bool first, bool last) {
+  const uint32_t s = (uint32_t)((uintptr_t)dst & 7);
+  if (s == 0) {
+    if (active) *reinterpret_cast<uint2*>(dst) = make_uint2(v[0], v[1]);
+    return;
+  }
+  uint32_t c[4] = {v[0], v[1], shfl_next(v[0]), shfl_next(v[1])};
+  if (!active) return;
+  unsigned char* x = dst - s + 8;
+  if (first) store_bytes(dst, v, 0, 8 - s);
+  if (last) {
+    store_bytes(x, v, 8 - s, s);
+  } else {
+    uint32_t o[2];
+    window2(c, 8 - s, o);
+    *reinterpret_cast<uint2*>(x) = make_uint2(o[0], o[1]);
+  }
+}
+
+// Loads [src, src + 16) for each active lane (lanes contiguous, shared
+// misalignment). Only aligned chunks that hold wanted bytes are read.
+__device__ __forceinline__ void load16_run(const unsigned char* src, bool active, bool last,
+                                           uint32_t (&o)[4]) {
+  const uint32_t s = (uint32_t)((uintptr_t)src & 15);
+  if (s == 0) {
+    uint4 v = active ? *reinterpret_cast<const uint4*>(src) : make_uint4(0, 0, 0, 0);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    return;
+  }
+  const unsigned char* f = src - s;
+  uint4 own = active ? *reinterpret_cast<const uint4*>(f) : make_uint4(0, 0, 0, 0);
+  uint32_t c[8] = {own.x, own.y, own.z, own.w, 0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c[k + 4] = shfl_next(c[k]);
+  if (active && last) {
+    uint4 nx = *reinterpret_cast<const uint4*>(f + 16);
+    c[4] = nx.x; c[5] = nx.y; c[6] = nx.z; c[7] = nx.w;
+  }
+  window4(c, s, o);
+}
+
+__device__ __forceinline__ void load8_run(const unsigned char* src, bool active, bool last,
+                                          uint32_t (&o)[2]) {
+  const uint32_t s = (uint32_t)((uintptr_t)src & 7);
+  if (s == 0) {
+    uint2 v = active ? *reinterpret_cast<const uint2*>(src) : make_uint2(0, 0);
+    o[0] = v.x; o[1] = v.y;
+    return;
+  }
+  const unsigned char* f = src - s;
+  uint2 own = active ? *reinterpret_cast<const uint2*>(f) : make_uint2(0, 0);
+  uint32_t c[4] = {own.x, own.y, 0, 0};
+  c[2] = shfl_next(c[0]);
+  c[3] = shfl_next(c[1]);
+  if (active && last) {
+    uint2 nx = *reinterpret_cast<const uint2*>(f + 8);
+    c[2] = nx.x; c[3] = nx.y;
+  }
+  window2(c, s, o);
+}
+
+// ---------------------------------------------------------------------------
+// encode
+
+struct EncodeGeom {
+  unsigned long long bw_magic;  // divider for block_words
+  unsigned int bw;
+};
+
+// Fills s_tab[512] with code (0..15) or 0x10 for an escape, from the 544-byte table
+// (a code byte other than 255 keeps its low nibble, as the reference's
+// `(code & 0x0F)` does).
+__device__ __forceinline__ void load_code_table(const unsigned char* tables, unsigned char* s_tab) {
+  for (int k = threadIdx.x; k < 512; k += kThreads) {
+    unsigned int t = tables[k];
+    s_tab[k] = (unsigned char)(t == 255 ? 0x10 : (t & 0x0F));
+  }
+}
+
+// Encodes the 16 words of one lane (packed 2 per dword) with the code table of one
+// plane: 16 body bytes, 8 code bytes, and a 16-bit escape mask.
+__device__ __forceinline__ void encode_lane(const uint32_t (&x)[8], const unsigned char* tab,
+                                            uint32_t (&body)[4], uint32_t (&codes)[2],
+                                            uint32_t& emask) {
+  body[0] = body[1] = body[2] = body[3] = 0;
+  codes[0] = codes[1] = 0;
+  emask = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t v = x[k];
+    const uint32_t c0 = tab[(v >> 7) & 0xFF];
+    const uint32_t c1 = tab[(v >> 23) & 0xFF];
+    const uint32_t b0 = (v & 0x7F) | ((v >> 8) & 0x80);
+    const uint32_t b1 = ((v >> 16) & 0x7F) | ((v >> 24) & 0x80);
+    body[k >> 1] |= (b0 | (b1 << 8)) << (16 * (k & 1));
+    codes[k >> 2] |= ((c0 & 0x0F) | ((c1 & 0x0F) << 4)) << (8 * (k & 3));
+    emask |= ((c0 >> 4) | ((c1 >> 4) << 1)) << (2 * k);
+  }
+}
+
+template <bool kFast, bool kSequential>
+__global__ __launch_bounds__(kThreads) void top16_encode_kernel(LaunchArgs a, EncodeGeom g) {
+  __shared__ unsigned char s_tab[512];
+  __shared__ unsigned int s_wave[kThreads / kWave];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1);
+  load_code_table(a.tables, s_tab);
+  __syncthreads();
+
+  unsigned int first, stop;
+  if (kSequential) {
+    first = 0;
+    stop = a.total_tiles;
+  } else {
+    first = xcd_remap(blockIdx.x, gridDim.x);
+    stop = first + 1;
+  }
+  unsigned long long running = 0;  // sequential mode: escapes in earlier tiles
+
+  for (unsigned int tile = first; tile < stop; ++tile) {
+    const unsigned int r = find_payload(a, tile);
+    const PayloadDesc d = a.p[r];
+    const unsigned long long n = payload_words(a, d);
+    const unsigned long long half = n >> 1;
+    unsigned long long start, end;
+    tile_range(a, d, tile - d.tile_begin, n, start, end);
+    unsigned char* payload = a.buf + d.buf_offset;
+    const unsigned long long i0 = start + (unsigned long long)tid * kWordsPerLane;
+    const bool active = i0 < end;
+
+    uint32_t x[8];
+    uint32_t body[4], codes[2], emask;
+    if (kFast) {
+      // Tiles never cross the K/V split and every lane is wholly inside or
+      // outside the tile (plane_words % 16 == 0).
+      const unsigned int plane = start >= half ? 1u : 0u;
+      if (active) {
+        const unsigned int in_plane = (unsigned int)(i0 - plane * half);
+        const unsigned int j = div_u32(in_plane, g.bw_magic, g.bw);
+        const unsigned int within = in_plane - j * g.bw;
+        const unsigned long long blk =
+            a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+        const uint4* src = reinterpret_cast<const uint4*>(
+            a.kv + plane * a.plane_stride + blk * a.block_stride + within);
+        const uint4 v0 = src[0];
+        const uint4 v1 = src[1];
+        x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+        x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = 0;
+      }
+      encode_lane(x, s_tab + plane * 256, body, codes, emask);
+      if (!active) emask = 0;
+      const bool first_lane = active && lane == 0;
+      const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= end);
+      store16_run(payload + 5 + i0, body, active, first_lane, last_lane);
+      store8_run(payload + 5 + n + (i0 >> 1), codes, active, first_lane, last_lane);
+    } else {
+      // Generic geometry: per-word addressing and plane, byte stores.
+#pragma unroll
+      for (int k = 0; k < 8; ++k) x[k] = 0;
+      body[0] = body[1] = body[2] = body[3] = 0;
+      codes[0] = codes[1] = 0;
+      emask = 0;
+#pragma unroll 4
+      for (int k = 0; k < kWordsPerLane; ++k) {
+        const unsigned long long i = i0 + k;
+        if (i >= end) break;
+        const uint32_t w = a.kv[word_offset(a, d, i)];
+        const uint32_t c = s_tab[(i >= half ? 256u : 0u) + ((w >> 7) & 0xFF)];
+        payload[5 + i] = (unsigned char)((w & 0x7F) | ((w >> 8) & 0x80));
+        emask |= (c >> 4) << k;
+        x[k >> 1] = (k & 1) ? (x[k >> 1] | (w << 16)) : w;
+        codes[k >> 3] |= (c & 0x0F) << (4 * (k & 7));
+      }
+      // code bytes: a lane starts at an even index, so no byte is shared
+      for (int k = 0; k < kWordsPerLane; k += 2) {
+        const unsigned long long i = i0 + k;
+        if (i >= end) break;
+        payload[5 + n + (i >> 1)] = (unsigned char)((codes[k >> 3] >> (4 * (k & 7))) & 0xFF);
+      }
+    }
+
+    // ---- escapes: per-lane count, workgroup prefix (ascending positions) ----
+    const unsigned int cnt = __popc(emask);
+    unsigned int tile_total;
+    const unsigned int lane_base = block_exclusive_sum(cnt, s_wave, tile_total);
+    if (kSequential) {
+      if (emask) {
+        const unsigned long long cap = escape_capacity(n);
+        unsigned char* entries = payload + 5 + n + (n + 1) / 2;
+        unsigned long long slot = running + lane_base;
+#pragma unroll
+        for (int k = 0; k < kWordsPerLane; ++k) {
+          if (!((emask >> k) & 1)) continue;
+          if (slot < cap)
+            put_entry(entries, slot, (unsigned int)(i0 + k), (x[k >> 1] >> (7 + 16 * (k & 1))) & 0xFF);
+          ++slot;
+        }
+      }
+      running += tile_total;
+    } else {
+      unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
+      if (emask) {
+        unsigned int idx = lane_base;
+#pragma unroll
+        for (int k = 0; k < kWordsPerLane; ++k) {
+          if (!((emask >> k) & 1)) continue;
+          if (idx < kStageSlots)
+            staged[idx] = ((unsigned int)(i0 + k - start) << 8) |
+                          ((x[k >> 1] >> (7 + 16 * (k & 1))) & 0xFF);
+          ++idx;
+        }
+      }
+      if (tid == 0) a.workspace[tile] = tile_total;
+    }
+  }
+
+  if (kSequential) {
+    // one payload: zero unused slots, then the header
+    const PayloadDesc d = a.p[0];
+    const unsigned long long n = payload_words(a, d);
+    const unsigned long long cap = escape_capacity(n);
+    unsigned char* payload = a.buf + d.buf_offset;
+    unsigned char* entries = payload + 5 + n + (n + 1) / 2;
+    const unsigned long long used = running < cap ? running : cap;
+    zero_fill(entries + 5 * used, 5 * (cap - used));
+    if (tid == 0) write_header(payload, n, running);
+  }
+}
+
+// Scans the escapes of one tile from the source words (tiles with more escapes
+// than were staged) and places them from slot `base` on.
+__device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned int local_tile,
+                            unsigned long long n, unsigned long long base,
+                            const unsigned char* s_tab, unsigned int* s_wave,
+                            unsigned char* entries, unsigned long long cap) {
+  unsigned long long start, end;
+  tile_range(a, d, local_tile, n, start, end);
+  const unsigned long long half = n >> 1;
+  const unsigned long long i0 = start + (unsigned long long)threadIdx.x * kWordsPerLane;
+  uint32_t emask = 0;
+  uint32_t ex[kWordsPerLane];
+#pragma unroll
+  for (int k = 0; k < kWordsPerLane; ++k) {
+    const unsigned long long i = i0 + k;
+    ex[k] = 0;
+    if (i < end) {
+      const uint32_t w = a.kv[word_offset(a, d, i)];
+      const uint32_t e = (w >> 7) & 0xFF;
+      ex[k] = e;
+      emask |= (uint32_t)(s_tab[(i >= half ? 256u : 0u) + e] >> 4) << k;
+    }
+  }
+  unsigned int total;
+  const unsigned int lane_base = block_exclusive_sum(__popc(emask), s_wave, total);
+  unsigned long long slot = base + lane_base;
+#pragma unroll
+  for (int k = 0; k < kWordsPerLane; ++k) {
+    if (!((emask >> k) & 1)) continue;
+    if (slot < cap) put_entry(entries, slot, (unsigned int)(i0 + k), ex[k]);
+    ++slot;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
+  __shared__ unsigned int s_base[kFinChunk];
+  __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups + 1];
+  __shared__ unsigned int s_over_base[kFinChunk / kFinGroups + 1];
+  __shared__ unsigned int s_over_count;
+  __shared__ unsigned int s_wave[kThreads / kWave];
+  __shared__ unsigned char s_tab[512];
+  constexpr int kPerThread = kFinChunk / kThreads;  // 16 tiles per thread per pass
+
+  const unsigned int tid = threadIdx.x;
+  const unsigned int r = blockIdx.x / kFinGroups;
+  const unsigned int grp = blockIdx.x % kFinGroups;
+  const PayloadDesc d = a.p[r];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long cap = escape_capacity(n);
+  const unsigned int tiles = payload_tiles(a, n);
+  unsigned char* payload = a.buf + d.buf_offset;
+  unsigned char* entries = payload + 5 + n + (n + 1) / 2;
+  const unsigned int* counts = a.workspace + d.tile_begin;
+  const unsigned int* staged =
+      a.workspace + a.total_tiles + (unsigned long long)d.tile_begin * kStageSlots;
+  load_code_table(a.tables, s_tab);
+
+  unsigned long long running = 0;
+  for (unsigned int chunk0 = 0; chunk0 < tiles; chunk0 += kFinChunk) {
+    const unsigned int m = min((unsigned int)kFinChunk, tiles - chunk0);
+    // exclusive scan of this chunk's counts into s_base
+    unsigned int mine[kPerThread];
+    unsigned int sum = 0;
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+      const unsigned int t = tid * kPerThread + k;
+      mine[k] = t < m ? counts[chunk0 + t] : 0;
+      sum += mine[k];
+    }
+    unsigned int chunk_total;
+    unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+      s_base[tid * kPerThread + k] = prefix;
+      prefix += mine[k];
+    }
+    if (tid == 0) s_over_count = 0;
+    __syncthreads();
+
+    // staged escapes of this group's tiles go straight to their slots
+    for (unsigned int t = grp + tid * kFinGroups; t < m; t += kThreads * kFinGroups) {
+      const unsigned int c = counts[chunk0 + t];
+      if (c == 0) continue;
+      const unsigned long long base = running + s_base[t];
+      if (base >= cap) continue;
+      if (c > (unsigned int)kStageSlots) {
+        const unsigned int q = atomicAdd(&s_over_count, 1u);
+        s_over_tile[q] = chunk0 + t;
+        s_over_base[q] = (unsigned int)base;
+        continue;
+      }
+      unsigned long long start, end;
+      tile_range(a, d, chunk0 + t, n, start, end);
+      const unsigned int* st = staged + (unsigned long long)(chunk0 + t) * kStageSlots;
+      for (unsigned int q = 0; q < c && base + q < cap; ++q) {
+        const unsigned int v = st[q];
+        put_entry(entries, base + q, (unsigned int)(start + (v >> 8)), v & 0xFF);
+      }
+    }
+    __syncthreads();
+    const unsigned int over = s_over_count;
+    for (unsigned int q = 0; q < over; ++q)
+      rescan_tile(a, d, s_over_tile[q], n, s_over_base[q], s_tab, s_wave, entries, cap);
+    running += chunk_total;
+    __syncthreads();
+  }
+
+  // unused escape slots are zeroed, split across the payload's groups
+  const unsigned long long used = running < cap ? running : cap;
+  const unsigned long long pad = 5 * (cap - used);
+  const unsigned long long per = (pad + kFinGroups - 1) / kFinGroups;
+  const unsigned long long lo = per * grp < pad ? per * grp : pad;
+  const unsigned long long hi = lo + per < pad ? lo + per : pad;
+  zero_fill(entries + 5 * used + lo, hi - lo);
+  if (grp == 0 && tid == 0) write_header(payload, n, running);
+}
+
+// ---------------------------------------------------------------------------
+// decode
+
+__global__ __launch_bounds__(kThreads) void top16_decode_kernel(LaunchArgs a, EncodeGeom g) {
+  __shared__ unsigned char s_cb[32];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1);
+  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const unsigned int r = find_payload(a, tile);
+  const PayloadDesc d = a.p[r];
+  const unsigned char* payload = a.buf + d.buf_offset;
+  if (payload[0] != 5) return;  // the reference decoder leaves such payloads untouched
+  if (tid < 32) s_cb[tid] = a.tables[512 + tid];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long half = n >> 1;
+  unsigned long long start, end;
+  tile_range(a, d, tile - d.tile_begin, n, start, end);
+  const unsigned int plane = start >= half ? 1u : 0u;
+  const unsigned long long i0 = start + (unsigned long long)tid * kWordsPerLane;
+  const bool active = i0 < end;
+  const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= end);
+
+  uint32_t body[4], codes[2];
+  load16_run(payload + 5 + i0, active, last_lane, body);
+  load8_run(payload + 5 + n + (i0 >> 1), active, last_lane, codes);
+  __syncthreads();
+  if (!active) return;
+
+  const unsigned char* cb = s_cb + plane * 16;
+  uint32_t out[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t nb = (codes[k >> 2] >> (8 * (k & 3))) & 0xFF;
+    const uint32_t e0 = cb[nb & 0x0F];
+    const uint32_t e1 = cb[nb >> 4];
+    const uint32_t bb = (body[k >> 1] >> (16 * (k & 1))) & 0xFFFF;
+    const uint32_t w0 = (bb & 0x7F) | ((bb & 0x80) << 8) | (e0 << 7);
+    const uint32_t w1 = ((bb >> 8) & 0x7F) | ((bb & 0x8000)) | (e1 << 7);
+    out[k] = w0 | (w1 << 16);
+  }
+  const unsigned int in_plane = (unsigned int)(i0 - plane * half);
+  const unsigned int j = div_u32(in_plane, g.bw_magic, g.bw);
+  const unsigned int within = in_plane - j * g.bw;
+  const unsigned long long blk =
+      a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+  uint4* dst = reinterpret_cast<uint4*>(a.kv + plane * a.plane_stride + blk * a.block_stride +
+                                        within);
+  dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
+  dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
+}
+
+// Any geometry: one word per thread, grid-stride over every payload of the launch.
+__global__ __launch_bounds__(kThreads) void top16_decode_generic(LaunchArgs a) {
+  const unsigned int r = blockIdx.y;
+  const PayloadDesc d = a.p[r];
+  const unsigned char* payload = a.buf + d.buf_offset;
+  if (payload[0] != 5) return;
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long half = n >> 1;
+  const unsigned char* body = payload + 5;
+  const unsigned char* codes = body + n;
+  const unsigned char* cb = a.tables + 512;
+  for (unsigned long long i = (unsigned long long)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (unsigned long long)gridDim.x * kThreads) {
+    const uint32_t code = (codes[i >> 1] >> ((i & 1) * 4)) & 0x0F;
+    const uint32_t e = cb[(i >= half ? 16u : 0u) + code];
+    const uint32_t b = body[i];
+    a.kv[word_offset(a, d, i)] = (uint16_t)((b & 0x7F) | ((b & 0x80) << 8) | (e << 7));
+  }
+}
+
+// ApplyTop16Escapes semantics (kvq_splitzip_cuda.cu:253-284): for slot <
+// min(count, cap) with position < n, set the word's exponent bits.
+__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
+  const unsigned int r = blockIdx.x / kPatchGroups;
+  const unsigned int grp = blockIdx.x % kPatchGroups;
+  const PayloadDesc d = a.p[r];
+  const unsigned char* payload = a.buf + d.buf_offset;
+  if (payload[0] != 5) return;
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long cap = escape_capacity(n);
+  unsigned long long count = (unsigned long long)payload[1] | ((unsigned long long)payload[2] << 8) |
+                             ((unsigned long long)payload[3] << 16) |
+                             ((unsigned long long)payload[4] << 24);
+  if (count > cap) count = cap;
+  const unsigned char* entries = payload + 5 + n + (n + 1) / 2;
+  for (unsigned long long s = (unsigned long long)grp * kThreads + threadIdx.x; s < count;
+       s += (unsigned long long)kPatchGroups * kThreads) {
+    const unsigned char* e = entries + s * 5;
+    const unsigned long long pos = (unsigned long long)e[0] | ((unsigned long long)e[1] << 8) |
+                                   ((unsigned long long)e[2] << 16) |
+                                   ((unsigned long long)e[3] << 24);
+    if (pos >= n) continue;
+    uint16_t* w = a.kv + word_offset(a, d, pos);
+    *w = (uint16_t)((*w & 0x807F) | ((uint32_t)e[4] << 7));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+inline unsigned long long align_up(unsigned long long v, unsigned long long a) {
+  return (v + a - 1) / a * a;
+}
+
+inline unsigned int host_payload_tiles(unsigned long long n, bool per_plane) {
+  if (per_plane) return 2u * (unsigned int)(((n >> 1) + kTileWords - 1) >> kTileShift);
+  return (unsigned int)((n + kTileWords - 1) >> kTileShift);
+}
+
+long long check_launch(const char* what) {
+  hipError_t st = hipGetLastError();
+  if (st != hipSuccess) return fail(what, st);
+  return 0;
+}
+
+// Encodes payloads a.p[0 .. a.payload_count) (tile_begin already set).
+long long launch_encode(LaunchArgs& a, const EncodeGeom& g, bool fast, bool sequential,
+                        hipStream_t stream) {
+  if (sequential) {
+    if (fast)
+      hipLaunchKernelGGL((top16_encode_kernel<true, true>), dim3(1), dim3(kThreads), 0, stream,
+                         a, g);
+    else
+      hipLaunchKernelGGL((top16_encode_kernel<false, true>), dim3(1), dim3(kThreads), 0, stream,
+                         a, g);
+    return check_launch("top16_encode_kernel");
+  }
+  if (fast)
+    hipLaunchKernelGGL((top16_encode_kernel<true, false>), dim3(a.total_tiles), dim3(kThreads), 0,
+                       stream, a, g);
+  else
+    hipLaunchKernelGGL((top16_encode_kernel<false, false>), dim3(a.total_tiles), dim3(kThreads),
+                       0, stream, a, g);
+  if (long long rc = check_launch("top16_encode_kernel")) return rc;
+  hipLaunchKernelGGL(top16_encode_finalize, dim3(a.payload_count * kFinGroups), dim3(kThreads), 0,
+                     stream, a);
+  return check_launch("top16_encode_finalize");
+}
+
+long long launch_decode(LaunchArgs& a, const EncodeGeom& g, bool fast, hipStream_t stream) {
+  if (fast) {
+    hipLaunchKernelGGL(top16_decode_kernel, dim3(a.total_tiles), dim3(kThreads), 0, stream, a, g);
+  } else {
+    unsigned long long max_n = 0;
+    for (unsigned int r = 0; r < a.payload_count; ++r)
+      max_n = std::max(max_n, 2ull * a.p[r].block_count * a.block_words);
+    unsigned int blocks = (unsigned int)std::min<unsigned long long>((max_n + kThreads - 1) / kThreads,
+                                                                   2048);
+    hipLaunchKernelGGL(top16_decode_generic, dim3(std::max(blocks, 1u), a.payload_count),
+                       dim3(kThreads), 0, stream, a);
+  }
+  if (long long rc = check_launch("top16_decode_kernel")) return rc;
+  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * kPatchGroups), dim3(kThreads), 0,
+                     stream, a);
+  return check_launch("top16_patch_escapes");
+}
+
+unsigned long long workspace_words(unsigned long long tiles) {
+  return tiles * (1ull + kStageSlots);
+}
+
+}  // namespace
+}  // namespace unchainkv
+
+using namespace unchainkv;
+
+extern "C" const char* kvq_splitzip_last_error() { return g_last_error.c_str(); }
+
+extern "C" long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr,
+                                                    unsigned long long dst_ptr,
+                                                    unsigned long long count,
+                                                    unsigned long long capacity,
+                                                    unsigned long long tables_ptr,
+                                                    unsigned long long stream_ptr) {
+  // Preconditions and declines of kvq_splitzip_cuda.cu:385-395.
+  if (src_ptr == 0 || dst_ptr == 0 || tables_ptr == 0 || count == 0 || count > 0xFFFFFFFFULL)
+    return 0;
+  const unsigned long long encoded = encoded_size(count);
+  const unsigned long long scratch_offset = (encoded + 3) & ~3ULL;
+  if (encoded >= count * 2 || scratch_offset + 2 * sizeof(unsigned int) > capacity) return 0;
+
+  LaunchArgs a{};
+  a.kv = reinterpret_cast<uint16_t*>(src_ptr);
+  a.buf = reinterpret_cast<unsigned char*>(dst_ptr);
+  a.tables = reinterpret_cast<const unsigned char*>(tables_ptr);
+  a.linear_words = count;
+  a.payload_count = 1;
+  // fast path: halves are whole lanes and the source is 16-byte aligned
+  const bool fast = (count % 32 == 0) && (src_ptr % 16 == 0);
+  a.tiles_per_plane_mode = fast ? 1 : 0;
+  a.plane_stride = count / 2;
+  a.block_words = count / 2;
+  a.block_stride = 0;
+  a.block_start = 0;
+  a.p[0].block_count = 1;
+  const unsigned int tiles = host_payload_tiles(count, fast);
+  a.total_tiles = tiles;
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)std::max<unsigned long long>(count / 2, 1));
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  // Parallel tiles need a workspace for per-tile escape counts; it lives in the
+  // caller's buffer past the payload when the capacity allows, else one
+  // workgroup walks the tiles in order.
+  const unsigned long long ws_offset = align_up(dst_ptr + encoded, 16) - dst_ptr;
+  const unsigned long long ws_bytes = workspace_words(tiles) * 4;
+  bool sequential = tiles == 1 || ws_offset + ws_bytes > capacity;
+  if (!sequential) a.workspace = reinterpret_cast<unsigned int*>(dst_ptr + ws_offset);
+  long long rc = launch_encode(a, g, fast, sequential, reinterpret_cast<hipStream_t>(stream_ptr));
+  if (rc < 0) return rc;
+  return (long long)encoded;
+}
+
+extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long block_ids_ptr, unsigned long long tables_ptr,
+    unsigned long long stream_ptr) {
+  // Preconditions of kvq_splitzip_cuda.cu:423-432.
+  if (src_ptr == 0 || dst_ptr == 0 || tables_ptr == 0 || count_words == 0 || block_count == 0 ||
+      block_words == 0 || count_words != 2 * block_count * block_words)
+    return 0;
+  if (encoded_bytes != encoded_size(count_words)) return 0;
+  if (block_count > 0xFFFFFFFFULL || block_words > 0xFFFFFFFFULL)
+    return fail_msg("decode_top16: block_count and block_words must fit in 32 bits");
+
+  LaunchArgs a{};
+  a.kv = reinterpret_cast<uint16_t*>(dst_ptr);
+  a.ids = reinterpret_cast<const long long*>(block_ids_ptr);
+  a.buf = reinterpret_cast<unsigned char*>(src_ptr);
+  a.tables = reinterpret_cast<const unsigned char*>(tables_ptr);
+  a.plane_stride = plane_stride;
+  a.block_stride = block_stride;
+  a.block_words = block_words;
+  a.block_start = block_start;
+  a.payload_count = 1;
+  a.p[0].block_count = (unsigned int)block_count;
+  const bool fast = block_words % 16 == 0 && dst_ptr % 16 == 0 && plane_stride % 8 == 0 &&
+                    block_stride % 8 == 0 && (count_words >> 1) <= 0xFFFFFFFFULL;
+  a.tiles_per_plane_mode = 1;
+  a.total_tiles = host_payload_tiles(count_words, true);
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)block_words);
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  long long rc = launch_decode(a, g, fast, reinterpret_cast<hipStream_t>(stream_ptr));
+  if (rc < 0) return rc;
+  return (long long)(count_words * sizeof(uint16_t));
+}
+
+extern "C" long long kvq_splitzip_bf16_decode_top16(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long tables_ptr, unsigned long long stream_ptr) {
+  return kvq_splitzip_bf16_decode_top16_blocks(src_ptr, encoded_bytes, dst_ptr, count_words,
+                                               block_count, block_words, plane_stride,
+                                               block_stride, block_start, 0, tables_ptr,
+                                               stream_ptr);
+}
+
+// ---------------------------------------------------------------------------
+// batched paged entry points (no counterpart in the reference: it encodes one
+// gathered request per call)
+
+extern "C" unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count) {
+  if (block_offsets == nullptr) return 0;
+  unsigned long long tiles = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    tiles += host_payload_tiles(n, block_words % 16 == 0);
+  }
+  return workspace_words(tiles) * 4;
+}
+
+namespace {
+
+struct PagedGeometry {
+  unsigned long long kv_ptr, plane_stride, block_stride, block_words, ids_ptr;
+};
+
+bool paged_fast(const PagedGeometry& pg) {
+  return pg.block_words % 16 == 0 && pg.kv_ptr % 16 == 0 && pg.plane_stride % 8 == 0 &&
+         pg.block_stride % 8 == 0;
+}
+
+// Fills a.p for payloads [first, first + count) and returns the tile total.
+unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
+                        const unsigned long long* block_offsets,
+                        const unsigned long long* buf_offsets, unsigned long long first,
+                        unsigned int count, bool per_plane) {
+  unsigned int tiles = 0;
+  for (unsigned int k = 0; k < count; ++k) {
+    const unsigned long long r = first + k;
+    const unsigned long long nblk = block_offsets[r + 1] - block_offsets[r];
+    a.p[k].buf_offset = buf_offsets[r];
+    a.p[k].ids_offset = block_offsets[r];
+    a.p[k].block_count = (unsigned int)nblk;
+    a.p[k].tile_begin = tiles;
+    tiles += host_payload_tiles(2 * nblk * pg.block_words, per_plane);
+  }
+  a.payload_count = count;
+  a.total_tiles = tiles;
+  return tiles;
+}
+
+}  // namespace
+
+// Gathers and encodes payload r = blocks ids[block_offsets[r] .. block_offsets[r+1])
+// of one paged layer into out + out_offsets[r], for every r, in one launch per 64
+// payloads. Returns the total encoded bytes, 0 on a failed precondition (see
+// the header), or -1 with kvq_splitzip_last_error() set.
+extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long stream_ptr) {
+  if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || tables_ptr == 0 || workspace_ptr == 0 ||
+      block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 || block_words == 0 ||
+      block_words > 0xFFFFFFFFULL)
+    return 0;
+  unsigned long long total = 0;
+  std::vector<std::pair<unsigned long long, unsigned long long>> spans;
+  spans.reserve(payload_count);
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    const unsigned long long e = encoded_size(n);
+    if (n > 0xFFFFFFFFULL || e >= 2 * n || out_offsets[r] + e > out_capacity) return 0;
+    spans.emplace_back(out_offsets[r], out_offsets[r] + e);
+    total += e;
+  }
+  std::sort(spans.begin(), spans.end());
+  for (size_t k = 1; k < spans.size(); ++k)
+    if (spans[k].first < spans[k - 1].second) return 0;  // overlapping payloads
+  if (kvq_splitzip_top16_paged_workspace_bytes(block_words, block_offsets, payload_count) >
+      workspace_bytes)
+    return 0;
+
+  PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
+  const bool fast = paged_fast(pg);
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)block_words);
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  unsigned int* ws = reinterpret_cast<unsigned int*>(workspace_ptr);
+  for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
+    LaunchArgs a{};
+    a.kv = reinterpret_cast<uint16_t*>(kv_ptr);
+    a.ids = reinterpret_cast<const long long*>(block_ids_ptr);
+    a.buf = reinterpret_cast<unsigned char*>(out_ptr);
+    a.tables = reinterpret_cast<const unsigned char*>(tables_ptr);
+    a.plane_stride = plane_stride;
+    a.block_stride = block_stride;
+    a.block_words = block_words;
+    a.tiles_per_plane_mode = fast ? 1 : 0;
+    const unsigned int count =
+        (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
+    const unsigned int tiles = fill_descs(a, pg, block_offsets, out_offsets, first, count, fast);
+    a.workspace = ws;
+    long long rc = launch_encode(a, g, fast, false, stream);
+    if (rc < 0) return rc;
+    ws += workspace_words(tiles);
+  }
+  return (long long)total;
+}
+
+// Decodes payload r (src + src_offsets[r], encoded_bytes[r] long) and scatters it
+// into blocks ids[block_offsets[r] .. block_offsets[r+1]) of one paged layer.
+// Returns the total raw bytes written, 0 on a failed precondition, -1 on error.
+extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
+    unsigned long long src_ptr, const unsigned long long* src_offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long tables_ptr,
+    unsigned long long stream_ptr) {
+  if (src_ptr == 0 || kv_ptr == 0 || block_ids_ptr == 0 || tables_ptr == 0 ||
+      src_offsets == nullptr || encoded_bytes == nullptr || block_offsets == nullptr ||
+      payload_count == 0 || block_words == 0 || block_words > 0xFFFFFFFFULL)
+    return 0;
+  unsigned long long total = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    if (encoded_bytes[r] != encoded_size(n) || (n >> 1) > 0xFFFFFFFFULL) return 0;
+    total += 2 * n;
+  }
+  PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
+  const bool fast = paged_fast(pg);
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)block_words);
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
+    LaunchArgs a{};
+    a.kv = reinterpret_cast<uint16_t*>(kv_ptr);
+    a.ids = reinterpret_cast<const long long*>(block_ids_ptr);
+    a.buf = reinterpret_cast<unsigned char*>(src_ptr);
+    a.tables = reinterpret_cast<const unsigned char*>(tables_ptr);
+    a.plane_stride = plane_stride;
+    a.block_stride = block_stride;
+    a.block_words = block_words;
+    a.tiles_per_plane_mode = 1;
+    const unsigned int count =
+        (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
+    fill_descs(a, pg, block_offsets, src_offsets, first, count, true);
+    long long rc = launch_decode(a, g, fast, stream);
+    if (rc < 0) return rc;
+  }
+  return (long long)total;
+}

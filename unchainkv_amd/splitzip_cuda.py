@@ -1,0 +1,465 @@
+"""Drop-in host module for the splitzip bf16 KV codec on MI355X.
+
+Mirrors ``unchain_kv.splitzip_cuda`` (src/unchain_kv/splitzip_cuda.py): the same
+function names, argument meanings and return conventions, over the HIP library
+``libunchain_kv_splitzip_cuda.so`` built from ``unchainkv_amd/csrc``:
+
+* ``encode_top16`` / ``decode_top16`` / ``encode_bf16`` / ``decode_fixed6``
+  return the byte count, ``None`` when the codec declines (library missing,
+  wrong device/dtype/layout, precondition failed), and raise ``RuntimeError``
+  with ``kvq_splitzip_last_error()`` when a launch fails;
+* ``_top16_tables(layer, device, torch)`` builds (and caches per device and
+  layer) the 544-byte device table from ``_TOP16_CODEBOOKS``.
+
+Additions (keyword-only or new names, so reference callers are unaffected):
+
+* ``codebooks=`` on ``encode_top16`` / ``decode_top16``: a 32-byte per-layer
+  codebook (16 K exponents, then 16 V exponents) instead of the embedded one;
+* ``PagedBatch`` + ``encode_top16_paged`` / ``decode_top16_paged``: every
+  request of one paged layer in one launch, gathering straight from the block
+  table (no packed copy of the request's blocks first).
+
+Everything runs asynchronously on ``torch.cuda.current_stream(device)``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+from . import codec_format
+
+_LIB = None
+_LOAD_ERROR: str | None = None
+_TOP16_TABLE_CACHE: dict = {}
+_TOP16_CODEBOOKS: bytes = (
+    Path(__file__).resolve().parent / "data" / "llama_top16_codebooks.bin"
+).read_bytes()
+
+_U64 = ctypes.c_ulonglong
+_U64P = ctypes.POINTER(ctypes.c_ulonglong)
+
+# (symbol, argtypes, restype, required)
+_SIGNATURES = (
+    ("kvq_splitzip_bf16_encode", [_U64] * 5, ctypes.c_longlong, True),
+    ("kvq_splitzip_bf16_encode_mode", [_U64] * 5 + [ctypes.c_int], ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_decode_fixed6", [_U64] * 10, ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_decode_fixed6_blocks", [_U64] * 11, ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_encode_top16", [_U64] * 6, ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_decode_top16", [_U64] * 11, ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_decode_top16_blocks", [_U64] * 12, ctypes.c_longlong, False),
+    ("kvq_splitzip_last_error", [], ctypes.c_char_p, True),
+    ("kvq_splitzip_top16_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
+    (
+        "kvq_splitzip_bf16_encode_top16_paged",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_decode_top16_paged",
+        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+)
+
+
+def _candidate_paths() -> list[str]:
+    """``$UNCHAIN_KV_SPLITZIP_LIB``, else the in-tree build, else the loader path."""
+    env = os.environ.get("UNCHAIN_KV_SPLITZIP_LIB")
+    if env:
+        return [env]
+    here = Path(__file__).resolve().parent
+    return [str(here / "lib" / "libunchain_kv_splitzip_cuda.so"), "libunchain_kv_splitzip_cuda.so"]
+
+
+def _bind(lib) -> None:
+    for name, argtypes, restype, required in _SIGNATURES:
+        try:
+            fn = getattr(lib, name)
+        except AttributeError:
+            if required:
+                raise
+            continue
+        fn.argtypes = argtypes
+        fn.restype = restype
+
+
+def _load():
+    global _LIB, _LOAD_ERROR
+    if _LIB is not None:
+        return _LIB
+    errors = []
+    for path in _candidate_paths():
+        try:
+            lib = ctypes.CDLL(path)
+        except OSError as exc:
+            errors.append(str(exc))
+            continue
+        # a library without the two mandatory symbols raises AttributeError here,
+        # as the reference loader does (src/unchain_kv/splitzip_cuda.py:54-61, 149-150)
+        _bind(lib)
+        _LIB = lib
+        return lib
+    _LOAD_ERROR = "; ".join(errors[-2:])
+    return None
+
+
+def available() -> bool:
+    return _load() is not None
+
+
+def load_error() -> str | None:
+    _load()
+    return _LOAD_ERROR
+
+
+def _raise_last(lib, default: str):
+    message = lib.kvq_splitzip_last_error()
+    raise RuntimeError(message.decode() if message else default)
+
+
+def _is_cuda(tensor) -> bool:
+    return getattr(getattr(tensor, "device", None), "type", "") == "cuda"
+
+
+# ---------------------------------------------------------------------------
+# fixed6 / fixed5 (Top-16 fallback)
+
+def encode_bf16(source, out, bits: int = 6) -> int | None:
+    lib = _load()
+    if lib is None or not _is_cuda(source):
+        return None
+    if bits not in {5, 6}:
+        raise ValueError("splitzip bf16 bits must be 5 or 6")
+    import torch
+
+    stream = torch.cuda.current_stream(source.device).cuda_stream
+    encode_mode = getattr(lib, "kvq_splitzip_bf16_encode_mode", None)
+    if encode_mode is not None:
+        encoded = encode_mode(int(source.data_ptr()), int(out.data_ptr()), int(source.numel()),
+                              int(out.numel()), int(stream), int(bits))
+    elif bits == 6:
+        encoded = lib.kvq_splitzip_bf16_encode(int(source.data_ptr()), int(out.data_ptr()),
+                                               int(source.numel()), int(out.numel()), int(stream))
+    else:
+        return None
+    if encoded < 0:
+        _raise_last(lib, "splitzip cuda encode failed")
+    return int(encoded)
+
+
+def _decode_layout(source, out, block_ids, raw_bytes, torch):
+    """Validation and geometry of a decode (src/unchain_kv/splitzip_cuda.py:200-230):
+    unique in-range block ids, uint8 source and bf16 (2, blocks, ...) target on the
+    same CUDA device, both contiguous, raw_bytes an even multiple of 2 * blocks."""
+    if not block_ids or raw_bytes <= 0 or raw_bytes % 2:
+        return None
+    if not _is_cuda(source) or source.device != getattr(out, "device", None):
+        return None
+    if source.dtype != torch.uint8 or out.dtype != torch.bfloat16:
+        return None
+    if not source.is_contiguous() or not out.is_contiguous():
+        return None
+    if out.dim() < 3 or out.shape[0] != 2:
+        return None
+    if len(set(block_ids)) != len(block_ids):
+        return None
+    if any(block < 0 or block >= out.shape[1] for block in block_ids):
+        return None
+    start = block_ids[0]
+    contiguous = list(block_ids) == list(range(start, start + len(block_ids)))
+    count_words = raw_bytes // 2
+    if count_words % (2 * len(block_ids)):
+        return None
+    block_words = count_words // (2 * len(block_ids))
+    current = torch.cuda.current_stream(out.device)
+    ids = None
+    if not contiguous:
+        ids = torch.tensor(block_ids, dtype=torch.int64, device=out.device)
+    return count_words, block_words, start, current, ids
+
+
+def decode_fixed6(source, out, block_ids: list[int], raw_bytes: int) -> int | None:
+    lib = _load()
+    decode = getattr(lib, "kvq_splitzip_bf16_decode_fixed6", None) if lib else None
+    if decode is None:
+        return None
+    import torch
+
+    layout = _decode_layout(source, out, block_ids, raw_bytes, torch)
+    if layout is None:
+        return None
+    count_words, block_words, start, current, ids = layout
+    decode_blocks = getattr(lib, "kvq_splitzip_bf16_decode_fixed6_blocks", None)
+    if ids is not None and decode_blocks is None:
+        return None
+    common = (int(source.data_ptr()), int(source.numel()), int(out.data_ptr()), count_words,
+              len(block_ids), block_words, int(out.stride(0)), int(out.stride(1)), start)
+    if decode_blocks is not None:
+        copied = decode_blocks(*common, int(ids.data_ptr()) if ids is not None else 0,
+                               int(current.cuda_stream))
+    else:
+        copied = decode(*common, int(current.cuda_stream))
+    if ids is not None:
+        ids.record_stream(current)
+    if copied < 0:
+        _raise_last(lib, "splitzip cuda decode failed")
+    return int(copied) or None
+
+
+# ---------------------------------------------------------------------------
+# Top-16
+
+def _tables_tensor(codebooks: bytes, device, torch):
+    return torch.tensor(list(codec_format.top16_tables(codebooks)), dtype=torch.uint8,
+                        device=device)
+
+
+def _top16_tables(layer_index: int, device, torch):
+    """544-byte device table for an embedded layer codebook, cached per
+    (device, layer); ``None`` outside the embedded layers
+    (src/unchain_kv/splitzip_cuda.py:283-298)."""
+    if not 0 <= layer_index < len(_TOP16_CODEBOOKS) // 32:
+        return None
+    key = (str(device), layer_index)
+    cached = _TOP16_TABLE_CACHE.get(key)
+    if cached is None:
+        cached = _tables_tensor(_TOP16_CODEBOOKS[layer_index * 32:(layer_index + 1) * 32], device,
+                                torch)
+        _TOP16_TABLE_CACHE[key] = cached
+    return cached
+
+
+def top16_tables_for(codebooks: bytes, device, torch):
+    """Device table for an explicit 32-byte codebook, cached per (device, bytes)."""
+    codebooks = bytes(codebooks)
+    if len(codebooks) != 32:
+        raise ValueError("a Top-16 layer codebook is 32 bytes (16 K then 16 V exponents)")
+    key = (str(device), codebooks)
+    cached = _TOP16_TABLE_CACHE.get(key)
+    if cached is None:
+        cached = _tables_tensor(codebooks, device, torch)
+        _TOP16_TABLE_CACHE[key] = cached
+    return cached
+
+
+def _resolve_tables(layer_index, codebooks, device, torch):
+    if codebooks is not None:
+        return top16_tables_for(codebooks, device, torch)
+    return _top16_tables(layer_index, device, torch)
+
+
+def encode_top16(source, out, layer_index: int, *, codebooks: bytes | None = None) -> int | None:
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_top16", None) if lib else None
+    if encode is None:
+        return None
+    if not _is_cuda(source) or source.device != getattr(out, "device", None):
+        return None
+    import torch
+
+    if source.dtype != torch.bfloat16 or out.dtype != torch.uint8:
+        return None
+    if not source.is_contiguous() or not out.is_contiguous():
+        return None
+    tables = _resolve_tables(layer_index, codebooks, source.device, torch)
+    if tables is None:
+        return None
+    stream = torch.cuda.current_stream(source.device).cuda_stream
+    encoded = encode(int(source.data_ptr()), int(out.data_ptr()), int(source.numel()),
+                     int(out.numel()), int(tables.data_ptr()), int(stream))
+    if encoded < 0:
+        _raise_last(lib, "splitzip top16 encode failed")
+    return int(encoded) or None
+
+
+def decode_top16(source, out, block_ids: list[int], raw_bytes: int, layer_index: int, *,
+                 codebooks: bytes | None = None) -> int | None:
+    lib = _load()
+    decode = getattr(lib, "kvq_splitzip_bf16_decode_top16", None) if lib else None
+    if decode is None:
+        return None
+    import torch
+
+    layout = _decode_layout(source, out, block_ids, raw_bytes, torch)
+    if layout is None:
+        return None
+    tables = _resolve_tables(layer_index, codebooks, source.device, torch)
+    if tables is None:
+        return None
+    count_words, block_words, start, current, ids = layout
+    decode_blocks = getattr(lib, "kvq_splitzip_bf16_decode_top16_blocks", None)
+    if ids is not None and decode_blocks is None:
+        return None
+    common = (int(source.data_ptr()), int(source.numel()), int(out.data_ptr()), count_words,
+              len(block_ids), block_words, int(out.stride(0)), int(out.stride(1)), start)
+    if decode_blocks is not None:
+        copied = decode_blocks(*common, int(ids.data_ptr()) if ids is not None else 0,
+                               int(tables.data_ptr()), int(current.cuda_stream))
+    else:
+        copied = decode(*common, int(tables.data_ptr()), int(current.cuda_stream))
+    if ids is not None:
+        ids.record_stream(current)
+    if copied < 0:
+        _raise_last(lib, "splitzip top16 decode failed")
+    return int(copied) or None
+
+
+# ---------------------------------------------------------------------------
+# batched paged Top-16 (one launch per layer for every request)
+
+class PagedBatch:
+    """Block tables of several requests over one paged KV layout.
+
+    ``block_tables[r]`` lists request r's block ids in order; payload r holds the
+    K words then the V words of those blocks (the order of
+    ``kv_layer[:, block_tables[r]]``). A batch is built once and reused for every
+    layer: vLLM gives a request the same block ids in every layer.
+
+    Payload r is placed at ``out_offsets[r]`` of the batch's payload buffer, chosen
+    so that its body section starts on a 256-byte boundary (the codes section then
+    starts 16-byte aligned too when the block words are a multiple of 16).
+    """
+
+    def __init__(self, block_tables, block_words: int, device, torch=None):
+        if torch is None:
+            import torch
+        if not block_tables or any(len(t) == 0 for t in block_tables):
+            raise ValueError("every request needs at least one block")
+        if block_words <= 0:
+            raise ValueError("block_words must be positive")
+        self.block_tables = [list(map(int, t)) for t in block_tables]
+        self.block_words = int(block_words)
+        self.device = device
+        flat = [b for t in self.block_tables for b in t]
+        if min(flat) < 0:
+            raise ValueError("block ids must be non-negative")
+        self.ids = torch.tensor(flat, dtype=torch.int64, device=device)
+        counts = [len(t) for t in self.block_tables]
+        offsets = [0]
+        for c in counts:
+            offsets.append(offsets[-1] + c)
+        self.payload_count = len(counts)
+        self.count_words = [2 * c * self.block_words for c in counts]
+        self.raw_bytes = [2 * n for n in self.count_words]
+        self.encoded_bytes = [codec_format.top16_encoded_size(n) for n in self.count_words]
+        out_offsets = []
+        end = 0
+        for size in self.encoded_bytes:
+            start = -(-(end + 5) // 256) * 256 - 5
+            out_offsets.append(start)
+            end = start + size
+        self.out_offsets = out_offsets
+        self.out_bytes = end
+        self._block_offsets = (ctypes.c_ulonglong * len(offsets))(*offsets)
+        self._out_offsets = (ctypes.c_ulonglong * len(out_offsets))(*out_offsets)
+        self._encoded = (ctypes.c_ulonglong * len(self.encoded_bytes))(*self.encoded_bytes)
+        self.max_block = max(flat)
+        self.unique_blocks = len(set(flat)) == len(flat)
+
+    @property
+    def total_raw_bytes(self) -> int:
+        return sum(self.raw_bytes)
+
+    @property
+    def total_encoded_bytes(self) -> int:
+        return sum(self.encoded_bytes)
+
+    def workspace_bytes(self) -> int:
+        lib = _load()
+        query = getattr(lib, "kvq_splitzip_top16_paged_workspace_bytes", None) if lib else None
+        if query is None:
+            raise RuntimeError(f"splitzip HIP library unavailable: {load_error()}")
+        return int(query(self.block_words, self._block_offsets, self.payload_count))
+
+    def new_payload_buffer(self, torch=None):
+        if torch is None:
+            import torch
+        return torch.empty(self.out_bytes, dtype=torch.uint8, device=self.device)
+
+    def new_workspace(self, torch=None):
+        if torch is None:
+            import torch
+        return torch.empty(max(self.workspace_bytes(), 16), dtype=torch.uint8,
+                           device=self.device)
+
+    def payload(self, out, r: int):
+        return out[self.out_offsets[r]:self.out_offsets[r] + self.encoded_bytes[r]]
+
+
+def _paged_layout_ok(kv_layer, batch: PagedBatch, torch) -> bool:
+    if not _is_cuda(kv_layer) or kv_layer.dtype != torch.bfloat16:
+        return False
+    if kv_layer.dim() < 3 or kv_layer.shape[0] != 2 or not kv_layer.is_contiguous():
+        return False
+    block_words = kv_layer[0, 0].numel()
+    return block_words == batch.block_words and batch.max_block < kv_layer.shape[1]
+
+
+def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index: int = -1, *,
+                       codebooks: bytes | None = None, tables=None) -> int | None:
+    """Gather + Top-16 encode every request of ``batch`` from one paged layer
+    ``(2, num_blocks, ...)`` into ``out`` (a ``batch.out_bytes`` uint8 buffer).
+    Returns the total encoded bytes or ``None`` when the codec declines."""
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_top16_paged", None) if lib else None
+    if encode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    if tables is None:
+        tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
+    if tables is None:
+        return None
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                     batch.payload_count, int(out.data_ptr()), batch._out_offsets,
+                     int(out.numel()), int(tables.data_ptr()), int(workspace.data_ptr()),
+                     int(workspace.numel()), int(stream))
+    if encoded < 0:
+        _raise_last(lib, "splitzip top16 paged encode failed")
+    return int(encoded) or None
+
+
+def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: PagedBatch,
+                       layer_index: int = -1, *, codebooks: bytes | None = None,
+                       tables=None) -> int | None:
+    """Decode payload r (``source[src_offsets[r]:][:encoded_bytes[r]]``) and scatter
+    it into ``batch.block_tables[r]`` of the paged layer ``kv_layer``; one launch
+    for every request. Returns the total raw bytes written or ``None``."""
+    lib = _load()
+    decode = getattr(lib, "kvq_splitzip_bf16_decode_top16_paged", None) if lib else None
+    if decode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch) or not batch.unique_blocks:
+        return None
+    if source.dtype != torch.uint8 or not source.is_contiguous() or source.device != kv_layer.device:
+        return None
+    if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
+        return None
+    if any(o + e > source.numel() for o, e in zip(src_offsets, encoded_bytes)):
+        return None
+    if tables is None:
+        tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
+    if tables is None:
+        return None
+    offs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, src_offsets))
+    encs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, encoded_bytes))
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
+                    int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                    batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                    int(tables.data_ptr()), int(stream))
+    if copied < 0:
+        _raise_last(lib, "splitzip top16 paged decode failed")
+    return int(copied) or None
