@@ -15,14 +15,18 @@ long long fail_msg(const std::string& msg);
 
 constexpr int kThreads = 256;                         // 4 waves of 64
 constexpr int kWave = 64;
-constexpr int kWordsPerLane = 16;                     // 32 B of bf16 per lane
+// Lane-run kernels: each lane owns 16 consecutive words (any alignment).
+constexpr int kWordsPerLane = 16;
 constexpr int kTileWords = kThreads * kWordsPerLane;  // 4096 words per workgroup tile
 constexpr int kTileShift = 12;
 static_assert((1 << kTileShift) == kTileWords, "tile size");
+// Chunk kernels (aligned sections): a lane handles 8-word chunks so that one
+// vector memory instruction of a wave covers 64 consecutive chunks.
+constexpr int kChunkWords = 8;
 
 // Escapes staged per tile by the encode kernel; tiles with more are re-scanned
 // by the finalize kernel.
-constexpr int kStageSlots = 64;
+constexpr int kStageSlots = 32;
 // Payload descriptors passed by value in the kernel arguments.
 constexpr int kMaxPayloads = 64;
 
@@ -54,7 +58,7 @@ struct LaunchArgs {
   unsigned int payload_count;
   unsigned int total_tiles;
   unsigned int tiles_per_plane_mode;  // 1: tiles never cross a plane (fast path); 0: one range [0, n)
-  unsigned int pad;
+  unsigned int tile_shift;            // log2 of the tile size in words
   PayloadDesc p[kMaxPayloads];
 };
 
@@ -84,7 +88,7 @@ __device__ __forceinline__ unsigned long long payload_words(const LaunchArgs& a,
 // (so a tile never crosses the K/V split), else [0, n) is tiled as one range.
 __device__ __forceinline__ unsigned int tiles_per_plane(const LaunchArgs& a,
                                                         unsigned long long plane_words) {
-  return (unsigned int)((plane_words + kTileWords - 1) >> kTileShift);
+  return (unsigned int)((plane_words + (1ull << a.tile_shift) - 1) >> a.tile_shift);
 }
 
 __device__ __forceinline__ void tile_range(const LaunchArgs& a, const PayloadDesc& d,
@@ -94,18 +98,20 @@ __device__ __forceinline__ void tile_range(const LaunchArgs& a, const PayloadDes
     unsigned long long plane_words = n >> 1;
     unsigned int tpp = tiles_per_plane(a, plane_words);
     unsigned int plane = local_tile >= tpp ? 1u : 0u;
-    start = plane * plane_words + (unsigned long long)(local_tile - plane * tpp) * kTileWords;
+    const unsigned long long tile = 1ull << a.tile_shift;
+    start = plane * plane_words + ((unsigned long long)(local_tile - plane * tpp) << a.tile_shift);
     unsigned long long stop = (plane + 1ull) * plane_words;
-    end = start + kTileWords < stop ? start + kTileWords : stop;
+    end = start + tile < stop ? start + tile : stop;
   } else {
-    start = (unsigned long long)local_tile * kTileWords;
-    end = start + kTileWords < n ? start + kTileWords : n;
+    const unsigned long long tile = 1ull << a.tile_shift;
+    start = (unsigned long long)local_tile << a.tile_shift;
+    end = start + tile < n ? start + tile : n;
   }
 }
 
 __device__ __forceinline__ unsigned int payload_tiles(const LaunchArgs& a, unsigned long long n) {
   if (a.tiles_per_plane_mode) return 2u * tiles_per_plane(a, n >> 1);
-  return (unsigned int)((n + kTileWords - 1) >> kTileShift);
+  return (unsigned int)((n + (1ull << a.tile_shift) - 1) >> a.tile_shift);
 }
 
 // Element offset of payload word i in the KV cache (any geometry).

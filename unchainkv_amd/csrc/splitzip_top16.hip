@@ -15,14 +15,18 @@
 // payload deterministic.
 //
 // Kernels (all launched on the caller's stream, no host synchronisation):
-//   top16_encode_kernel<fast, sequential>  gather through the block table +
-//       encode one 4096-word tile per workgroup; escapes are counted per tile and
-//       up to kStageSlots of them staged in the workspace.
-//   top16_encode_finalize                  per payload: scan tile counts, place
-//       escapes in ascending order, zero unused slots, write the header.
-//   top16_decode_kernel                    decode + scatter one tile per workgroup.
-//   top16_decode_generic                   any geometry, one word per thread.
-//   top16_patch_escapes                    apply escapes (any order) after decode.
+//   top16_encode_tile        the batched layout (aligned sections, block words a
+//       multiple of 1024): gather through the block table + encode one 4096-word
+//       tile per workgroup, one block per wave so addressing is scalar; escapes
+//       are counted per tile and up to kStageSlots of them staged in the workspace.
+//   top16_encode_lanes<fast, sequential>  any section alignment or geometry:
+//       16 consecutive words per lane (misaligned stores realigned through
+//       neighbour-lane shuffles); or one workgroup walking every tile in order.
+//   top16_encode_finalize    per payload: scan tile counts, place escapes in
+//       ascending order, zero unused slots, write the header.
+//   top16_decode_tile / top16_decode_lanes / top16_decode_generic
+//       decode + scatter for aligned sections, any alignment, any geometry.
+//   top16_patch_escapes      apply escapes (any order) after decode.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -49,7 +53,7 @@ long long fail_msg(const std::string& msg) {
 namespace {
 
 constexpr int kFinGroups = 8;     // finalize workgroups per payload
-constexpr int kFinChunk = 4096;   // tiles scanned per finalize pass (LDS resident)
+constexpr int kFinChunk = 8192;   // tiles scanned per finalize pass (LDS resident)
 constexpr int kPatchGroups = 8;   // escape-patch workgroups per payload
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
@@ -127,6 +131,33 @@ __device__ __forceinline__ unsigned int block_exclusive_sum(unsigned int v, unsi
 #pragma unroll
   for (int k = 0; k < kThreads / kWave; ++k) {
     unsigned int t = s_wave[k];
+    if (k < wave) before += t;
+    total += t;
+  }
+  __syncthreads();
+  return before + incl - v;
+}
+
+
+// Same for a 64-bit value holding up to four 16-bit counters (no carries: every
+// counter stays below 2^16). Uses s_wave64[4]; contains barriers.
+__device__ __forceinline__ unsigned long long block_exclusive_sum64(unsigned long long v,
+                                                                    unsigned long long* s_wave64,
+                                                                    unsigned long long& total) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  unsigned long long incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    unsigned long long t = __shfl_up(incl, d, kWave);
+    if (lane >= d) incl += t;
+  }
+  if (lane == kWave - 1) s_wave64[wave] = incl;
+  __syncthreads();
+  unsigned long long before = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < kThreads / kWave; ++k) {
+    unsigned long long t = s_wave64[k];
     if (k < wave) before += t;
     total += t;
   }
@@ -237,6 +268,38 @@ struct EncodeGeom {
   unsigned int bw;
 };
 
+// Geometry of one tile of a launch (wave-uniform values).
+struct TileInfo {
+  unsigned long long n, half, start, end, ids_offset;
+  unsigned char* payload;
+  unsigned int plane;
+};
+
+__device__ __forceinline__ TileInfo tile_info(const LaunchArgs& a, unsigned int tile) {
+  TileInfo t;
+  const unsigned int r = find_payload(a, tile);
+  const PayloadDesc d = a.p[r];
+  t.n = payload_words(a, d);
+  t.half = t.n >> 1;
+  tile_range(a, d, tile - d.tile_begin, t.n, t.start, t.end);
+  t.plane = t.start >= t.half ? 1u : 0u;
+  t.payload = a.buf + d.buf_offset;
+  t.ids_offset = d.ids_offset;
+  return t;
+}
+
+// Element offset in the paged layer of payload word i (i inside plane t.plane).
+__device__ __forceinline__ unsigned long long chunk_offset(const LaunchArgs& a, const TileInfo& t,
+                                                           const EncodeGeom& geo,
+                                                           unsigned long long i) {
+  const unsigned int in_plane = (unsigned int)(i - t.plane * t.half);
+  const unsigned int j = div_u32(in_plane, geo.bw_magic, geo.bw);
+  const unsigned int within = in_plane - j * geo.bw;
+  const unsigned long long blk =
+      a.ids ? (unsigned long long)a.ids[t.ids_offset + j] : a.block_start + j;
+  return t.plane * a.plane_stride + blk * a.block_stride + within;
+}
+
 // Fills s_tab[512] with code (0..15) or 0x10 for an escape, from the 544-byte table
 // (a code byte other than 255 keeps its low nibble, as the reference's
 // `(code & 0x0F)` does).
@@ -269,7 +332,7 @@ __device__ __forceinline__ void encode_lane(const uint32_t (&x)[8], const unsign
 }
 
 template <bool kFast, bool kSequential>
-__global__ __launch_bounds__(kThreads) void top16_encode_kernel(LaunchArgs a, EncodeGeom g) {
+__global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, EncodeGeom g) {
   __shared__ unsigned char s_tab[512];
   __shared__ unsigned int s_wave[kThreads / kWave];
   const unsigned int tid = threadIdx.x;
@@ -400,6 +463,194 @@ __global__ __launch_bounds__(kThreads) void top16_encode_kernel(LaunchArgs a, En
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Tile kernels: the batched layout (aligned sections) with one block per wave.
+//
+// A workgroup encodes/decodes one 4096-word tile of one plane; wave w covers words
+// [start + 1024w, start + 1024w + 1024), which lie in one KV block (block words a
+// multiple of 1024), so block lookup and every base address are wave-uniform
+// scalars and lane l handles words 16l .. 16l + 15 of its wave's range. The
+// per-word work is a handful of VALU operations (byte permutes, bit-field inserts)
+// plus one LDS lookup for the encoder.
+
+// Scalar (SGPR) copies of wave-uniform values.
+__device__ __forceinline__ unsigned int uniform(unsigned int v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
+  return ((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned int)(v >> 32)) << 32) |
+         __builtin_amdgcn_readfirstlane((unsigned int)v);
+}
+
+// Wave-uniform element offset of payload word i (in plane t.plane) in the layer.
+__device__ __forceinline__ unsigned long long wave_block_offset(const LaunchArgs& a,
+                                                                const TileInfo& t,
+                                                                const EncodeGeom& geo,
+                                                                unsigned long long i) {
+  const unsigned int in_plane = uniform((unsigned int)(i - t.plane * t.half));
+  const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
+  const unsigned int within = in_plane - j * geo.bw;
+  const unsigned long long blk =
+      a.ids ? (unsigned long long)a.ids[t.ids_offset + j] : a.block_start + j;
+  return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
+}
+
+__global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
+  __shared__ unsigned char s_tab[256];  // this tile's plane: code, or 0x10 for an escape
+  __shared__ unsigned int s_wave[kThreads / kWave];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1);
+  const unsigned int wave = uniform(tid >> 6);
+  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const TileInfo t = tile_info(a, tile);
+  if (tid < 64) {
+    const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.tables + t.plane * 256 + 4 * tid);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t c = (raw >> (8 * e)) & 0xFF;
+      packed |= (c == 255 ? 0x10u : (c & 0x0Fu)) << (8 * e);
+    }
+    reinterpret_cast<uint32_t*>(s_tab)[tid] = packed;
+  }
+  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
+  const bool active = wstart < t.end;  // whole waves (plane words are a multiple of 1024)
+  uint32_t x[8];
+  if (active) {
+    const uint16_t* src = a.kv + wave_block_offset(a, t, geo, wstart);
+    const uint4 v0 = reinterpret_cast<const uint4*>(src)[2 * lane];
+    const uint4 v1 = reinterpret_cast<const uint4*>(src)[2 * lane + 1];
+    x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+    x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) x[k] = 0;
+  }
+  __syncthreads();  // s_tab ready
+
+  uint32_t body[4], codes[2], flags = 0, D[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // body bytes of 4 words: mantissa bits 0-6 and the sign bit into bit 7
+    // (bytes 1 and 3 of t0/t1 are don't-care: the permute keeps bytes 0 and 2)
+    const uint32_t t0 = (x[2 * q] & 0x007F007Fu) | ((x[2 * q] >> 8) & ~0x007F007Fu);
+    const uint32_t t1 = (x[2 * q + 1] & 0x007F007Fu) | ((x[2 * q + 1] >> 8) & ~0x007F007Fu);
+    body[q] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
+    // codes of 4 words, one per byte (0x10 marks an escape)
+    const uint32_t c0 = s_tab[(x[2 * q] >> 7) & 0xFF];
+    const uint32_t c1 = s_tab[(x[2 * q] >> 23) & 0xFF];
+    const uint32_t c2 = s_tab[(x[2 * q + 1] >> 7) & 0xFF];
+    const uint32_t c3 = s_tab[(x[2 * q + 1] >> 23) & 0xFF];
+    D[q] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+    flags |= D[q];
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t ta = D[2 * h] & 0x0F0F0F0Fu, tb = D[2 * h + 1] & 0x0F0F0F0Fu;
+    codes[h] = __builtin_amdgcn_perm(tb | (tb >> 4), ta | (ta >> 4), 0x06040200u);
+  }
+  if (active) {
+    unsigned char* pbody = t.payload + 5 + wstart;
+    unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+    reinterpret_cast<uint4*>(pbody)[lane] = make_uint4(body[0], body[1], body[2], body[3]);
+    reinterpret_cast<uint2*>(pcode)[lane] = make_uint2(codes[0], codes[1]);
+  }
+
+  // escapes (rare): per-lane mask, workgroup prefix in ascending word order
+  uint32_t emask = 0;
+  if (active && (flags & 0x10101010u)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t m = D[q] & 0x10101010u;
+      emask |= (((m >> 4) & 1) | ((m >> 11) & 2) | ((m >> 18) & 4) | ((m >> 25) & 8)) << (4 * q);
+    }
+  }
+  const unsigned int cnt = __popc(emask);
+  const unsigned int incl = __ballot(cnt != 0) ? wave_inclusive_sum(cnt) : 0u;
+  if (lane == kWave - 1) s_wave[wave] = incl;
+  __syncthreads();
+  unsigned int before = 0, tile_total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / kWave; ++w) {
+    const unsigned int v = s_wave[w];
+    if (w < (int)wave) before += v;
+    tile_total += v;
+  }
+  if (tid == 0) a.workspace[tile] = tile_total;
+  if (emask) {
+    unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
+    unsigned int idx = before + incl - cnt;
+    const unsigned int local0 = (unsigned int)(wstart - t.start) + lane * kWordsPerLane;
+#pragma unroll
+    for (int k = 0; k < kWordsPerLane; ++k) {
+      if (!((emask >> k) & 1)) continue;
+      if (idx < kStageSlots)
+        staged[idx] = ((local0 + k) << 8) | ((x[k >> 1] >> (7 + 16 * (k & 1))) & 0xFF);
+      ++idx;
+    }
+  }
+}
+
+// Per-byte 0xFF/0x00 masks from bit 3 of each byte of s (byte permute with the
+// sign-replicating selectors 8-11).
+__device__ __forceinline__ uint32_t bit3_mask(uint32_t s) {
+  return __builtin_amdgcn_perm(s << 12, s << 4, 0x090B080Au);
+}
+
+// Exponents of four 4-bit codes (one per byte of s) from a 16-byte codebook held
+// in four dwords: two byte permutes (codes 0-7 and 8-15) merged by bit 3.
+__device__ __forceinline__ uint32_t codebook_lookup4(uint32_t s, const uint32_t (&cb)[4]) {
+  const uint32_t s7 = s & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(cb[1], cb[0], s7);
+  const uint32_t hi = __builtin_amdgcn_perm(cb[3], cb[2], s7);
+  const uint32_t mask = bit3_mask(s);
+  return (hi & mask) | (lo & ~mask);
+}
+
+// Two decoded words from bytes [b0, e0, b1, e1] (body byte, exponent): mantissa
+// from b, exponent into bits 7-14, b's bit 7 into the sign bit 15.
+__device__ __forceinline__ uint32_t assemble_pair(uint32_t x) {
+  const uint32_t y = (x & 0x007F007Fu) | ((x >> 1) & ~0x007F007Fu);
+  return ((x << 8) & 0x80008000u) | (y & ~0x80008000u);
+}
+
+__global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
+  const unsigned int lane = threadIdx.x & (kWave - 1);
+  const unsigned int wave = uniform(threadIdx.x >> 6);
+  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const TileInfo t = tile_info(a, tile);
+  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
+  if (wstart >= t.end) return;  // no barrier in this kernel
+  const unsigned int mode = t.payload[0];
+  const uint32_t* cbw = reinterpret_cast<const uint32_t*>(a.tables + 512 + t.plane * 16);
+  const uint32_t cb[4] = {cbw[0], cbw[1], cbw[2], cbw[3]};
+  const uint4 b4 = reinterpret_cast<const uint4*>(t.payload + 5 + wstart)[lane];
+  const uint2 c2 = reinterpret_cast<const uint2*>(t.payload + 5 + t.n + (wstart >> 1))[lane];
+  uint16_t* dst = a.kv + wave_block_offset(a, t, geo, wstart);
+  // the reference decoder leaves a payload whose byte 0 is not 5 untouched
+  if (mode != 5) return;
+  const uint32_t body[4] = {b4.x, b4.y, b4.z, b4.w};
+  const uint32_t cd[2] = {c2.x, c2.y};
+  uint32_t out[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t u = cd[h] >> 4;
+    // codes of words 8h .. 8h + 7 as bytes (low nibble first)
+    const uint32_t sa = __builtin_amdgcn_perm(u, cd[h], 0x05010400u) & 0x0F0F0F0Fu;
+    const uint32_t sb = __builtin_amdgcn_perm(u, cd[h], 0x07030602u) & 0x0F0F0F0Fu;
+    const uint32_t ea = codebook_lookup4(sa, cb);
+    const uint32_t eb = codebook_lookup4(sb, cb);
+    out[4 * h + 0] = assemble_pair(__builtin_amdgcn_perm(ea, body[2 * h], 0x05010400u));
+    out[4 * h + 1] = assemble_pair(__builtin_amdgcn_perm(ea, body[2 * h], 0x07030602u));
+    out[4 * h + 2] = assemble_pair(__builtin_amdgcn_perm(eb, body[2 * h + 1], 0x05010400u));
+    out[4 * h + 3] = assemble_pair(__builtin_amdgcn_perm(eb, body[2 * h + 1], 0x07030602u));
+  }
+  uint4* d4 = reinterpret_cast<uint4*>(dst) + 2 * lane;
+  d4[0] = make_uint4(out[0], out[1], out[2], out[3]);
+  d4[1] = make_uint4(out[4], out[5], out[6], out[7]);
+}
+
 // Scans the escapes of one tile from the source words (tiles with more escapes
 // than were staged) and places them from slot `base` on.
 __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned int local_tile,
@@ -409,33 +660,37 @@ __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned 
   unsigned long long start, end;
   tile_range(a, d, local_tile, n, start, end);
   const unsigned long long half = n >> 1;
-  const unsigned long long i0 = start + (unsigned long long)threadIdx.x * kWordsPerLane;
-  uint32_t emask = 0;
-  uint32_t ex[kWordsPerLane];
+  for (unsigned long long sub = start; sub < end; sub += kTileWords) {
+    const unsigned long long i0 = sub + (unsigned long long)threadIdx.x * kWordsPerLane;
+    uint32_t emask = 0;
+    uint32_t ex[kWordsPerLane];
 #pragma unroll
-  for (int k = 0; k < kWordsPerLane; ++k) {
-    const unsigned long long i = i0 + k;
-    ex[k] = 0;
-    if (i < end) {
-      const uint32_t w = a.kv[word_offset(a, d, i)];
-      const uint32_t e = (w >> 7) & 0xFF;
-      ex[k] = e;
-      emask |= (uint32_t)(s_tab[(i >= half ? 256u : 0u) + e] >> 4) << k;
+    for (int k = 0; k < kWordsPerLane; ++k) {
+      const unsigned long long i = i0 + k;
+      ex[k] = 0;
+      if (i < end) {
+        const uint32_t w = a.kv[word_offset(a, d, i)];
+        const uint32_t e = (w >> 7) & 0xFF;
+        ex[k] = e;
+        emask |= (uint32_t)(s_tab[(i >= half ? 256u : 0u) + e] >> 4) << k;
+      }
     }
-  }
-  unsigned int total;
-  const unsigned int lane_base = block_exclusive_sum(__popc(emask), s_wave, total);
-  unsigned long long slot = base + lane_base;
+    unsigned int total;
+    const unsigned int lane_base = block_exclusive_sum(__popc(emask), s_wave, total);
+    unsigned long long slot = base + lane_base;
 #pragma unroll
-  for (int k = 0; k < kWordsPerLane; ++k) {
-    if (!((emask >> k) & 1)) continue;
-    if (slot < cap) put_entry(entries, slot, (unsigned int)(i0 + k), ex[k]);
-    ++slot;
+    for (int k = 0; k < kWordsPerLane; ++k) {
+      if (!((emask >> k) & 1)) continue;
+      if (slot < cap) put_entry(entries, slot, (unsigned int)(i0 + k), ex[k]);
+      ++slot;
+    }
+    base += total;
   }
 }
 
 __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
   __shared__ unsigned int s_base[kFinChunk];
+  __shared__ unsigned int s_cnt[kFinChunk];
   __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups + 1];
   __shared__ unsigned int s_over_base[kFinChunk / kFinGroups + 1];
   __shared__ unsigned int s_over_count;
@@ -474,6 +729,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
 #pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
       s_base[tid * kPerThread + k] = prefix;
+      s_cnt[tid * kPerThread + k] = mine[k];
       prefix += mine[k];
     }
     if (tid == 0) s_over_count = 0;
@@ -481,7 +737,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
 
     // staged escapes of this group's tiles go straight to their slots
     for (unsigned int t = grp + tid * kFinGroups; t < m; t += kThreads * kFinGroups) {
-      const unsigned int c = counts[chunk0 + t];
+      const unsigned int c = s_cnt[t];
       if (c == 0) continue;
       const unsigned long long base = running + s_base[t];
       if (base >= cap) continue;
@@ -520,32 +776,26 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
 // ---------------------------------------------------------------------------
 // decode
 
-__global__ __launch_bounds__(kThreads) void top16_decode_kernel(LaunchArgs a, EncodeGeom g) {
+// Decode + scatter for any section alignment (block words a multiple of 16,
+// destination 16-byte aligned): 16 consecutive words per lane, misaligned
+// sections read as aligned chunks and realigned with the neighbour lane's data.
+__global__ __launch_bounds__(kThreads) void top16_decode_lanes(LaunchArgs a, EncodeGeom geo) {
   __shared__ unsigned char s_cb[32];
   const unsigned int tid = threadIdx.x;
   const unsigned int lane = tid & (kWave - 1);
-  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const unsigned int r = find_payload(a, tile);
-  const PayloadDesc d = a.p[r];
-  const unsigned char* payload = a.buf + d.buf_offset;
-  if (payload[0] != 5) return;  // the reference decoder leaves such payloads untouched
   if (tid < 32) s_cb[tid] = a.tables[512 + tid];
-  const unsigned long long n = payload_words(a, d);
-  const unsigned long long half = n >> 1;
-  unsigned long long start, end;
-  tile_range(a, d, tile - d.tile_begin, n, start, end);
-  const unsigned int plane = start >= half ? 1u : 0u;
-  const unsigned long long i0 = start + (unsigned long long)tid * kWordsPerLane;
-  const bool active = i0 < end;
-  const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= end);
-
+  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const TileInfo t = tile_info(a, tile);
+  const unsigned int mode = t.payload[0];
+  const unsigned long long i0 = t.start + (unsigned long long)tid * kWordsPerLane;
+  const bool active = i0 < t.end;
+  const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= t.end);
   uint32_t body[4], codes[2];
-  load16_run(payload + 5 + i0, active, last_lane, body);
-  load8_run(payload + 5 + n + (i0 >> 1), active, last_lane, codes);
-  __syncthreads();
-  if (!active) return;
-
-  const unsigned char* cb = s_cb + plane * 16;
+  load16_run(t.payload + 5 + i0, active, last_lane, body);
+  load8_run(t.payload + 5 + t.n + (i0 >> 1), active, last_lane, codes);
+  __syncthreads();  // s_cb ready
+  if (!active || mode != 5) return;
+  const unsigned char* cb = s_cb + t.plane * 16;
   uint32_t out[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
@@ -554,16 +804,10 @@ __global__ __launch_bounds__(kThreads) void top16_decode_kernel(LaunchArgs a, En
     const uint32_t e1 = cb[nb >> 4];
     const uint32_t bb = (body[k >> 1] >> (16 * (k & 1))) & 0xFFFF;
     const uint32_t w0 = (bb & 0x7F) | ((bb & 0x80) << 8) | (e0 << 7);
-    const uint32_t w1 = ((bb >> 8) & 0x7F) | ((bb & 0x8000)) | (e1 << 7);
+    const uint32_t w1 = ((bb >> 8) & 0x7F) | (bb & 0x8000) | (e1 << 7);
     out[k] = w0 | (w1 << 16);
   }
-  const unsigned int in_plane = (unsigned int)(i0 - plane * half);
-  const unsigned int j = div_u32(in_plane, g.bw_magic, g.bw);
-  const unsigned int within = in_plane - j * g.bw;
-  const unsigned long long blk =
-      a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
-  uint4* dst = reinterpret_cast<uint4*>(a.kv + plane * a.plane_stride + blk * a.block_stride +
-                                        within);
+  uint4* dst = reinterpret_cast<uint4*>(a.kv + chunk_offset(a, t, geo, i0));
   dst[0] = make_uint4(out[0], out[1], out[2], out[3]);
   dst[1] = make_uint4(out[4], out[5], out[6], out[7]);
 }
@@ -622,9 +866,49 @@ inline unsigned long long align_up(unsigned long long v, unsigned long long a) {
   return (v + a - 1) / a * a;
 }
 
-inline unsigned int host_payload_tiles(unsigned long long n, bool per_plane) {
-  if (per_plane) return 2u * (unsigned int)(((n >> 1) + kTileWords - 1) >> kTileShift);
-  return (unsigned int)((n + kTileWords - 1) >> kTileShift);
+constexpr unsigned int kMinTileShift = kTileShift;
+
+enum class Kernel { kTile, kLanes, kGeneric };
+
+struct Plan {
+  Kernel kernel;
+  bool sequential;
+  unsigned int tile_shift;
+  bool per_plane;
+};
+
+inline unsigned int host_payload_tiles(unsigned long long n, bool per_plane,
+                                       unsigned int shift) {
+  const unsigned long long tile = 1ull << shift;
+  if (per_plane) return 2u * (unsigned int)(((n >> 1) + tile - 1) >> shift);
+  return (unsigned int)((n + tile - 1) >> shift);
+}
+
+// A payload at `base` has its body 16-byte and its code section 8-byte aligned
+// (what the tile kernels load and store).
+inline bool sections_aligned(unsigned long long base, unsigned long long n) {
+  return (base + 5) % 16 == 0 && (base + 5 + n) % 8 == 0;
+}
+
+// tile_ok: every wave's 1024 words lie in one block (block words a multiple of
+// 1024), sections aligned for 16-byte body and 8-byte code stores, table dword
+// aligned.
+Plan make_plan(bool geometry_fast, bool tile_ok, bool sequential) {
+  Plan p;
+  p.sequential = sequential;
+  p.tile_shift = kTileShift;
+  if (geometry_fast && tile_ok && !sequential) {
+    p.kernel = Kernel::kTile;
+  } else {
+    p.kernel = geometry_fast ? Kernel::kLanes : Kernel::kGeneric;
+  }
+  p.per_plane = geometry_fast;
+  return p;
+}
+
+void apply_plan(LaunchArgs& a, const Plan& p) {
+  a.tiles_per_plane_mode = p.per_plane ? 1 : 0;
+  a.tile_shift = p.tile_shift;
 }
 
 long long check_launch(const char* what) {
@@ -633,50 +917,71 @@ long long check_launch(const char* what) {
   return 0;
 }
 
-// Encodes payloads a.p[0 .. a.payload_count) (tile_begin already set).
-long long launch_encode(LaunchArgs& a, const EncodeGeom& g, bool fast, bool sequential,
-                        hipStream_t stream) {
-  if (sequential) {
-    if (fast)
-      hipLaunchKernelGGL((top16_encode_kernel<true, true>), dim3(1), dim3(kThreads), 0, stream,
-                         a, g);
+// Encodes payloads a.p[0 .. a.payload_count) (descriptors and tiling set).
+long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream) {
+  const dim3 block(kThreads);
+  if (p.sequential) {
+    if (p.kernel == Kernel::kGeneric)
+      hipLaunchKernelGGL((top16_encode_lanes<false, true>), dim3(1), block, 0, stream, a, g);
     else
-      hipLaunchKernelGGL((top16_encode_kernel<false, true>), dim3(1), dim3(kThreads), 0, stream,
-                         a, g);
-    return check_launch("top16_encode_kernel");
+      hipLaunchKernelGGL((top16_encode_lanes<true, true>), dim3(1), block, 0, stream, a, g);
+    return check_launch("top16_encode_lanes");
   }
-  if (fast)
-    hipLaunchKernelGGL((top16_encode_kernel<true, false>), dim3(a.total_tiles), dim3(kThreads), 0,
-                       stream, a, g);
-  else
-    hipLaunchKernelGGL((top16_encode_kernel<false, false>), dim3(a.total_tiles), dim3(kThreads),
-                       0, stream, a, g);
-  if (long long rc = check_launch("top16_encode_kernel")) return rc;
-  hipLaunchKernelGGL(top16_encode_finalize, dim3(a.payload_count * kFinGroups), dim3(kThreads), 0,
-                     stream, a);
+  switch (p.kernel) {
+    case Kernel::kTile:
+      hipLaunchKernelGGL(top16_encode_tile, dim3(a.total_tiles), block, 0, stream, a, g);
+      break;
+    case Kernel::kLanes:
+      hipLaunchKernelGGL((top16_encode_lanes<true, false>), dim3(a.total_tiles), block, 0, stream,
+                         a, g);
+      break;
+    case Kernel::kGeneric:
+      hipLaunchKernelGGL((top16_encode_lanes<false, false>), dim3(a.total_tiles), block, 0,
+                         stream, a, g);
+      break;
+  }
+  if (long long rc = check_launch("top16_encode")) return rc;
+  hipLaunchKernelGGL(top16_encode_finalize, dim3(a.payload_count * kFinGroups), block, 0, stream,
+                     a);
   return check_launch("top16_encode_finalize");
 }
 
-long long launch_decode(LaunchArgs& a, const EncodeGeom& g, bool fast, hipStream_t stream) {
-  if (fast) {
-    hipLaunchKernelGGL(top16_decode_kernel, dim3(a.total_tiles), dim3(kThreads), 0, stream, a, g);
-  } else {
-    unsigned long long max_n = 0;
-    for (unsigned int r = 0; r < a.payload_count; ++r)
-      max_n = std::max(max_n, 2ull * a.p[r].block_count * a.block_words);
-    unsigned int blocks = (unsigned int)std::min<unsigned long long>((max_n + kThreads - 1) / kThreads,
-                                                                   2048);
-    hipLaunchKernelGGL(top16_decode_generic, dim3(std::max(blocks, 1u), a.payload_count),
-                       dim3(kThreads), 0, stream, a);
+long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream) {
+  const dim3 block(kThreads);
+  switch (p.kernel) {
+    case Kernel::kTile:
+      hipLaunchKernelGGL(top16_decode_tile, dim3(a.total_tiles), block, 0, stream, a, g);
+      break;
+    case Kernel::kLanes:
+      hipLaunchKernelGGL(top16_decode_lanes, dim3(a.total_tiles), block, 0, stream, a, g);
+      break;
+    case Kernel::kGeneric: {
+      unsigned long long max_n = 0;
+      for (unsigned int r = 0; r < a.payload_count; ++r)
+        max_n = std::max(max_n, 2ull * a.p[r].block_count * a.block_words);
+      const unsigned int blocks = (unsigned int)std::min<unsigned long long>(
+          (max_n + kThreads - 1) / kThreads, 2048);
+      hipLaunchKernelGGL(top16_decode_generic, dim3(std::max(blocks, 1u), a.payload_count), block,
+                         0, stream, a);
+      break;
+    }
   }
-  if (long long rc = check_launch("top16_decode_kernel")) return rc;
-  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * kPatchGroups), dim3(kThreads), 0,
-                     stream, a);
+  if (long long rc = check_launch("top16_decode")) return rc;
+  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * kPatchGroups), block, 0, stream,
+                     a);
   return check_launch("top16_patch_escapes");
 }
 
 unsigned long long workspace_words(unsigned long long tiles) {
   return tiles * (1ull + kStageSlots);
+}
+
+EncodeGeom make_geom(unsigned long long block_words) {
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)std::max<unsigned long long>(block_words, 1));
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  return g;
 }
 
 }  // namespace
@@ -705,28 +1010,33 @@ extern "C" long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr,
   a.tables = reinterpret_cast<const unsigned char*>(tables_ptr);
   a.linear_words = count;
   a.payload_count = 1;
-  // fast path: halves are whole lanes and the source is 16-byte aligned
-  const bool fast = (count % 32 == 0) && (src_ptr % 16 == 0);
-  a.tiles_per_plane_mode = fast ? 1 : 0;
+  // 16-byte loads need halves made of whole 16-word lanes and an aligned source;
+  // the contiguous source is addressed as one block per plane
+  const bool geometry_fast = (count % 32 == 0) && (src_ptr % 16 == 0);
   a.plane_stride = count / 2;
   a.block_words = count / 2;
   a.block_stride = 0;
   a.block_start = 0;
   a.p[0].block_count = 1;
-  const unsigned int tiles = host_payload_tiles(count, fast);
-  a.total_tiles = tiles;
-  EncodeGeom g{};
-  const Divider dv = make_divider((unsigned int)std::max<unsigned long long>(count / 2, 1));
-  g.bw = dv.d;
-  g.bw_magic = dv.m;
+  const EncodeGeom g = make_geom(count / 2);
+  const bool aligned = sections_aligned(dst_ptr, count) && tables_ptr % 4 == 0 &&
+                       (count / 2) % 1024 == 0;
   // Parallel tiles need a workspace for per-tile escape counts; it lives in the
   // caller's buffer past the payload when the capacity allows, else one
   // workgroup walks the tiles in order.
+  Plan plan = make_plan(geometry_fast, aligned, false);
+  unsigned int tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
   const unsigned long long ws_offset = align_up(dst_ptr + encoded, 16) - dst_ptr;
   const unsigned long long ws_bytes = workspace_words(tiles) * 4;
-  bool sequential = tiles == 1 || ws_offset + ws_bytes > capacity;
-  if (!sequential) a.workspace = reinterpret_cast<unsigned int*>(dst_ptr + ws_offset);
-  long long rc = launch_encode(a, g, fast, sequential, reinterpret_cast<hipStream_t>(stream_ptr));
+  if (tiles == 1 || ws_offset + ws_bytes > capacity) {
+    plan = make_plan(geometry_fast, aligned, true);
+    tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
+  } else {
+    a.workspace = reinterpret_cast<unsigned int*>(dst_ptr + ws_offset);
+  }
+  apply_plan(a, plan);
+  a.total_tiles = tiles;
+  long long rc = launch_encode(a, g, plan, reinterpret_cast<hipStream_t>(stream_ptr));
   if (rc < 0) return rc;
   return (long long)encoded;
 }
@@ -757,15 +1067,17 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
   a.block_start = block_start;
   a.payload_count = 1;
   a.p[0].block_count = (unsigned int)block_count;
-  const bool fast = block_words % 16 == 0 && dst_ptr % 16 == 0 && plane_stride % 8 == 0 &&
-                    block_stride % 8 == 0 && (count_words >> 1) <= 0xFFFFFFFFULL;
-  a.tiles_per_plane_mode = 1;
-  a.total_tiles = host_payload_tiles(count_words, true);
-  EncodeGeom g{};
-  const Divider dv = make_divider((unsigned int)block_words);
-  g.bw = dv.d;
-  g.bw_magic = dv.m;
-  long long rc = launch_decode(a, g, fast, reinterpret_cast<hipStream_t>(stream_ptr));
+  const bool geometry_fast = block_words % 16 == 0 && dst_ptr % 16 == 0 && plane_stride % 8 == 0 &&
+                             block_stride % 8 == 0 && (count_words >> 1) <= 0xFFFFFFFFULL;
+  const Plan plan = make_plan(geometry_fast,
+                              sections_aligned(src_ptr, count_words) && tables_ptr % 4 == 0 &&
+                                  block_words % 1024 == 0,
+                              false);
+  apply_plan(a, plan);
+  a.tiles_per_plane_mode = 1;  // decode always tiles per plane (the generic path ignores tiles)
+  a.total_tiles = host_payload_tiles(count_words, true, plan.tile_shift);
+  long long rc = launch_decode(a, make_geom(block_words), plan,
+                               reinterpret_cast<hipStream_t>(stream_ptr));
   if (rc < 0) return rc;
   return (long long)(count_words * sizeof(uint16_t));
 }
@@ -793,7 +1105,8 @@ extern "C" unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
   unsigned long long tiles = 0;
   for (unsigned long long r = 0; r < payload_count; ++r) {
     const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
-    tiles += host_payload_tiles(n, block_words % 16 == 0);
+    // the smallest tile of any plan bounds the tile count
+    tiles += host_payload_tiles(n, true, kMinTileShift);
   }
   return workspace_words(tiles) * 4;
 }
@@ -809,11 +1122,21 @@ bool paged_fast(const PagedGeometry& pg) {
          pg.block_stride % 8 == 0;
 }
 
+bool paged_aligned(unsigned long long buf, const unsigned long long* block_offsets,
+                   const unsigned long long* buf_offsets, unsigned long long count,
+                   unsigned long long block_words) {
+  for (unsigned long long r = 0; r < count; ++r) {
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    if (!sections_aligned(buf + buf_offsets[r], n)) return false;
+  }
+  return true;
+}
+
 // Fills a.p for payloads [first, first + count) and returns the tile total.
 unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
                         const unsigned long long* block_offsets,
                         const unsigned long long* buf_offsets, unsigned long long first,
-                        unsigned int count, bool per_plane) {
+                        unsigned int count, const Plan& plan) {
   unsigned int tiles = 0;
   for (unsigned int k = 0; k < count; ++k) {
     const unsigned long long r = first + k;
@@ -822,7 +1145,7 @@ unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
     a.p[k].ids_offset = block_offsets[r];
     a.p[k].block_count = (unsigned int)nblk;
     a.p[k].tile_begin = tiles;
-    tiles += host_payload_tiles(2 * nblk * pg.block_words, per_plane);
+    tiles += host_payload_tiles(2 * nblk * pg.block_words, plan.per_plane, plan.tile_shift);
   }
   a.payload_count = count;
   a.total_tiles = tiles;
@@ -864,13 +1187,15 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
   if (kvq_splitzip_top16_paged_workspace_bytes(block_words, block_offsets, payload_count) >
       workspace_bytes)
     return 0;
+  if (workspace_ptr % 4 != 0) return 0;
 
-  PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
-  const bool fast = paged_fast(pg);
-  EncodeGeom g{};
-  const Divider dv = make_divider((unsigned int)block_words);
-  g.bw = dv.d;
-  g.bw_magic = dv.m;
+  const PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
+  const Plan plan = make_plan(
+      paged_fast(pg),
+      paged_aligned(out_ptr, block_offsets, out_offsets, payload_count, block_words) &&
+          tables_ptr % 4 == 0 && block_words % 1024 == 0,
+      false);
+  const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned int* ws = reinterpret_cast<unsigned int*>(workspace_ptr);
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
@@ -882,12 +1207,12 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
     a.plane_stride = plane_stride;
     a.block_stride = block_stride;
     a.block_words = block_words;
-    a.tiles_per_plane_mode = fast ? 1 : 0;
+    apply_plan(a, plan);
     const unsigned int count =
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
-    const unsigned int tiles = fill_descs(a, pg, block_offsets, out_offsets, first, count, fast);
+    const unsigned int tiles = fill_descs(a, pg, block_offsets, out_offsets, first, count, plan);
     a.workspace = ws;
-    long long rc = launch_encode(a, g, fast, false, stream);
+    long long rc = launch_encode(a, g, plan, stream);
     if (rc < 0) return rc;
     ws += workspace_words(tiles);
   }
@@ -915,12 +1240,14 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
     if (encoded_bytes[r] != encoded_size(n) || (n >> 1) > 0xFFFFFFFFULL) return 0;
     total += 2 * n;
   }
-  PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
-  const bool fast = paged_fast(pg);
-  EncodeGeom g{};
-  const Divider dv = make_divider((unsigned int)block_words);
-  g.bw = dv.d;
-  g.bw_magic = dv.m;
+  const PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
+  Plan plan = make_plan(
+      paged_fast(pg),
+      paged_aligned(src_ptr, block_offsets, src_offsets, payload_count, block_words) &&
+          tables_ptr % 4 == 0 && block_words % 1024 == 0,
+      false);
+  plan.per_plane = true;
+  const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
     LaunchArgs a{};
@@ -931,11 +1258,11 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
     a.plane_stride = plane_stride;
     a.block_stride = block_stride;
     a.block_words = block_words;
-    a.tiles_per_plane_mode = 1;
+    apply_plan(a, plan);
     const unsigned int count =
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
-    fill_descs(a, pg, block_offsets, src_offsets, first, count, true);
-    long long rc = launch_decode(a, g, fast, stream);
+    fill_descs(a, pg, block_offsets, src_offsets, first, count, plan);
+    long long rc = launch_decode(a, g, plan, stream);
     if (rc < 0) return rc;
   }
   return (long long)total;
