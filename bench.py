@@ -31,6 +31,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0
+CALIBRATION_BYTES = 256 << 20
 METRIC = "codec encode/decode GB/s of raw bf16 KV (% HBM peak) + compression ratio"
 
 
@@ -211,7 +212,16 @@ def main() -> int:
             step()
         torch.cuda.synchronize()
         verify(torch, w)
-        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload}))
+        # calibration for HBM counters: one plain copy of a known size (256 MiB
+        # read + 256 MiB written) in the same process
+        src = torch.empty(CALIBRATION_BYTES // 2, dtype=torch.int16, device=w["device"])
+        src.fill_(3)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload,
+                          "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
 
     for _ in range(args.warmup):
