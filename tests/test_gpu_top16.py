@@ -296,6 +296,44 @@ def test_paged_encode_decode_matches_oracle(sz, codebooks, bw, pool, requests, r
     assert not got[:, free].any()
 
 
+@pytest.mark.parametrize("label", ["dense tile", "overflow"])
+def test_paged_escape_heavy_tiles(sz, codebooks, label):
+    """Tiles with more escapes than the tile kernel stages (re-scan in the finalize
+    kernel), and a payload whose escapes overflow the capacity (header 255)."""
+    say("paged escape-heavy", label)
+    bw, pool = 2048, 64
+    books = codebooks[3 * 32:4 * 32]
+    tables = oracle.top16_tables(books)
+    rng = np.random.default_rng(31)
+    words = random_words(rng, 2 * pool * bw, books, 0.0 if label == "dense tile" else 0.01)
+    kv_host = words.reshape(2, pool, bw)
+    block_tables = [[5, 9, 1, 30, 50, 51, 52, 53, 54, 55, 56, 57, 58, 59, 60, 61, 62, 3, 4, 6],
+                    [44, 2], [7, 8, 63, 12, 40, 41, 42, 43]]
+    if label == "dense tile":
+        outside = sorted(set(range(256)) - set(books))
+        # 300 escapes inside one tile of payload 0's V plane (cap 410) and 60 in one
+        # tile of payload 2's K plane (cap 164)
+        for blk, lo, count in ((1, 2048 + 100, 300), (12, 0, 60)):
+            for w in range(lo % bw, lo % bw + count):
+                plane = 1 if blk == 1 else 0
+                kv_host[plane, blk, w] = (kv_host[plane, blk, w] & 0x807F) | (
+                    outside[w % len(outside)] << 7)
+    kv = bf16(kv_host.reshape(-1)).view(2, pool, bw)
+    batch = sz.PagedBatch(block_tables, bw, "cuda")
+    out = batch.new_payload_buffer()
+    out.fill_(0x77)
+    ws = batch.new_workspace()
+    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books) == batch.total_encoded_bytes
+    torch.cuda.synchronize()
+    host = out.cpu().numpy()
+    for r, t in enumerate(block_tables):
+        ref = oracle.top16_encode(kv_host[:, t].reshape(-1), tables)
+        got = host[batch.out_offsets[r]:batch.out_offsets[r] + batch.encoded_bytes[r]]
+        assert bytes(got) == bytes(ref), f"payload {r}"
+        if label == "overflow":
+            assert got[0] == 255
+
+
 def test_paged_full_size_llama3_8b_layer(sz):
     """One full layer of the Llama-3-8B paged encode workload (8 requests x 4096
     tokens from a 4096-block pool): byte parity of every payload with the oracle

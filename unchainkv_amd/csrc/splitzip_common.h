@@ -59,8 +59,46 @@ struct LaunchArgs {
   unsigned int total_tiles;
   unsigned int tiles_per_plane_mode;  // 1: tiles never cross a plane (fast path); 0: one range [0, n)
   unsigned int tile_shift;            // log2 of the tile size in words
+  unsigned int uniform_tiles;         // tiles of every payload when all are equal, else 0
   PayloadDesc p[kMaxPayloads];
 };
+
+// ---------------------------------------------------------------------------
+// streaming (nontemporal) vector memory access: the codec reads its source once
+// and writes its destination once, so neither should displace cached data.
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+#ifndef UKV_NT_LOADS
+#define UKV_NT_LOADS 1
+#endif
+#ifndef UKV_NT_STORES
+#define UKV_NT_STORES 1
+#endif
+
+template <typename T>
+__device__ __forceinline__ T load_stream(const void* p) {
+#if UKV_NT_LOADS
+  return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+#else
+  return *reinterpret_cast<const T*>(p);
+#endif
+}
+template <typename T>
+__device__ __forceinline__ void store_stream(void* p, T v) {
+#if UKV_NT_STORES
+  __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
+#else
+  *reinterpret_cast<T*>(p) = v;
+#endif
+}
+__device__ __forceinline__ u32x4 load_stream16(const void* p) { return load_stream<u32x4>(p); }
+__device__ __forceinline__ u32x2 load_stream8(const void* p) { return load_stream<u32x2>(p); }
+__device__ __forceinline__ uint32_t load_stream4(const void* p) { return load_stream<uint32_t>(p); }
+__device__ __forceinline__ void store_stream16(void* p, u32x4 v) { store_stream<u32x4>(p, v); }
+__device__ __forceinline__ void store_stream8(void* p, u32x2 v) { store_stream<u32x2>(p, v); }
+__device__ __forceinline__ void store_stream4(void* p, uint32_t v) { store_stream<uint32_t>(p, v); }
 
 // ---------------------------------------------------------------------------
 // launch-shape helpers
@@ -73,6 +111,7 @@ __device__ __forceinline__ unsigned int xcd_remap(unsigned int wg, unsigned int 
 }
 
 __device__ __forceinline__ unsigned int find_payload(const LaunchArgs& a, unsigned int tile) {
+  if (a.uniform_tiles) return tile / a.uniform_tiles;
   unsigned int r = 0;
   for (unsigned int k = 1; k < a.payload_count; ++k)
     if (a.p[k].tile_begin <= tile) r = k;

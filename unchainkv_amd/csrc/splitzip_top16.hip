@@ -52,9 +52,9 @@ long long fail_msg(const std::string& msg) {
 
 namespace {
 
-constexpr int kFinGroups = 8;     // finalize workgroups per payload
-constexpr int kFinChunk = 8192;   // tiles scanned per finalize pass (LDS resident)
-constexpr int kPatchGroups = 8;   // escape-patch workgroups per payload
+constexpr int kFinGroups = 8;                          // finalize workgroups per payload
+constexpr int kFinPerThread = 8;                       // tile counts per thread per pass
+constexpr int kFinChunk = kThreads * kFinPerThread;    // tiles scanned per finalize pass
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
   return (n + 199) / 200;
@@ -273,6 +273,7 @@ struct TileInfo {
   unsigned long long n, half, start, end, ids_offset;
   unsigned char* payload;
   unsigned int plane;
+  unsigned int local_tile;  // tile index within its payload
 };
 
 __device__ __forceinline__ TileInfo tile_info(const LaunchArgs& a, unsigned int tile) {
@@ -281,11 +282,25 @@ __device__ __forceinline__ TileInfo tile_info(const LaunchArgs& a, unsigned int 
   const PayloadDesc d = a.p[r];
   t.n = payload_words(a, d);
   t.half = t.n >> 1;
-  tile_range(a, d, tile - d.tile_begin, t.n, t.start, t.end);
+  t.local_tile = tile - d.tile_begin;
+  tile_range(a, d, t.local_tile, t.n, t.start, t.end);
   t.plane = t.start >= t.half ? 1u : 0u;
   t.payload = a.buf + d.buf_offset;
   t.ids_offset = d.ids_offset;
   return t;
+}
+
+// Zeroes tile `local_tile`'s share of its payload's escape section; the finalize
+// kernel then writes the used slots over it (workgroup-cooperative, no barrier).
+__device__ __forceinline__ void zero_escape_share(const LaunchArgs& a, unsigned char* payload,
+                                                  unsigned long long n, unsigned int local_tile) {
+  const unsigned int tiles = payload_tiles(a, n);
+  const unsigned int len = (unsigned int)(5 * escape_capacity(n));  // < 2^30 for n < 2^32
+  const unsigned int share = (len + tiles - 1) / tiles;
+  const unsigned int lo = share * local_tile;
+  if (lo >= len) return;
+  const unsigned int hi = min(lo + share, len);
+  zero_fill(payload + 5 + n + (n + 1) / 2 + lo, hi - lo);
 }
 
 // Element offset in the paged layer of payload word i (i inside plane t.plane).
@@ -447,6 +462,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
         }
       }
       if (tid == 0) a.workspace[tile] = tile_total;
+      zero_escape_share(a, payload, n, tile - d.tile_begin);
     }
   }
 
@@ -467,12 +483,27 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
 // ---------------------------------------------------------------------------
 // Tile kernels: the batched layout (aligned sections) with one block per wave.
 //
-// A workgroup encodes/decodes one 4096-word tile of one plane; wave w covers words
+// A workgroup handles one 4096-word tile of one plane; wave w covers words
 // [start + 1024w, start + 1024w + 1024), which lie in one KV block (block words a
 // multiple of 1024), so block lookup and every base address are wave-uniform
-// scalars and lane l handles words 16l .. 16l + 15 of its wave's range. The
-// per-word work is a handful of VALU operations (byte permutes, bit-field inserts)
-// plus one LDS lookup for the encoder.
+// scalars. Lane l handles two 8-word runs of its wave's range, words 8l .. 8l + 7
+// ("run A") and 512 + 8l .. 512 + 8l + 7 ("run B"), so that every vector memory
+// instruction of the wave covers one contiguous span (1 KiB of bf16, 512 B of body
+// bytes, 256 B of code bytes). The per-word work is a handful of VALU operations
+// (byte permutes, bit-field inserts) plus one LDS lookup for the encoder.
+
+#ifndef UKV_XCD_REMAP
+#define UKV_XCD_REMAP 1
+#endif
+
+// Index of this workgroup's tile (XCD-aware: each XCD walks a contiguous run).
+__device__ __forceinline__ unsigned int group_index() {
+#if UKV_XCD_REMAP
+  return xcd_remap(blockIdx.x, gridDim.x);
+#else
+  return blockIdx.x;
+#endif
+}
 
 // Scalar (SGPR) copies of wave-uniform values.
 __device__ __forceinline__ unsigned int uniform(unsigned int v) {
@@ -496,100 +527,142 @@ __device__ __forceinline__ unsigned long long wave_block_offset(const LaunchArgs
   return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
 }
 
-__global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
-  __shared__ unsigned char s_tab[256];  // this tile's plane: code, or 0x10 for an escape
-  __shared__ unsigned int s_wave[kThreads / kWave];
-  const unsigned int tid = threadIdx.x;
-  const unsigned int lane = tid & (kWave - 1);
-  const unsigned int wave = uniform(tid >> 6);
-  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const TileInfo t = tile_info(a, tile);
-  if (tid < 64) {
-    const uint32_t raw = *reinterpret_cast<const uint32_t*>(a.tables + t.plane * 256 + 4 * tid);
-    uint32_t packed = 0;
+// Code table byte for each of four exponents packed in a dword of the 544-byte
+// table: the code (0..15), or 0x10 for an escape (a code byte other than 255 keeps
+// its low nibble, as the reference's `(code & 0x0F)` does).
+__device__ __forceinline__ uint32_t pack_codes4(uint32_t raw) {
+  uint32_t packed = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t c = (raw >> (8 * e)) & 0xFF;
-      packed |= (c == 255 ? 0x10u : (c & 0x0Fu)) << (8 * e);
-    }
-    reinterpret_cast<uint32_t*>(s_tab)[tid] = packed;
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t c = (raw >> (8 * e)) & 0xFF;
+    packed |= (c == 255 ? 0x10u : (c & 0x0Fu)) << (8 * e);
   }
-  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
-  const bool active = wstart < t.end;  // whole waves (plane words are a multiple of 1024)
-  uint32_t x[8];
-  if (active) {
-    const uint16_t* src = a.kv + wave_block_offset(a, t, geo, wstart);
-    const uint4 v0 = reinterpret_cast<const uint4*>(src)[2 * lane];
-    const uint4 v1 = reinterpret_cast<const uint4*>(src)[2 * lane + 1];
-    x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
-    x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) x[k] = 0;
-  }
-  __syncthreads();  // s_tab ready
+  return packed;
+}
 
-  uint32_t body[4], codes[2], flags = 0, D[4];
+// Encodes one 8-word run (4 dwords) with the code table of its plane: 8 body
+// bytes, 4 code bytes, and an 8-bit escape mask.
+__device__ __forceinline__ void encode_run8(const uint32_t* x, const unsigned char* tab,
+                                            uint32_t (&body)[2], uint32_t& codes,
+                                            uint32_t& emask) {
+  uint32_t D[2], flags = 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < 2; ++q) {
     // body bytes of 4 words: mantissa bits 0-6 and the sign bit into bit 7
     // (bytes 1 and 3 of t0/t1 are don't-care: the permute keeps bytes 0 and 2)
-    const uint32_t t0 = (x[2 * q] & 0x007F007Fu) | ((x[2 * q] >> 8) & ~0x007F007Fu);
-    const uint32_t t1 = (x[2 * q + 1] & 0x007F007Fu) | ((x[2 * q + 1] >> 8) & ~0x007F007Fu);
+    const uint32_t w0 = x[2 * q], w1 = x[2 * q + 1];
+    const uint32_t t0 = (w0 & 0x007F007Fu) | ((w0 >> 8) & ~0x007F007Fu);
+    const uint32_t t1 = (w1 & 0x007F007Fu) | ((w1 >> 8) & ~0x007F007Fu);
     body[q] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
     // codes of 4 words, one per byte (0x10 marks an escape)
-    const uint32_t c0 = s_tab[(x[2 * q] >> 7) & 0xFF];
-    const uint32_t c1 = s_tab[(x[2 * q] >> 23) & 0xFF];
-    const uint32_t c2 = s_tab[(x[2 * q + 1] >> 7) & 0xFF];
-    const uint32_t c3 = s_tab[(x[2 * q + 1] >> 23) & 0xFF];
+    const uint32_t c0 = tab[(w0 >> 7) & 0xFF];
+    const uint32_t c1 = tab[(w0 >> 23) & 0xFF];
+    const uint32_t c2 = tab[(w1 >> 7) & 0xFF];
+    const uint32_t c3 = tab[(w1 >> 23) & 0xFF];
     D[q] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
     flags |= D[q];
   }
+  const uint32_t ta = D[0] & 0x0F0F0F0Fu, tb = D[1] & 0x0F0F0F0Fu;
+  codes = __builtin_amdgcn_perm(tb | (tb >> 4), ta | (ta >> 4), 0x06040200u);
+  emask = 0;
+  if (flags & 0x10101010u) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t ta = D[2 * h] & 0x0F0F0F0Fu, tb = D[2 * h + 1] & 0x0F0F0F0Fu;
-    codes[h] = __builtin_amdgcn_perm(tb | (tb >> 4), ta | (ta >> 4), 0x06040200u);
-  }
-  if (active) {
-    unsigned char* pbody = t.payload + 5 + wstart;
-    unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
-    reinterpret_cast<uint4*>(pbody)[lane] = make_uint4(body[0], body[1], body[2], body[3]);
-    reinterpret_cast<uint2*>(pcode)[lane] = make_uint2(codes[0], codes[1]);
-  }
-
-  // escapes (rare): per-lane mask, workgroup prefix in ascending word order
-  uint32_t emask = 0;
-  if (active && (flags & 0x10101010u)) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       const uint32_t m = D[q] & 0x10101010u;
       emask |= (((m >> 4) & 1) | ((m >> 11) & 2) | ((m >> 18) & 4) | ((m >> 25) & 8)) << (4 * q);
     }
   }
-  const unsigned int cnt = __popc(emask);
-  const unsigned int incl = __ballot(cnt != 0) ? wave_inclusive_sum(cnt) : 0u;
-  if (lane == kWave - 1) s_wave[wave] = incl;
+}
+
+__global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
+  __shared__ uint32_t s_tab[64];  // this tile's plane, 4 code bytes per dword
+  __shared__ unsigned int s_wave[kThreads / kWave];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1);
+  const unsigned int wave = uniform(tid >> 6);
+  const unsigned int tile = group_index();
+  const TileInfo t = tile_info(a, tile);
+  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
+  const bool active = wstart < t.end;  // whole waves (plane words are a multiple of 1024)
+  // source loads first, then the code table, so the table's round trip overlaps them
+  uint32_t x[8];
+  if (active) {
+    const uint16_t* src = a.kv + wave_block_offset(a, t, geo, wstart);
+    const u32x4 v0 = load_stream16(src + 8 * lane);
+    const u32x4 v1 = load_stream16(src + 512 + 8 * lane);
+    x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+    x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) x[q] = 0;
+  }
+  if (tid < 64)
+    s_tab[tid] = pack_codes4(reinterpret_cast<const uint32_t*>(a.tables + t.plane * 256)[tid]);
+  __syncthreads();  // s_tab ready
+  const unsigned char* tab = reinterpret_cast<const unsigned char*>(s_tab);
+
+  uint32_t body_a[2], body_b[2], code_a, code_b, mask_a, mask_b;
+  encode_run8(x, tab, body_a, code_a, mask_a);
+  encode_run8(x + 4, tab, body_b, code_b, mask_b);
+  if (active) {
+    unsigned char* pbody = t.payload + 5 + wstart;
+    unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+    store_stream8(pbody + 8 * lane, u32x2{body_a[0], body_a[1]});
+    store_stream8(pbody + 512 + 8 * lane, u32x2{body_b[0], body_b[1]});
+    store_stream4(pcode + 4 * lane, code_a);
+    store_stream4(pcode + 256 + 4 * lane, code_b);
+  } else {
+    mask_a = mask_b = 0;
+  }
+
+  // escapes (rare), in ascending word order: run A of every lane of the wave,
+  // then run B of every lane, then the next wave. Per-lane counts of both runs are
+  // packed into one word (16 bits each) for a single shuffle scan; a wave without
+  // escapes skips the scan.
+  const unsigned int cnt = __popc(mask_a) | (__popc(mask_b) << 16);
+  unsigned int incl = 0;
+  if (__ballot(cnt != 0)) {
+    incl = cnt;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const unsigned int v = (unsigned int)__shfl_up((int)incl, d, kWave);
+      if (lane >= (unsigned int)d) incl += v;
+    }
+  }
+  const unsigned int wave_tot = uniform((unsigned int)__shfl((int)incl, kWave - 1, kWave));
+  const unsigned int wave_a = wave_tot & 0xFFFFu;
+  if (lane == 0) s_wave[wave] = wave_a + (wave_tot >> 16);
   __syncthreads();
-  unsigned int before = 0, tile_total = 0;
+  unsigned int before = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / kWave; ++w) {
     const unsigned int v = s_wave[w];
     if (w < (int)wave) before += v;
-    tile_total += v;
+    total += v;
   }
-  if (tid == 0) a.workspace[tile] = tile_total;
-  if (emask) {
+  if (tid == 0) a.workspace[tile] = total;
+  if (mask_a | mask_b) {
+    const unsigned int excl = incl - cnt;
     unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
-    unsigned int idx = before + incl - cnt;
-    const unsigned int local0 = (unsigned int)(wstart - t.start) + lane * kWordsPerLane;
+    const unsigned int local = wave * 1024 + lane * 8;
+    unsigned int idx = before + (excl & 0xFFFFu);
 #pragma unroll
-    for (int k = 0; k < kWordsPerLane; ++k) {
-      if (!((emask >> k) & 1)) continue;
+    for (int j = 0; j < 8; ++j) {
+      if (!((mask_a >> j) & 1)) continue;
       if (idx < kStageSlots)
-        staged[idx] = ((local0 + k) << 8) | ((x[k >> 1] >> (7 + 16 * (k & 1))) & 0xFF);
+        staged[idx] = ((local + j) << 8) | ((x[j >> 1] >> (7 + 16 * (j & 1))) & 0xFF);
+      ++idx;
+    }
+    idx = before + wave_a + (excl >> 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (!((mask_b >> j) & 1)) continue;
+      if (idx < kStageSlots)
+        staged[idx] = ((local + 512 + j) << 8) | ((x[4 + (j >> 1)] >> (7 + 16 * (j & 1))) & 0xFF);
       ++idx;
     }
   }
+  zero_escape_share(a, t.payload, t.n, t.local_tile);
 }
 
 // Per-byte 0xFF/0x00 masks from bit 3 of each byte of s (byte permute with the
@@ -615,40 +688,45 @@ __device__ __forceinline__ uint32_t assemble_pair(uint32_t x) {
   return ((x << 8) & 0x80008000u) | (y & ~0x80008000u);
 }
 
+// Decodes one 8-word run: 8 body bytes (2 dwords) and 4 code bytes -> 4 dwords.
+__device__ __forceinline__ u32x4 decode_run8(u32x2 body, uint32_t cd, const uint32_t (&cb)[4]) {
+  const uint32_t u = cd >> 4;
+  // codes of the 8 words as bytes (low nibble first)
+  const uint32_t sa = __builtin_amdgcn_perm(u, cd, 0x05010400u) & 0x0F0F0F0Fu;
+  const uint32_t sb = __builtin_amdgcn_perm(u, cd, 0x07030602u) & 0x0F0F0F0Fu;
+  const uint32_t ea = codebook_lookup4(sa, cb);
+  const uint32_t eb = codebook_lookup4(sb, cb);
+  return u32x4{assemble_pair(__builtin_amdgcn_perm(ea, body.x, 0x05010400u)),
+               assemble_pair(__builtin_amdgcn_perm(ea, body.x, 0x07030602u)),
+               assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x05010400u)),
+               assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x07030602u))};
+}
+
 __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = uniform(threadIdx.x >> 6);
-  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const TileInfo t = tile_info(a, tile);
+  const TileInfo t = tile_info(a, group_index());
   const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
-  if (wstart >= t.end) return;  // no barrier in this kernel
+  if (wstart >= t.end) return;  // whole waves; no barrier in this kernel
   const unsigned int mode = t.payload[0];
   const uint32_t* cbw = reinterpret_cast<const uint32_t*>(a.tables + 512 + t.plane * 16);
   const uint32_t cb[4] = {cbw[0], cbw[1], cbw[2], cbw[3]};
-  const uint4 b4 = reinterpret_cast<const uint4*>(t.payload + 5 + wstart)[lane];
-  const uint2 c2 = reinterpret_cast<const uint2*>(t.payload + 5 + t.n + (wstart >> 1))[lane];
+  const unsigned char* pbody = t.payload + 5 + wstart;
+  const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+  const u32x2 body_a = load_stream8(pbody + 8 * lane);
+  const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
+  const uint32_t code_a = load_stream4(pcode + 4 * lane);
+  const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
   uint16_t* dst = a.kv + wave_block_offset(a, t, geo, wstart);
+  const u32x4 out_a = decode_run8(body_a, code_a, cb);
+  const u32x4 out_b = decode_run8(body_b, code_b, cb);
+  // Keeps the payload loads ahead of the mode test below: without this use the
+  // compiler sinks them under the test and the mode byte's round trip comes first.
+  asm volatile("" ::"v"(out_a), "v"(out_b));
   // the reference decoder leaves a payload whose byte 0 is not 5 untouched
   if (mode != 5) return;
-  const uint32_t body[4] = {b4.x, b4.y, b4.z, b4.w};
-  const uint32_t cd[2] = {c2.x, c2.y};
-  uint32_t out[8];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const uint32_t u = cd[h] >> 4;
-    // codes of words 8h .. 8h + 7 as bytes (low nibble first)
-    const uint32_t sa = __builtin_amdgcn_perm(u, cd[h], 0x05010400u) & 0x0F0F0F0Fu;
-    const uint32_t sb = __builtin_amdgcn_perm(u, cd[h], 0x07030602u) & 0x0F0F0F0Fu;
-    const uint32_t ea = codebook_lookup4(sa, cb);
-    const uint32_t eb = codebook_lookup4(sb, cb);
-    out[4 * h + 0] = assemble_pair(__builtin_amdgcn_perm(ea, body[2 * h], 0x05010400u));
-    out[4 * h + 1] = assemble_pair(__builtin_amdgcn_perm(ea, body[2 * h], 0x07030602u));
-    out[4 * h + 2] = assemble_pair(__builtin_amdgcn_perm(eb, body[2 * h + 1], 0x05010400u));
-    out[4 * h + 3] = assemble_pair(__builtin_amdgcn_perm(eb, body[2 * h + 1], 0x07030602u));
-  }
-  uint4* d4 = reinterpret_cast<uint4*>(dst) + 2 * lane;
-  d4[0] = make_uint4(out[0], out[1], out[2], out[3]);
-  d4[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  store_stream16(dst + 8 * lane, out_a);
+  store_stream16(dst + 512 + 8 * lane, out_b);
 }
 
 // Scans the escapes of one tile from the source words (tiles with more escapes
@@ -689,15 +767,11 @@ __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned 
 }
 
 __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
-  __shared__ unsigned int s_base[kFinChunk];
-  __shared__ unsigned int s_cnt[kFinChunk];
-  __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups + 1];
-  __shared__ unsigned int s_over_base[kFinChunk / kFinGroups + 1];
+  __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups];
+  __shared__ unsigned int s_over_base[kFinChunk / kFinGroups];
   __shared__ unsigned int s_over_count;
   __shared__ unsigned int s_wave[kThreads / kWave];
   __shared__ unsigned char s_tab[512];
-  constexpr int kPerThread = kFinChunk / kThreads;  // 16 tiles per thread per pass
-
   const unsigned int tid = threadIdx.x;
   const unsigned int r = blockIdx.x / kFinGroups;
   const unsigned int grp = blockIdx.x % kFinGroups;
@@ -710,37 +784,31 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   const unsigned int* counts = a.workspace + d.tile_begin;
   const unsigned int* staged =
       a.workspace + a.total_tiles + (unsigned long long)d.tile_begin * kStageSlots;
-  load_code_table(a.tables, s_tab);
+  if (tid == 0) s_over_count = 0;  // ordered by the barriers of the first scan
 
-  unsigned long long running = 0;
+  unsigned long long running = 0;  // escapes in earlier chunks
   for (unsigned int chunk0 = 0; chunk0 < tiles; chunk0 += kFinChunk) {
     const unsigned int m = min((unsigned int)kFinChunk, tiles - chunk0);
-    // exclusive scan of this chunk's counts into s_base
-    unsigned int mine[kPerThread];
+    // thread tid holds the counts of tiles chunk0 + tid * kFinPerThread + k
+    unsigned int mine[kFinPerThread];
     unsigned int sum = 0;
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
-      const unsigned int t = tid * kPerThread + k;
+    for (int k = 0; k < kFinPerThread; ++k) {
+      const unsigned int t = tid * kFinPerThread + k;
       mine[k] = t < m ? counts[chunk0 + t] : 0;
       sum += mine[k];
     }
     unsigned int chunk_total;
     unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
-#pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
-      s_base[tid * kPerThread + k] = prefix;
-      s_cnt[tid * kPerThread + k] = mine[k];
-      prefix += mine[k];
-    }
-    if (tid == 0) s_over_count = 0;
-    __syncthreads();
 
     // staged escapes of this group's tiles go straight to their slots
-    for (unsigned int t = grp + tid * kFinGroups; t < m; t += kThreads * kFinGroups) {
-      const unsigned int c = s_cnt[t];
-      if (c == 0) continue;
-      const unsigned long long base = running + s_base[t];
-      if (base >= cap) continue;
+#pragma unroll
+    for (int k = 0; k < kFinPerThread; ++k) {
+      const unsigned int t = tid * kFinPerThread + k;
+      const unsigned int c = mine[k];
+      const unsigned long long base = running + prefix;
+      prefix += c;
+      if (t % kFinGroups != grp || c == 0 || base >= cap) continue;
       if (c > (unsigned int)kStageSlots) {
         const unsigned int q = atomicAdd(&s_over_count, 1u);
         s_over_tile[q] = chunk0 + t;
@@ -756,20 +824,20 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       }
     }
     __syncthreads();
+    // tiles with more escapes than were staged are scanned again from the source
     const unsigned int over = s_over_count;
-    for (unsigned int q = 0; q < over; ++q)
-      rescan_tile(a, d, s_over_tile[q], n, s_over_base[q], s_tab, s_wave, entries, cap);
+    if (over) {
+      load_code_table(a.tables, s_tab);
+      __syncthreads();
+      for (unsigned int q = 0; q < over; ++q)
+        rescan_tile(a, d, s_over_tile[q], n, s_over_base[q], s_tab, s_wave, entries, cap);
+    }
     running += chunk_total;
     __syncthreads();
+    if (tid == 0) s_over_count = 0;
   }
 
-  // unused escape slots are zeroed, split across the payload's groups
-  const unsigned long long used = running < cap ? running : cap;
-  const unsigned long long pad = 5 * (cap - used);
-  const unsigned long long per = (pad + kFinGroups - 1) / kFinGroups;
-  const unsigned long long lo = per * grp < pad ? per * grp : pad;
-  const unsigned long long hi = lo + per < pad ? lo + per : pad;
-  zero_fill(entries + 5 * used + lo, hi - lo);
+  // unused escape slots were zeroed by the tile kernel
   if (grp == 0 && tid == 0) write_header(payload, n, running);
 }
 
@@ -833,30 +901,34 @@ __global__ __launch_bounds__(kThreads) void top16_decode_generic(LaunchArgs a) {
 }
 
 // ApplyTop16Escapes semantics (kvq_splitzip_cuda.cu:253-284): for slot <
-// min(count, cap) with position < n, set the word's exponent bits.
-__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
-  const unsigned int r = blockIdx.x / kPatchGroups;
-  const unsigned int grp = blockIdx.x % kPatchGroups;
+// min(count, cap) with position < n, the word gets the escape's exponent bits.
+// The decode kernel wrote sign and mantissa from the body byte, so the patched word
+// is rebuilt from that byte and stored (no read of the destination). One thread
+// per escape slot: grid = payload_count x slot_groups.
+__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a,
+                                                                unsigned int slot_groups) {
+  const unsigned int r = blockIdx.x / slot_groups;
+  const unsigned long long s =
+      (unsigned long long)(blockIdx.x % slot_groups) * kThreads + threadIdx.x;
   const PayloadDesc d = a.p[r];
-  const unsigned char* payload = a.buf + d.buf_offset;
-  if (payload[0] != 5) return;
   const unsigned long long n = payload_words(a, d);
   const unsigned long long cap = escape_capacity(n);
-  unsigned long long count = (unsigned long long)payload[1] | ((unsigned long long)payload[2] << 8) |
-                             ((unsigned long long)payload[3] << 16) |
-                             ((unsigned long long)payload[4] << 24);
-  if (count > cap) count = cap;
-  const unsigned char* entries = payload + 5 + n + (n + 1) / 2;
-  for (unsigned long long s = (unsigned long long)grp * kThreads + threadIdx.x; s < count;
-       s += (unsigned long long)kPatchGroups * kThreads) {
-    const unsigned char* e = entries + s * 5;
-    const unsigned long long pos = (unsigned long long)e[0] | ((unsigned long long)e[1] << 8) |
-                                   ((unsigned long long)e[2] << 16) |
-                                   ((unsigned long long)e[3] << 24);
-    if (pos >= n) continue;
-    uint16_t* w = a.kv + word_offset(a, d, pos);
-    *w = (uint16_t)((*w & 0x807F) | ((uint32_t)e[4] << 7));
-  }
+  if (s >= cap) return;
+  const unsigned char* payload = a.buf + d.buf_offset;
+  const unsigned char* e = payload + 5 + n + (n + 1) / 2 + s * 5;
+  // header and entry are independent loads
+  const unsigned int mode = payload[0];
+  const unsigned long long count = (unsigned long long)payload[1] |
+                                   ((unsigned long long)payload[2] << 8) |
+                                   ((unsigned long long)payload[3] << 16) |
+                                   ((unsigned long long)payload[4] << 24);
+  const unsigned long long pos = (unsigned long long)e[0] | ((unsigned long long)e[1] << 8) |
+                                 ((unsigned long long)e[2] << 16) |
+                                 ((unsigned long long)e[3] << 24);
+  const unsigned int exponent = e[4];
+  if (mode != 5 || s >= count || pos >= n) return;
+  const unsigned int b = payload[5 + pos];
+  a.kv[word_offset(a, d, pos)] = (uint16_t)((b & 0x7F) | ((b & 0x80) << 8) | (exponent << 7));
 }
 
 // ---------------------------------------------------------------------------
@@ -967,8 +1039,15 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     }
   }
   if (long long rc = check_launch("top16_decode")) return rc;
-  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * kPatchGroups), block, 0, stream,
-                     a);
+  unsigned long long max_cap = 0;
+  for (unsigned int r = 0; r < a.payload_count; ++r) {
+    const unsigned long long n =
+        a.linear_words ? a.linear_words : 2ull * a.p[r].block_count * a.block_words;
+    max_cap = std::max(max_cap, escape_capacity(n));
+  }
+  const unsigned int slot_groups = (unsigned int)((max_cap + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * slot_groups), block, 0, stream,
+                     a, slot_groups);
   return check_launch("top16_patch_escapes");
 }
 
@@ -1138,6 +1217,7 @@ unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
                         const unsigned long long* buf_offsets, unsigned long long first,
                         unsigned int count, const Plan& plan) {
   unsigned int tiles = 0;
+  bool uniform = true;
   for (unsigned int k = 0; k < count; ++k) {
     const unsigned long long r = first + k;
     const unsigned long long nblk = block_offsets[r + 1] - block_offsets[r];
@@ -1146,9 +1226,13 @@ unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
     a.p[k].block_count = (unsigned int)nblk;
     a.p[k].tile_begin = tiles;
     tiles += host_payload_tiles(2 * nblk * pg.block_words, plan.per_plane, plan.tile_shift);
+    uniform = uniform && nblk == block_offsets[first + 1] - block_offsets[first];
   }
   a.payload_count = count;
   a.total_tiles = tiles;
+  // every payload has the same tile count: the kernels find a tile's payload by
+  // one division instead of a search of the descriptors
+  a.uniform_tiles = uniform ? tiles / count : 0;
   return tiles;
 }
 
