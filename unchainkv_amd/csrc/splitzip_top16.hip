@@ -55,6 +55,7 @@ namespace {
 constexpr int kFinGroups = 8;                          // finalize workgroups per payload
 constexpr int kFinPerThread = 8;                       // tile counts per thread per pass
 constexpr int kFinChunk = kThreads * kFinPerThread;    // tiles scanned per finalize pass
+constexpr int kFinPreload = 4;                         // staged escapes loaded with the counts
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
   return (n + 199) / 200;
@@ -292,9 +293,8 @@ __device__ __forceinline__ TileInfo tile_info(const LaunchArgs& a, unsigned int 
 
 // Zeroes tile `local_tile`'s share of its payload's escape section; the finalize
 // kernel then writes the used slots over it (workgroup-cooperative, no barrier).
-__device__ __forceinline__ void zero_escape_share(const LaunchArgs& a, unsigned char* payload,
-                                                  unsigned long long n, unsigned int local_tile) {
-  const unsigned int tiles = payload_tiles(a, n);
+__device__ __forceinline__ void zero_escape_share(unsigned char* payload, unsigned long long n,
+                                                  unsigned int local_tile, unsigned int tiles) {
   const unsigned int len = (unsigned int)(5 * escape_capacity(n));  // < 2^30 for n < 2^32
   const unsigned int share = (len + tiles - 1) / tiles;
   const unsigned int lo = share * local_tile;
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
         }
       }
       if (tid == 0) a.workspace[tile] = tile_total;
-      zero_escape_share(a, payload, n, tile - d.tile_begin);
+      zero_escape_share(payload, n, tile - d.tile_begin, payload_tiles(a, n));
     }
   }
 
@@ -514,16 +514,49 @@ __device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
          __builtin_amdgcn_readfirstlane((unsigned int)v);
 }
 
-// Wave-uniform element offset of payload word i (in plane t.plane) in the layer.
-__device__ __forceinline__ unsigned long long wave_block_offset(const LaunchArgs& a,
-                                                                const TileInfo& t,
-                                                                const EncodeGeom& geo,
-                                                                unsigned long long i) {
-  const unsigned int in_plane = uniform((unsigned int)(i - t.plane * t.half));
+// One 4096-word tile of the per-plane tiling that the tile kernels use. In-plane
+// arithmetic is 32-bit (the host only picks these kernels for plane words < 2^31)
+// and free of branches on the launch layout, so the kernel-argument loads of the
+// prologue can be issued together.
+struct PlaneTile {
+  unsigned long long n;   // payload words
+  unsigned char* payload;
+  const long long* ids;   // the payload's block table (when there is one)
+  unsigned int plane;
+  unsigned int in_plane0;  // first word of the tile within its plane
+  unsigned int words;      // words in the tile: a multiple of 1024, at most the tile size
+  unsigned int local_tile;
+  unsigned int payload_tiles;
+};
+
+template <int kShift>
+__device__ __forceinline__ PlaneTile plane_tile(const LaunchArgs& a, unsigned int tile) {
+  constexpr unsigned int kWords = 1u << kShift;
+  PlaneTile t;
+  const PayloadDesc d = a.p[find_payload(a, tile)];
+  const unsigned int plane_words = d.block_count * (unsigned int)a.block_words;
+  const unsigned int tpp = (plane_words + kWords - 1) >> kShift;
+  t.local_tile = tile - d.tile_begin;
+  t.plane = t.local_tile >= tpp ? 1u : 0u;
+  t.in_plane0 = (t.local_tile - t.plane * tpp) << kShift;
+  t.words = min(kWords, plane_words - t.in_plane0);
+  t.n = 2ull * plane_words;
+  t.payload = a.buf + d.buf_offset;
+  t.ids = a.ids + d.ids_offset;
+  t.payload_tiles = 2 * tpp;
+  return t;
+}
+
+// Wave-uniform element offset in the layer of in-plane word `in_plane` of tile t
+// (block from the payload's block table, or block_start + j without one).
+template <bool kIds>
+__device__ __forceinline__ unsigned long long wave_source(const LaunchArgs& a, const PlaneTile& t,
+                                                          const EncodeGeom& geo,
+                                                          unsigned int in_plane) {
   const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
   const unsigned int within = in_plane - j * geo.bw;
   const unsigned long long blk =
-      a.ids ? (unsigned long long)a.ids[t.ids_offset + j] : a.block_start + j;
+      kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
   return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
 }
 
@@ -574,6 +607,7 @@ __device__ __forceinline__ void encode_run8(const uint32_t* x, const unsigned ch
   }
 }
 
+template <bool kIds>
 __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
   __shared__ uint32_t s_tab[64];  // this tile's plane, 4 code bytes per dword
   __shared__ unsigned int s_wave[kThreads / kWave];
@@ -581,13 +615,14 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
   const unsigned int lane = tid & (kWave - 1);
   const unsigned int wave = uniform(tid >> 6);
   const unsigned int tile = group_index();
-  const TileInfo t = tile_info(a, tile);
-  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
-  const bool active = wstart < t.end;  // whole waves (plane words are a multiple of 1024)
+  const PlaneTile t = plane_tile<kTileShift>(a, tile);
+  const unsigned int in_plane = t.in_plane0 + wave * 1024;
+  const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
+  const bool active = wave * 1024 < t.words;  // whole waves
   // source loads first, then the code table, so the table's round trip overlaps them
   uint32_t x[8];
   if (active) {
-    const uint16_t* src = a.kv + wave_block_offset(a, t, geo, wstart);
+    const uint16_t* src = a.kv + wave_source<kIds>(a, t, geo, in_plane);
     const u32x4 v0 = load_stream16(src + 8 * lane);
     const u32x4 v1 = load_stream16(src + 512 + 8 * lane);
     x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
@@ -662,7 +697,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
       ++idx;
     }
   }
-  zero_escape_share(a, t.payload, t.n, t.local_tile);
+  zero_escape_share(t.payload, t.n, t.local_tile, t.payload_tiles);
 }
 
 // Per-byte 0xFF/0x00 masks from bit 3 of each byte of s (byte permute with the
@@ -702,31 +737,55 @@ __device__ __forceinline__ u32x4 decode_run8(u32x2 body, uint32_t cd, const uint
                assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x07030602u))};
 }
 
+// 1024-word chunks per wave of the decode tile kernel (two per wave measured
+// slower on MI355X than one).
+constexpr int kDecodeChunks = 1;
+constexpr int kDecodeTileShift = 12;
+static_assert((kThreads / kWave) * kDecodeChunks * 1024 == (1 << kDecodeTileShift), "decode tile");
+
+template <bool kIds>
 __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = uniform(threadIdx.x >> 6);
-  const TileInfo t = tile_info(a, group_index());
-  const unsigned long long wstart = t.start + (unsigned long long)wave * 1024;
-  if (wstart >= t.end) return;  // whole waves; no barrier in this kernel
+  const PlaneTile t = plane_tile<kDecodeTileShift>(a, group_index());
+  const unsigned int chunk0 = wave * kDecodeChunks;
+  if (chunk0 * 1024 >= t.words) return;  // whole chunks; no barrier in this kernel
   const unsigned int mode = t.payload[0];
   const uint32_t* cbw = reinterpret_cast<const uint32_t*>(a.tables + 512 + t.plane * 16);
   const uint32_t cb[4] = {cbw[0], cbw[1], cbw[2], cbw[3]};
-  const unsigned char* pbody = t.payload + 5 + wstart;
-  const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
-  const u32x2 body_a = load_stream8(pbody + 8 * lane);
-  const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
-  const uint32_t code_a = load_stream4(pcode + 4 * lane);
-  const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
-  uint16_t* dst = a.kv + wave_block_offset(a, t, geo, wstart);
-  const u32x4 out_a = decode_run8(body_a, code_a, cb);
-  const u32x4 out_b = decode_run8(body_b, code_b, cb);
-  // Keeps the payload loads ahead of the mode test below: without this use the
-  // compiler sinks them under the test and the mode byte's round trip comes first.
-  asm volatile("" ::"v"(out_a), "v"(out_b));
+  bool act[kDecodeChunks];
+  u32x4 out_a[kDecodeChunks], out_b[kDecodeChunks];
+  uint16_t* dst[kDecodeChunks];
+#pragma unroll
+  for (int k = 0; k < kDecodeChunks; ++k) {
+    act[k] = (chunk0 + k) * 1024 < t.words;
+    if (!act[k]) continue;
+    const unsigned int in_plane = t.in_plane0 + (chunk0 + k) * 1024;
+    const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
+    const unsigned char* pbody = t.payload + 5 + wstart;
+    const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+    const u32x2 body_a = load_stream8(pbody + 8 * lane);
+    const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
+    const uint32_t code_a = load_stream4(pcode + 4 * lane);
+    const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
+    dst[k] = a.kv + wave_source<kIds>(a, t, geo, in_plane);
+    out_a[k] = decode_run8(body_a, code_a, cb);
+    out_b[k] = decode_run8(body_b, code_b, cb);
+  }
+#pragma unroll
+  for (int k = 0; k < kDecodeChunks; ++k) {
+    // Keeps the payload loads ahead of the mode test below: without this use the
+    // compiler sinks them under the test and the mode byte's round trip comes first.
+    if (act[k]) asm volatile("" ::"v"(out_a[k]), "v"(out_b[k]));
+  }
   // the reference decoder leaves a payload whose byte 0 is not 5 untouched
   if (mode != 5) return;
-  store_stream16(dst + 8 * lane, out_a);
-  store_stream16(dst + 512 + 8 * lane, out_b);
+#pragma unroll
+  for (int k = 0; k < kDecodeChunks; ++k) {
+    if (!act[k]) continue;
+    store_stream16(dst[k] + 8 * lane, out_a[k]);
+    store_stream16(dst[k] + 512 + 8 * lane, out_b[k]);
+  }
 }
 
 // Scans the escapes of one tile from the source words (tiles with more escapes
@@ -789,7 +848,11 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   unsigned long long running = 0;  // escapes in earlier chunks
   for (unsigned int chunk0 = 0; chunk0 < tiles; chunk0 += kFinChunk) {
     const unsigned int m = min((unsigned int)kFinChunk, tiles - chunk0);
-    // thread tid holds the counts of tiles chunk0 + tid * kFinPerThread + k
+    // Thread tid holds the counts of tiles chunk0 + tid * kFinPerThread + k and
+    // places the escapes of the one among them that belongs to this group
+    // (k == grp). Its first staged escapes are loaded along with the counts, so
+    // the common tile (few escapes) needs a single round trip.
+    static_assert(kFinPerThread == kFinGroups, "one tile of each group per thread");
     unsigned int mine[kFinPerThread];
     unsigned int sum = 0;
 #pragma unroll
@@ -798,29 +861,41 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       mine[k] = t < m ? counts[chunk0 + t] : 0;
       sum += mine[k];
     }
+    const unsigned int own = tid * kFinPerThread + grp;  // this thread's tile of the group
+    const unsigned int* st = staged + (unsigned long long)(chunk0 + own) * kStageSlots;
+    unsigned int pre[kFinPreload];
+#pragma unroll
+    for (int q = 0; q < kFinPreload; ++q) pre[q] = own < m ? st[q] : 0;
     unsigned int chunk_total;
     unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
 
-    // staged escapes of this group's tiles go straight to their slots
+    // staged escapes of this group's tile go straight to their slots
+    unsigned int c = 0;
 #pragma unroll
     for (int k = 0; k < kFinPerThread; ++k) {
-      const unsigned int t = tid * kFinPerThread + k;
-      const unsigned int c = mine[k];
-      const unsigned long long base = running + prefix;
-      prefix += c;
-      if (t % kFinGroups != grp || c == 0 || base >= cap) continue;
+      if ((unsigned int)k < grp) prefix += mine[k];
+      if ((unsigned int)k == grp) c = mine[k];
+    }
+    const unsigned long long base = running + prefix;
+    if (c != 0 && base < cap) {
       if (c > (unsigned int)kStageSlots) {
         const unsigned int q = atomicAdd(&s_over_count, 1u);
-        s_over_tile[q] = chunk0 + t;
+        s_over_tile[q] = chunk0 + own;
         s_over_base[q] = (unsigned int)base;
-        continue;
-      }
-      unsigned long long start, end;
-      tile_range(a, d, chunk0 + t, n, start, end);
-      const unsigned int* st = staged + (unsigned long long)(chunk0 + t) * kStageSlots;
-      for (unsigned int q = 0; q < c && base + q < cap; ++q) {
-        const unsigned int v = st[q];
-        put_entry(entries, base + q, (unsigned int)(start + (v >> 8)), v & 0xFF);
+      } else {
+        unsigned long long start, end;
+        tile_range(a, d, chunk0 + own, n, start, end);
+        for (unsigned int q = 0; q < c && base + q < cap; ++q) {
+          unsigned int v = pre[0];
+          if (q < (unsigned int)kFinPreload) {
+#pragma unroll
+            for (int e = 1; e < kFinPreload; ++e)
+              if (q == (unsigned int)e) v = pre[e];
+          } else {
+            v = st[q];
+          }
+          put_entry(entries, base + q, (unsigned int)(start + (v >> 8)), v & 0xFF);
+        }
       }
     }
     __syncthreads();
@@ -939,6 +1014,8 @@ inline unsigned long long align_up(unsigned long long v, unsigned long long a) {
 }
 
 constexpr unsigned int kMinTileShift = kTileShift;
+// The tile kernels use 32-bit in-plane word arithmetic.
+constexpr unsigned long long kTilePlaneLimit = 1ull << 31;
 
 enum class Kernel { kTile, kLanes, kGeneric };
 
@@ -978,6 +1055,14 @@ Plan make_plan(bool geometry_fast, bool tile_ok, bool sequential) {
   return p;
 }
 
+// Decode tiles every payload per plane; the tile kernel's tiles are larger.
+Plan make_decode_plan(bool geometry_fast, bool tile_ok) {
+  Plan p = make_plan(geometry_fast, tile_ok, false);
+  p.per_plane = true;
+  if (p.kernel == Kernel::kTile) p.tile_shift = kDecodeTileShift;
+  return p;
+}
+
 void apply_plan(LaunchArgs& a, const Plan& p) {
   a.tiles_per_plane_mode = p.per_plane ? 1 : 0;
   a.tile_shift = p.tile_shift;
@@ -1001,7 +1086,10 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   }
   switch (p.kernel) {
     case Kernel::kTile:
-      hipLaunchKernelGGL(top16_encode_tile, dim3(a.total_tiles), block, 0, stream, a, g);
+      if (a.ids)
+        hipLaunchKernelGGL(top16_encode_tile<true>, dim3(a.total_tiles), block, 0, stream, a, g);
+      else
+        hipLaunchKernelGGL(top16_encode_tile<false>, dim3(a.total_tiles), block, 0, stream, a, g);
       break;
     case Kernel::kLanes:
       hipLaunchKernelGGL((top16_encode_lanes<true, false>), dim3(a.total_tiles), block, 0, stream,
@@ -1022,7 +1110,10 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   const dim3 block(kThreads);
   switch (p.kernel) {
     case Kernel::kTile:
-      hipLaunchKernelGGL(top16_decode_tile, dim3(a.total_tiles), block, 0, stream, a, g);
+      if (a.ids)
+        hipLaunchKernelGGL(top16_decode_tile<true>, dim3(a.total_tiles), block, 0, stream, a, g);
+      else
+        hipLaunchKernelGGL(top16_decode_tile<false>, dim3(a.total_tiles), block, 0, stream, a, g);
       break;
     case Kernel::kLanes:
       hipLaunchKernelGGL(top16_decode_lanes, dim3(a.total_tiles), block, 0, stream, a, g);
@@ -1148,12 +1239,10 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
   a.p[0].block_count = (unsigned int)block_count;
   const bool geometry_fast = block_words % 16 == 0 && dst_ptr % 16 == 0 && plane_stride % 8 == 0 &&
                              block_stride % 8 == 0 && (count_words >> 1) <= 0xFFFFFFFFULL;
-  const Plan plan = make_plan(geometry_fast,
-                              sections_aligned(src_ptr, count_words) && tables_ptr % 4 == 0 &&
-                                  block_words % 1024 == 0,
-                              false);
+  const Plan plan = make_decode_plan(
+      geometry_fast, sections_aligned(src_ptr, count_words) && tables_ptr % 4 == 0 &&
+                         block_words % 1024 == 0 && (count_words >> 1) < kTilePlaneLimit);
   apply_plan(a, plan);
-  a.tiles_per_plane_mode = 1;  // decode always tiles per plane (the generic path ignores tiles)
   a.total_tiles = host_payload_tiles(count_words, true, plan.tile_shift);
   long long rc = launch_decode(a, make_geom(block_words), plan,
                                reinterpret_cast<hipStream_t>(stream_ptr));
@@ -1317,20 +1406,19 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
       src_offsets == nullptr || encoded_bytes == nullptr || block_offsets == nullptr ||
       payload_count == 0 || block_words == 0 || block_words > 0xFFFFFFFFULL)
     return 0;
-  unsigned long long total = 0;
+  unsigned long long total = 0, max_plane = 0;
   for (unsigned long long r = 0; r < payload_count; ++r) {
     if (block_offsets[r + 1] <= block_offsets[r]) return 0;
     const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
     if (encoded_bytes[r] != encoded_size(n) || (n >> 1) > 0xFFFFFFFFULL) return 0;
     total += 2 * n;
+    max_plane = std::max(max_plane, n >> 1);
   }
   const PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
-  Plan plan = make_plan(
+  const Plan plan = make_decode_plan(
       paged_fast(pg),
       paged_aligned(src_ptr, block_offsets, src_offsets, payload_count, block_words) &&
-          tables_ptr % 4 == 0 && block_words % 1024 == 0,
-      false);
-  plan.per_plane = true;
+          tables_ptr % 4 == 0 && block_words % 1024 == 0 && max_plane < kTilePlaneLimit);
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
