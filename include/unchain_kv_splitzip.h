@@ -146,6 +146,41 @@ long long kvq_splitzip_bf16_decode_top16_paged(
     const unsigned long long* block_offsets, unsigned long long tables_ptr,
     unsigned long long stream_ptr);
 
+/* Workspace bytes that kvq_splitzip_bf16_encode_mode_paged needs for this batch (no
+ * counterpart in the reference). */
+unsigned long long kvq_splitzip_palette_paged_workspace_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count);
+
+/* Gather + palette encode of a batch: bits 6 -> fixed6 (mode 3), bits 5 -> fixed5
+ * (mode 4) (no counterpart in the reference; it replaces index_select +
+ * kvq_splitzip_bf16_encode_mode per request, the connector's Top-16 overflow
+ * fallback, vllm_connector.py:4557-4616). Payload r goes to out + out_offsets[r];
+ * each payload gets its own ascending palette, or byte 0 = 255 alone when its
+ * distinct high bytes exceed the palette. workspace (16-byte aligned) must hold
+ * kvq_splitzip_palette_paged_workspace_bytes() bytes. Returns the sum of the
+ * encoded sizes, or 0 when a precondition fails. */
+long long kvq_splitzip_bf16_encode_mode_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long workspace_ptr,
+    unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits);
+
+/* Palette decode + scatter of a batch (no counterpart in the reference; it replaces
+ * one kvq_splitzip_bf16_decode_fixed6_blocks call per request, and decodes fixed5 on
+ * the GPU where the reference uses torch ops). Payload r (src + src_offsets[r],
+ * encoded_bytes[r] long, which must be the format's exact size) is written into the
+ * blocks of block table r; a payload whose byte 0 is not the format's mode byte is
+ * left unapplied. Returns the total raw bytes. */
+long long kvq_splitzip_bf16_decode_mode_paged(
+    unsigned long long src_ptr, const unsigned long long* src_offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long stream_ptr, int bits);
+
 #ifdef __cplusplus
 }
 #endif

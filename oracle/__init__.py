@@ -71,6 +71,12 @@ def load():
     lib.sz_fixed6_encode.restype = u64
     lib.sz_fixed6_decode.argtypes = [p, u64, p]
     lib.sz_fixed6_decode.restype = ctypes.c_int
+    lib.sz_palette_encoded_size.argtypes = [u64, ctypes.c_int]
+    lib.sz_palette_encoded_size.restype = u64
+    lib.sz_palette_encode.argtypes = [p, u64, ctypes.c_int, p]
+    lib.sz_palette_encode.restype = u64
+    lib.sz_palette_decode.argtypes = [p, u64, ctypes.c_int, p]
+    lib.sz_palette_decode.restype = ctypes.c_int
     lib.sz_top16_encode_paged_batch.argtypes = [
         p, u64, u64, u64, p, p, u64, p, p, p, u64, ctypes.c_int
     ]
@@ -100,6 +106,10 @@ def top16_encoded_size(n: int) -> int:
 
 def fixed6_encoded_size(n: int) -> int:
     return 65 + n + ((n + 3) // 4) * 3
+
+
+def palette_encoded_size(n: int, bits: int) -> int:
+    return fixed6_encoded_size(n) if bits == 6 else 33 + n + ((n + 7) // 8) * 5
 
 
 # ---------------------------------------------------------------------------
@@ -171,6 +181,25 @@ def fixed6_decode(payload: np.ndarray, n: int) -> np.ndarray:
     payload = np.ascontiguousarray(payload, dtype=np.uint8)
     words = np.zeros(n, dtype=np.uint16)
     load().sz_fixed6_decode(_ptr(payload), n, _ptr(words))
+    return words
+
+
+def palette_encode(words: np.ndarray, bits: int) -> np.ndarray | None:
+    """fixed6 (bits 6, mode 3) or fixed5 (bits 5, mode 4) canonical payload."""
+    words = np.ascontiguousarray(words, dtype=np.uint16).reshape(-1)
+    out = np.zeros(palette_encoded_size(words.size, bits), dtype=np.uint8)
+    size = load().sz_palette_encode(_ptr(words), words.size, bits, _ptr(out))
+    return out if size else None
+
+
+def palette_decode(payload: np.ndarray, n: int, bits: int,
+                   initial: np.ndarray | None = None) -> np.ndarray:
+    """Words in payload order; a payload without the format's mode byte leaves the
+    initial words unchanged."""
+    payload = np.ascontiguousarray(payload, dtype=np.uint8)
+    words = (np.zeros(n, dtype=np.uint16) if initial is None
+             else np.array(initial, dtype=np.uint16).reshape(-1).copy())
+    load().sz_palette_decode(_ptr(payload), n, bits, _ptr(words))
     return words
 
 

@@ -207,57 +207,73 @@ SZ_EXPORT void sz_exponent_histogram(const uint16_t* words, uint64_t n, uint64_t
   for (uint64_t i = 0; i < n; ++i) counts[(i >= half ? 256 : 0) + ((words[i] >> 7) & 0xFF)]++;
 }
 
-/* ---- fixed6 (mode 3): kvq_splitzip_cuda.cu:20-82 (encode), :113-144 (decode) ----
- * Payload: [3][64-byte palette of high bytes][n low bytes][codes: 4 x 6 bits per 3
- * bytes, little-endian, first code in the low bits]. More than 64 distinct high
- * bytes: byte 0 = 255 (.cu:59-61). Canonical palette: ascending, zero padded. */
-SZ_EXPORT uint64_t sz_fixed6_encode(const uint16_t* words, uint64_t n, uint8_t* out) {
-  if (n == 0) return 0;
-  uint64_t encoded = sz_fixed6_encoded_size(n);
+/* ---- palette codecs: fixed6 (mode 3) and fixed5 (mode 4) ----
+ * kvq_splitzip_cuda.cu:20-111 (encode), :113-144 (fixed6 decode); the fixed5 decode
+ * follows the connector's torch decoder for mode 4 (vllm_connector.py:5266-5275:
+ * LSB-first 5-bit codes, `_unpack_splitzip_bits` :3345-3404).
+ * Payload: [mode][palette of high bytes: 64 (fixed6) or 32 (fixed5) bytes][n low
+ * bytes][codes: groups of 4 x 6 bits in 3 bytes, or 8 x 5 bits in 5 bytes,
+ * little-endian, first word in the low bits]. More distinct high bytes than
+ * palette entries: byte 0 = 255 and nothing else is written (.cu:58-61, 86-88).
+ * Canonical palette: ascending, zero padded. */
+SZ_EXPORT uint64_t sz_palette_encoded_size(uint64_t n, int bits) {
+  return bits == 6 ? 65 + n + ((n + 3) / 4) * 3 : 33 + n + ((n + 7) / 8) * 5;
+}
+
+SZ_EXPORT uint64_t sz_palette_encode(const uint16_t* words, uint64_t n, int bits, uint8_t* out) {
+  if (n == 0 || (bits != 5 && bits != 6)) return 0;
+  const int limit = bits == 6 ? 64 : 32, group = bits == 6 ? 4 : 8, group_bytes = bits == 6 ? 3 : 5;
+  const uint64_t encoded = sz_palette_encoded_size(n, bits);
   if (encoded >= 2 * n) return 0;
   uint8_t present[256] = {0};
   for (uint64_t i = 0; i < n; ++i) present[words[i] >> 8] = 1;
   int rank[256];
   int distinct = 0;
   for (int h = 0; h < 256; ++h) rank[h] = present[h] ? distinct++ : -1;
-  if (distinct > 64) {
+  if (distinct > limit) {
     out[0] = 255;
     return encoded;
   }
-  out[0] = 3;
-  memset(out + 1, 0, 64);
+  out[0] = (uint8_t)(bits == 6 ? 3 : 4);
+  memset(out + 1, 0, (size_t)limit);
   for (int h = 0; h < 256; ++h)
     if (rank[h] >= 0) out[1 + rank[h]] = (uint8_t)h;
-  uint8_t* low = out + 65;
+  uint8_t* low = out + 1 + limit;
   uint8_t* codes = low + n;
-  for (uint64_t g = 0; g < (n + 3) / 4; ++g) {
-    uint32_t bits = 0;
-    for (int k = 0; k < 4; ++k) {
-      uint64_t i = g * 4 + k;
+  for (uint64_t g = 0; g < (n + group - 1) / group; ++g) {
+    uint64_t packed = 0;
+    for (int k = 0; k < group; ++k) {
+      uint64_t i = g * group + k;
       if (i >= n) break;
       low[i] = (uint8_t)(words[i] & 0xFF);
-      bits |= (uint32_t)(rank[words[i] >> 8] & 0x3F) << (k * 6);
+      packed |= (uint64_t)(rank[words[i] >> 8] & (limit - 1)) << (k * bits);
     }
-    codes[g * 3] = (uint8_t)bits;
-    codes[g * 3 + 1] = (uint8_t)(bits >> 8);
-    codes[g * 3 + 2] = (uint8_t)(bits >> 16);
+    for (int b = 0; b < group_bytes; ++b) codes[g * group_bytes + b] = (uint8_t)(packed >> (8 * b));
   }
   return encoded;
 }
 
-SZ_EXPORT int sz_fixed6_decode(const uint8_t* payload, uint64_t n, uint16_t* words) {
-  if (payload[0] != 3) return 0;
+SZ_EXPORT int sz_palette_decode(const uint8_t* payload, uint64_t n, int bits, uint16_t* words) {
+  const int limit = bits == 6 ? 64 : 32, group = bits == 6 ? 4 : 8, group_bytes = bits == 6 ? 3 : 5;
+  if (payload[0] != (bits == 6 ? 3 : 4)) return 0;
   const uint8_t* palette = payload + 1;
-  const uint8_t* low = payload + 65;
+  const uint8_t* low = payload + 1 + limit;
   const uint8_t* codes = low + n;
   for (uint64_t i = 0; i < n; ++i) {
-    uint64_t g = i / 4;
-    uint32_t packed = (uint32_t)codes[g * 3] | ((uint32_t)codes[g * 3 + 1] << 8) |
-                      ((uint32_t)codes[g * 3 + 2] << 16);
-    uint32_t code = (packed >> ((i % 4) * 6)) & 0x3F;
+    uint64_t g = i / group, packed = 0;
+    for (int b = 0; b < group_bytes; ++b) packed |= (uint64_t)codes[g * group_bytes + b] << (8 * b);
+    uint32_t code = (uint32_t)(packed >> ((i % group) * bits)) & (uint32_t)(limit - 1);
     words[i] = (uint16_t)(((uint16_t)palette[code] << 8) | low[i]);
   }
   return 1;
+}
+
+SZ_EXPORT uint64_t sz_fixed6_encode(const uint16_t* words, uint64_t n, uint8_t* out) {
+  return sz_palette_encode(words, n, 6, out);
+}
+
+SZ_EXPORT int sz_fixed6_decode(const uint8_t* payload, uint64_t n, uint16_t* words) {
+  return sz_palette_decode(payload, n, 6, words);
 }
 
 /* ---- multi-threaded CPU baseline: gather + canonical Top-16 encode of a batch ----

@@ -387,3 +387,33 @@ def test_fixed6_overflow_marks_255():
     assert payload[0] == 255
     ok = oracle.fixed6_encode(np.tile(words[:64], 8))
     assert ok is not None and ok[0] == 3
+
+
+def test_fixed5_matches_bit_unpacking_restatement():
+    """fixed5 (mode 4): 32-entry ascending palette, 8 x 5-bit codes per 5 bytes,
+    LSB first, as the connector's mode-4 torch decoder reads them
+    (src/unchain_kv/vllm_connector.py:5266-5275 with _unpack_splitzip_bits)."""
+    rng = np.random.default_rng(12)
+    n = 1001
+    highs = np.array(sorted(rng.choice(256, 29, replace=False)), np.uint16)
+    words = ((highs[rng.integers(0, highs.size, n)] << 8) | rng.integers(0, 256, n)).astype(np.uint16)
+    payload = oracle.palette_encode(words, 5)
+    assert payload.size == 33 + n + ((n + 7) // 8) * 5 and payload[0] == 4
+    palette = bytes(payload[1:33])
+    assert list(palette[:29]) == [int(h) for h in highs] and not any(palette[29:])
+    low = bytes(payload[33:33 + n])
+    codes = oracle.unpack_bits_py(bytes(payload[33 + n:]), n, 5)
+    rebuilt = np.array([(palette[c] << 8) | low[i] for i, c in enumerate(codes)], np.uint16)
+    assert np.array_equal(rebuilt, words)
+    assert np.array_equal(oracle.palette_decode(payload, n, 5), words)
+    # a fixed5 payload is not a fixed6 payload: the fixed6 decoder leaves it alone
+    assert not oracle.palette_decode(payload, n, 6).any()
+
+
+def test_fixed5_overflow_marks_255_and_fixed6_agrees_with_generic_form():
+    words = np.tile((np.arange(33, dtype=np.uint16) << 8) | 7, 4)
+    assert oracle.palette_encode(words, 5)[0] == 255
+    assert oracle.palette_encode(np.tile((np.arange(32, dtype=np.uint16) << 8) | 7, 4), 5)[0] == 4
+    rng = np.random.default_rng(2)
+    w6 = ((rng.integers(0, 40, 777) << 8) | rng.integers(0, 256, 777)).astype(np.uint16)
+    assert np.array_equal(oracle.palette_encode(w6, 6), oracle.fixed6_encode(w6))

@@ -32,6 +32,19 @@ def fixed5_encoded_size(n: int) -> int:
     return 33 + n + ((n + 7) // 8) * 5
 
 
+def palette_encoded_size(n: int, bits: int) -> int:
+    """fixed6 (bits 6) or fixed5 (bits 5) payload size."""
+    if bits == 6:
+        return fixed6_encoded_size(n)
+    if bits == 5:
+        return fixed5_encoded_size(n)
+    raise ValueError("palette codecs have 5 or 6 bits")
+
+
+def palette_header_bytes(bits: int) -> int:
+    return 65 if bits == 6 else 33
+
+
 def top16_ratio(n: int) -> float:
     return 2 * n / top16_encoded_size(n)
 

@@ -169,6 +169,114 @@ __device__ __forceinline__ unsigned long long word_offset(const LaunchArgs& a,
 }
 
 // ---------------------------------------------------------------------------
+// tile geometry shared by the tile kernels of both codecs
+
+// q = x / d for x, d < 2^32 via m = floor(2^64 / d) + 1 (exact for every 32-bit x).
+struct Divider {
+  unsigned long long m;
+  unsigned int d;
+};
+
+inline Divider make_divider(unsigned int d) {
+  Divider r;
+  r.d = d;
+  r.m = d <= 1 ? 0 : (~0ull / d) + 1;
+  return r;
+}
+
+__device__ __forceinline__ unsigned int div_u32(unsigned int x, unsigned long long m,
+                                                unsigned int d) {
+  return d <= 1 ? x : (unsigned int)__umul64hi((unsigned long long)x, m);
+}
+
+
+struct EncodeGeom {
+  unsigned long long bw_magic;  // divider for block_words
+  unsigned int bw;
+};
+
+
+#ifndef UKV_XCD_REMAP
+#define UKV_XCD_REMAP 1
+#endif
+
+// Index of this workgroup's tile (XCD-aware: each XCD walks a contiguous run).
+__device__ __forceinline__ unsigned int group_index() {
+#if UKV_XCD_REMAP
+  return xcd_remap(blockIdx.x, gridDim.x);
+#else
+  return blockIdx.x;
+#endif
+}
+
+// Scalar (SGPR) copies of wave-uniform values.
+__device__ __forceinline__ unsigned int uniform(unsigned int v) {
+  return __builtin_amdgcn_readfirstlane(v);
+}
+__device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
+  return ((unsigned long long)__builtin_amdgcn_readfirstlane((unsigned int)(v >> 32)) << 32) |
+         __builtin_amdgcn_readfirstlane((unsigned int)v);
+}
+
+// One 4096-word tile of the per-plane tiling that the tile kernels use. In-plane
+// arithmetic is 32-bit (the host only picks these kernels for plane words < 2^31)
+// and free of branches on the launch layout, so the kernel-argument loads of the
+// prologue can be issued together.
+struct PlaneTile {
+  unsigned long long n;   // payload words
+  unsigned char* payload;
+  const long long* ids;   // the payload's block table (when there is one)
+  unsigned int plane;
+  unsigned int in_plane0;  // first word of the tile within its plane
+  unsigned int words;      // words in the tile: a multiple of 1024, at most the tile size
+  unsigned int local_tile;
+  unsigned int payload_tiles;
+  unsigned int payload_index;  // index of the payload within the launch
+};
+
+template <int kShift>
+__device__ __forceinline__ PlaneTile plane_tile(const LaunchArgs& a, unsigned int tile) {
+  constexpr unsigned int kWords = 1u << kShift;
+  PlaneTile t;
+  t.payload_index = find_payload(a, tile);
+  const PayloadDesc d = a.p[t.payload_index];
+  const unsigned int plane_words = d.block_count * (unsigned int)a.block_words;
+  const unsigned int tpp = (plane_words + kWords - 1) >> kShift;
+  t.local_tile = tile - d.tile_begin;
+  t.plane = t.local_tile >= tpp ? 1u : 0u;
+  t.in_plane0 = (t.local_tile - t.plane * tpp) << kShift;
+  t.words = min(kWords, plane_words - t.in_plane0);
+  t.n = 2ull * plane_words;
+  t.payload = a.buf + d.buf_offset;
+  t.ids = a.ids + d.ids_offset;
+  t.payload_tiles = 2 * tpp;
+  return t;
+}
+
+// Wave-uniform element offset in the layer of in-plane word `in_plane` of tile t
+// (block from the payload's block table, or block_start + j without one).
+template <bool kIds>
+__device__ __forceinline__ unsigned long long wave_source(const LaunchArgs& a, const PlaneTile& t,
+                                                          const EncodeGeom& geo,
+                                                          unsigned int in_plane) {
+  const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
+  const unsigned int within = in_plane - j * geo.bw;
+  const unsigned long long blk =
+      kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
+  return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
+}
+
+
+inline EncodeGeom make_geom(unsigned long long block_words) {
+  EncodeGeom g{};
+  const Divider dv = make_divider((unsigned int)(block_words > 1 ? block_words : 1));
+  g.bw = dv.d;
+  g.bw_magic = dv.m;
+  return g;
+}
+
+
+// ---------------------------------------------------------------------------
 // byte-window helpers: c[] holds consecutive little-endian dwords; take 4 (or 2)
 // dwords starting at byte offset off (wave-uniform, 0 <= off < 16 or < 8).
 

@@ -63,6 +63,20 @@ _SIGNATURES = (
         ctypes.c_longlong,
         False,
     ),
+    ("kvq_splitzip_palette_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
+    (
+        "kvq_splitzip_bf16_encode_mode_paged",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64,
+         ctypes.c_int],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_decode_mode_paged",
+        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, ctypes.c_int],
+        ctypes.c_longlong,
+        False,
+    ),
 )
 
 
@@ -389,6 +403,37 @@ class PagedBatch:
     def payload(self, out, r: int):
         return out[self.out_offsets[r]:self.out_offsets[r] + self.encoded_bytes[r]]
 
+    def palette_layout(self, bits: int) -> tuple[list[int], list[int], int]:
+        """(offsets, encoded sizes, buffer bytes) of the batch's fixed6 (bits 6) or
+        fixed5 (bits 5) payloads; each payload's low-byte section starts on a
+        256-byte boundary."""
+        header = codec_format.palette_header_bytes(bits)
+        sizes = [codec_format.palette_encoded_size(n, bits) for n in self.count_words]
+        offsets, end = [], 0
+        for size in sizes:
+            start = -(-(end + header) // 256) * 256 - header
+            offsets.append(start)
+            end = start + size
+        return offsets, sizes, end
+
+    def palette_workspace_bytes(self) -> int:
+        lib = _load()
+        query = getattr(lib, "kvq_splitzip_palette_paged_workspace_bytes", None) if lib else None
+        if query is None:
+            raise RuntimeError(f"splitzip HIP library unavailable: {load_error()}")
+        return int(query(self.block_words, self._block_offsets, self.payload_count))
+
+    def new_palette_buffer(self, bits: int, torch=None):
+        if torch is None:
+            import torch
+        return torch.empty(self.palette_layout(bits)[2], dtype=torch.uint8, device=self.device)
+
+    def new_palette_workspace(self, torch=None):
+        if torch is None:
+            import torch
+        return torch.empty(max(self.palette_workspace_bytes(), 16), dtype=torch.uint8,
+                           device=self.device)
+
 
 def _paged_layout_ok(kv_layer, batch: PagedBatch, torch) -> bool:
     if not _is_cuda(kv_layer) or kv_layer.dtype != torch.bfloat16:
@@ -462,4 +507,68 @@ def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Page
                     int(tables.data_ptr()), int(stream))
     if copied < 0:
         _raise_last(lib, "splitzip top16 paged decode failed")
+    return int(copied) or None
+
+
+# ---------------------------------------------------------------------------
+# batched paged fixed6 / fixed5 (the Top-16 overflow fallback, one launch per layer)
+
+def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6) -> int | None:
+    """Gather + fixed6 (bits 6) or fixed5 (bits 5) encode of every request of
+    ``batch``; payload r goes to ``batch.palette_layout(bits)[0][r]`` of ``out``.
+    Returns the total encoded bytes or ``None`` when the codec declines."""
+    if bits not in {5, 6}:
+        raise ValueError("splitzip bf16 bits must be 5 or 6")
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_mode_paged", None) if lib else None
+    if encode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    offsets, _, _ = batch.palette_layout(bits)
+    offs = (ctypes.c_ulonglong * batch.payload_count)(*offsets)
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                     batch.payload_count, int(out.data_ptr()), offs, int(out.numel()),
+                     int(workspace.data_ptr()), int(workspace.numel()), int(stream), int(bits))
+    if encoded < 0:
+        _raise_last(lib, "splitzip palette paged encode failed")
+    return int(encoded) or None
+
+
+def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: PagedBatch,
+                      bits: int = 6) -> int | None:
+    """Decode fixed6 (bits 6) or fixed5 (bits 5) payload r
+    (``source[src_offsets[r]:][:encoded_bytes[r]]``) and scatter it into
+    ``batch.block_tables[r]``; one launch for every request."""
+    if bits not in {5, 6}:
+        raise ValueError("splitzip bf16 bits must be 5 or 6")
+    lib = _load()
+    decode = getattr(lib, "kvq_splitzip_bf16_decode_mode_paged", None) if lib else None
+    if decode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch) or not batch.unique_blocks:
+        return None
+    if source.dtype != torch.uint8 or not source.is_contiguous() or source.device != kv_layer.device:
+        return None
+    if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
+        return None
+    if any(o + e > source.numel() for o, e in zip(src_offsets, encoded_bytes)):
+        return None
+    offs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, src_offsets))
+    encs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, encoded_bytes))
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
+                    int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                    batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                    int(stream), int(bits))
+    if copied < 0:
+        _raise_last(lib, "splitzip palette paged decode failed")
     return int(copied) or None
