@@ -1,0 +1,144 @@
+"""Codec policy of the connector hooks (no GPU): Top-16 backoff, codec choice,
+environment knobs and restore validation. The backoff cases follow the
+reference's tests/test_vllm_connector.py:2966-3045."""
+
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+from unchainkv_amd import codec_format
+from unchainkv_amd.connector import (BITS_FIXED5, BITS_FIXED6, BITS_TOP16, CodecConfig,
+                                     SplitzipLayerCodec)
+from unchainkv_amd.trace import RecordingTrace
+
+MIB = 1 << 20
+
+
+def codec(**kwargs):
+    trace = RecordingTrace()
+    return SplitzipLayerCodec(CodecConfig(**kwargs), trace=trace), trace
+
+
+def test_backoff_single_flight_and_recovery():
+    c, trace = codec(top16=True, top16_max_cooldown=32)
+    attempt = c._should_try_splitzip_top16(7, MIB)
+    assert attempt == (True, 0, False)
+    c._finish_splitzip_top16_attempt(7, *attempt[1:], True)
+    assert c._splitzip_top16_windows == {7: 1}
+    for expected_window in (2, 4, 8, 16, 32, 32):
+        while c._splitzip_top16_cooldowns[7] > 0:
+            assert not c._should_try_splitzip_top16(7, MIB)[0]
+        with ThreadPoolExecutor(max_workers=8) as pool:
+            attempts = list(pool.map(lambda _: c._should_try_splitzip_top16(7, MIB), range(16)))
+        probes = [a for a in attempts if a[0]]
+        assert len(probes) == 1  # one probe in flight
+        c._finish_splitzip_top16_attempt(7, probes[0][1], probes[0][2], True)
+        assert c._splitzip_top16_windows[7] == expected_window
+    while c._splitzip_top16_cooldowns[7] > 0:
+        c._should_try_splitzip_top16(7, MIB)
+    probe = c._should_try_splitzip_top16(7, MIB)
+    c._finish_splitzip_top16_attempt(7, *probe[1:], False)
+    assert 7 not in c._splitzip_top16_cooldowns and 7 not in c._splitzip_top16_windows
+    assert "splitzip_top16_probe_success" in trace.names()
+    before = dict(c._splitzip_top16_cooldowns)
+    assert not c._should_try_splitzip_top16(7, MIB - 1)[0]
+    assert c._splitzip_top16_cooldowns == before
+
+
+def test_stale_ready_result_cannot_reset_backoff():
+    c, trace = codec(top16=True)
+    first = c._should_try_splitzip_top16(7, MIB)
+    late = c._should_try_splitzip_top16(7, MIB)
+    c._finish_splitzip_top16_attempt(7, *first[1:], True)
+    c._finish_splitzip_top16_attempt(7, *late[1:], False)
+    assert c._splitzip_top16_cooldowns == {7: 1}
+    assert c._splitzip_top16_windows == {7: 1}
+    assert trace.names()[-1] == "splitzip_top16_stale_result"
+
+
+def test_disable_is_sticky_and_epoch_guarded():
+    c, trace = codec(top16=True)
+    ok, epoch, _ = c._should_try_splitzip_top16(3, MIB)
+    c._disable_splitzip_top16(3, epoch + 5)  # stale epoch: ignored
+    assert 3 not in c._splitzip_top16_unavailable_layers
+    c._disable_splitzip_top16(3, epoch)
+    assert 3 in c._splitzip_top16_unavailable_layers
+    assert not c._should_try_splitzip_top16(3, MIB)[0]
+    assert trace.names()[-2:] == ["splitzip_top16_stale_result", "splitzip_top16_unavailable"]
+
+
+def test_cancelled_probe_allows_the_next_probe():
+    c, trace = codec(top16=True)
+    first = c._should_try_splitzip_top16(1, MIB)
+    c._finish_splitzip_top16_attempt(1, *first[1:], True)  # window 1
+    c._should_try_splitzip_top16(1, MIB)  # cooldown 1 -> 0
+    probe = c._should_try_splitzip_top16(1, MIB)
+    assert probe[0] and probe[2]
+    assert not c._should_try_splitzip_top16(1, MIB)[0]  # single flight
+    c._cancel_splitzip_top16_probe(1, probe[1], probe[2])
+    again = c._should_try_splitzip_top16(1, MIB)
+    assert again[0] and again[2] and again[1] == probe[1] + 1
+    assert "splitzip_top16_probe_error" in trace.names()
+
+
+def test_codec_choice_top16_large_fixed6_small_and_fixed5_rules():
+    c, _ = codec(top16=True)
+    assert c._choose_bits(7, MIB)[0] == BITS_TOP16
+    assert c._choose_bits(7, MIB - 2)[0] == BITS_FIXED6
+    c5, _ = codec(fixed5=True, fixed5_layers={1, 3})
+    assert c5._choose_bits(1, 4096)[0] == BITS_FIXED5
+    assert c5._choose_bits(2, 4096)[0] == BITS_FIXED6  # not in the layer list
+    c5._splitzip_fixed6_layers.add(3)                   # downgraded after an overflow
+    assert c5._choose_bits(3, 4096)[0] == BITS_FIXED6
+    both, _ = codec(top16=True, fixed5=True)
+    assert both._choose_bits(0, MIB)[0] == BITS_TOP16
+    assert both._choose_bits(0, 4096)[0] == BITS_FIXED5
+    both._splitzip_top16_unavailable_layers.add(0)
+    # Top-16 requested but unavailable for the layer: fixed6, not fixed5
+    assert both._choose_bits(0, MIB)[0] == BITS_FIXED6
+
+
+def test_config_from_environment():
+    cfg = CodecConfig.from_env({
+        "UNCHAIN_KV_SPLITZIP_TOP16": "1",
+        "UNCHAIN_KV_SPLITZIP_FIXED5": "1",
+        "UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS": "1, 3,5",
+        "UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN": "0",
+    })
+    assert cfg.top16 and cfg.fixed5
+    assert cfg.fixed5_layers == {1, 3, 5}
+    assert cfg.top16_max_cooldown == 1  # clamped to at least 1, as the reference does
+    default = CodecConfig.from_env({})
+    assert not default.top16 and default.top16_max_cooldown == 32 and not default.fixed5_layers
+
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.mark.parametrize("payload,encoded_bytes,raw_bytes", [
+    (b"\xff", 1, 16),             # mode out of range
+    (b"\x03", 79, 16),            # length differs from the metadata
+    (b"\x05" + bytes(4), 5, 16),  # Top-16 size mismatch
+    (b"\x06" + bytes(15), 16, 16),  # raw payload one byte short
+    (b"\x06" + bytes(16), 17, 12),  # raw_bytes disagrees with the blocks
+])
+def test_restore_rejects_bad_payloads_before_any_gpu_work(payload, encoded_bytes, raw_bytes):
+    """tests/test_vllm_connector.py:2679-2721 of the reference: refused payloads
+    never reach the device."""
+    c, _ = codec()
+    kv = torch.zeros((2, 2, 2), dtype=torch.bfloat16)  # CPU tensor: any GPU use would fail
+    got = c.load_kv_layer_batch(0, kv, [([0, 1], payload, {"raw_bytes": raw_bytes,
+                                                          "encoded_bytes": encoded_bytes})])
+    assert got == [(0, 0)]
+
+
+def test_restore_rejects_unsupported_torch_modes_and_bad_blocks():
+    c, trace = codec()
+    kv = torch.zeros((2, 4, 2), dtype=torch.bfloat16)
+    meta = {"raw_bytes": 16, "encoded_bytes": 3}
+    assert c.load_kv_layer_batch(0, kv, [([0, 1], b"\x01\x00\x00", meta)]) == [(0, 0)]
+    assert trace.names() == ["splitzip_mode_unsupported"]
+    raw = {"raw_bytes": 16, "encoded_bytes": 17}
+    assert c.load_kv_layer_batch(0, kv, [([0, 0], b"\x06" + bytes(16), raw)]) == [(0, 0)]
+    assert c.load_kv_layer_batch(0, kv, [([0, 9], b"\x06" + bytes(16), raw)]) == [(0, 0)]
+    assert codec_format.MODE_RAW == 6

@@ -1,0 +1,204 @@
+"""The connector codec hooks on the GPU: save -> ready -> load round trips for
+every codec the policy picks (Top-16, the fixed6 fallback on overflow, raw mode 6
+when fixed6 overflows too, fixed5), with the payload bytes checked against the
+oracle and against the per-request drop-in encoder."""
+
+import numpy as np
+import pytest
+
+import oracle
+from unchainkv_amd import codec_format
+from unchainkv_amd.connector import (BITS_FIXED5, BITS_FIXED6, BITS_RAW, BITS_TOP16,
+                                     CodecConfig, SplitzipLayerCodec)
+from unchainkv_amd.trace import RecordingTrace
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def sz():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU visible")
+    from unchainkv_amd import splitzip_cuda
+
+    assert splitzip_cuda.available(), splitzip_cuda.load_error()
+    return splitzip_cuda
+
+
+def say(*parts):
+    print("[case]", *parts, flush=True)
+
+
+def u16(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+BW = 16384  # Llama-3-8B block: 16 tokens x 8 heads x 128
+
+
+def layer_from_words(words, pool):
+    return torch.from_numpy(words.view(np.int16).copy()).cuda().view(torch.bfloat16).view(
+        2, pool, 16, 8, 128)
+
+
+def words_with_books(rng, books, pool, escape_rate=0.0, distinct_high=None):
+    n = 2 * pool * BW
+    half = n // 2
+    exps = np.empty(n, np.uint16)
+    exps[:half] = np.frombuffer(books[:16], np.uint8)[rng.integers(0, 16, half)]
+    exps[half:] = np.frombuffer(books[16:], np.uint8)[rng.integers(0, 16, n - half)]
+    outside = np.array(sorted(set(range(256)) - set(books)), np.uint16)
+    esc = rng.random(n) < escape_rate
+    exps[esc] = outside[rng.integers(0, outside.size, int(esc.sum()))]
+    words = ((rng.integers(0, 2, n).astype(np.uint16) << 15) | (exps << 7)
+             | rng.integers(0, 128, n).astype(np.uint16))
+    return words.astype(np.uint16)
+
+
+def disjoint_tables(rng, pool, sizes):
+    perm = rng.permutation(pool).tolist()
+    tables, at = [], 0
+    for size in sizes:
+        tables.append(perm[at:at + size])
+        at += size
+    return tables
+
+
+def roundtrip(codec, layer_index, kv, tables, pool):
+    pending = codec.save_kv_layer(layer_index, kv, tables)
+    payloads = codec.ready(pending)
+    target = torch.zeros_like(kv)
+    recv = [[(b + 7) % pool for b in t] for t in tables]  # receiver's own block ids
+    requests = [(rt, bytes(p.view), p.metadata(layer_index, BW)) for rt, p in zip(recv, payloads)]
+    results = codec.load_kv_layer_batch(layer_index, target, requests)
+    torch.cuda.synchronize()
+    src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
+    for t, rt, res in zip(tables, recv, results):
+        assert res == (len(t), 2 * 2 * len(t) * BW)
+        assert np.array_equal(dst[:, rt], src[:, t])
+    return payloads
+
+
+def test_top16_roundtrip_matches_dropin_payload_bytes(sz, codebooks):
+    say("connector top16")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(1)
+    pool = 64
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.001), pool)
+    tables = disjoint_tables(rng, pool, [16, 20, 17])  # >= 1 MiB each: Top-16
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    payloads = roundtrip(codec, 5, kv, tables, pool)
+    assert [p.bits for p in payloads] == [BITS_TOP16] * 3
+    for t, p in zip(tables, payloads):
+        # the per-request drop-in call on the gathered blocks gives the same bytes
+        source = kv[:, t].contiguous()
+        out = torch.empty(source.numel() * 2, dtype=torch.uint8, device="cuda")
+        size = sz.encode_top16(source, out, 5)
+        torch.cuda.synchronize()
+        assert size == p.encoded_bytes
+        assert bytes(out[:size].cpu().numpy()) == bytes(p.view)
+        ref = oracle.top16_encode(u16(source).reshape(-1), oracle.top16_tables(books))
+        assert bytes(ref) == bytes(p.view)
+    assert "codec_encode_submitted" in trace.names()
+
+
+def test_top16_overflow_falls_back_to_fixed6_and_backs_off(sz, codebooks):
+    say("connector overflow -> fixed6")
+    books = codebooks[2 * 32:3 * 32]
+    rng = np.random.default_rng(2)
+    pool = 64
+    words = words_with_books(rng, books, pool, 0.0)
+    kv_host = words.reshape(2, pool, BW)
+    tables = disjoint_tables(rng, pool, [16, 16, 16])
+    # request 1 gets 1.2% escapes: more than the 0.5% capacity
+    outside = np.array(sorted(set(range(256)) - set(books))[:16], np.uint16)
+    for b in tables[1]:
+        hit = rng.random((2, BW)) < 0.012
+        block = kv_host[:, b]
+        block[hit] = (block[hit] & 0x807F) | (outside[rng.integers(0, 16, int(hit.sum()))] << 7)
+        kv_host[:, b] = block
+    kv = layer_from_words(kv_host.reshape(-1), pool)
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    payloads = roundtrip(codec, 2, kv, tables, pool)
+    assert [p.bits for p in payloads] == [BITS_TOP16, BITS_FIXED6, BITS_TOP16]
+    assert payloads[1].fallback and payloads[1].view[0] == codec_format.MODE_FIXED6
+    assert bytes(payloads[1].view) == bytes(oracle.fixed6_encode(kv_host[:, tables[1]].reshape(-1)))
+    assert codec._splitzip_top16_windows == {2: 1}
+    assert "splitzip_top16_overflow" in trace.names()
+    # the next payload of the layer waits out the window, then probes
+    assert codec._choose_bits(2, 1 << 20)[0] == BITS_FIXED6
+
+
+def test_fixed6_overflow_falls_back_to_raw_mode(sz, codebooks):
+    say("connector fixed6 overflow -> raw")
+    rng = np.random.default_rng(3)
+    pool = 8
+    words = rng.integers(0, 1 << 16, 2 * pool * BW).astype(np.uint16)  # every high byte
+    kv = layer_from_words(words, pool)
+    tables = [[0, 1, 2], [5]]
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    payloads = roundtrip(codec, 0, kv, tables, pool)
+    assert [p.bits for p in payloads] == [BITS_RAW, BITS_RAW]
+    assert payloads[0].view[0] == codec_format.MODE_RAW
+    assert payloads[0].encoded_bytes == payloads[0].raw_bytes + 1
+    assert trace.names().count("splitzip_fixed6_overflow") == 2
+
+
+def test_layer_without_codebook_is_unavailable_and_sticks_to_fixed6(sz, codebooks):
+    say("connector layer 40 without codebook")
+    rng = np.random.default_rng(4)
+    pool = 24
+    books = codebooks[:32]
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.0), pool)
+    tables = disjoint_tables(rng, pool, [16])
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    first = roundtrip(codec, 40, kv, tables, pool)
+    assert first[0].bits == BITS_FIXED6 and first[0].fallback
+    assert 40 in codec._splitzip_top16_unavailable_layers
+    second = roundtrip(codec, 40, kv, tables, pool)
+    assert second[0].bits == BITS_FIXED6 and not second[0].fallback
+    # with an explicit codebook the layer uses Top-16
+    with_books = SplitzipLayerCodec(CodecConfig(top16=True), codebooks={40: books})
+    assert roundtrip(with_books, 40, kv, tables, pool)[0].bits == BITS_TOP16
+
+
+def test_small_requests_fixed5_and_its_overflow_downgrade(sz, codebooks):
+    say("connector fixed5")
+    rng = np.random.default_rng(5)
+    pool = 6
+    highs = np.array(sorted(rng.choice(256, 20, replace=False)), np.uint16)
+    words = ((highs[rng.integers(0, 20, 2 * pool * BW)] << 8)
+             | rng.integers(0, 256, 2 * pool * BW)).astype(np.uint16)
+    kv_host = words.reshape(2, pool, BW)
+    kv_host[:, 4] = (np.arange(BW, dtype=np.uint16) % 40) << 8  # 40 distinct: fixed5 overflows
+    kv = layer_from_words(kv_host.reshape(-1), pool)
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, fixed5=True))
+    payloads = roundtrip(codec, 3, kv, [[0], [4]], pool)  # 64 KiB each: below the Top-16 size
+    assert payloads[0].bits == BITS_FIXED5 and payloads[0].view[0] == codec_format.MODE_FIXED5
+    assert payloads[1].bits == BITS_FIXED6 and payloads[1].fallback
+    assert 3 in codec._splitzip_fixed6_layers
+    assert codec._choose_bits(3, 4096)[0] == BITS_FIXED6
+
+
+def test_single_request_load_signature_matches_reference(sz, codebooks):
+    say("connector load_kv_layer")
+    rng = np.random.default_rng(6)
+    pool = 40
+    books = codebooks[:32]
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.002), pool)
+    src, dst = disjoint_tables(rng, pool, [16, 16])
+    codec = SplitzipLayerCodec(CodecConfig(top16=True))
+    payload = codec.ready(codec.save_kv_layer(0, kv, [src]))[0]
+    assert payload.bits == BITS_TOP16
+    target = torch.zeros_like(kv)
+    meta = payload.metadata(0, BW)
+    assert codec.load_kv_layer(target, dst, [bytes(payload.view)], meta) == (16, meta["raw_bytes"])
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(target).reshape(2, pool, BW)[:, dst],
+                          u16(kv).reshape(2, pool, BW)[:, src])
+    assert codec.load_kv_layer(target, dst[:2], [bytes(payload.view)], meta) == (0, 0)

@@ -1,0 +1,514 @@
+"""The codec half of UnchainKV's vLLM connector, on the MI355X codec.
+
+The reference connector (src/unchain_kv/vllm_connector.py) encodes each request's
+KV blocks in its per-layer save hook and restores them in its per-layer load hook.
+This module keeps that codec behaviour and its knobs, batched per layer:
+
+* policy: Top-16 for payloads of at least 1 MiB when enabled, with the per-layer
+  overflow backoff (windows 1, 2, 4 ... up to the cooldown cap, one probe in
+  flight, stale results ignored; :2906-3021); a layer whose Top-16 encode declines
+  is marked unavailable and uses fixed6 from then on (:3111-3118); fixed5 where
+  enabled, downgraded to fixed6 for a layer after it declines or overflows;
+* save (``save_kv_layer``): every request of the layer is encoded by one batched
+  launch per codec (gathering the blocks in the kernel), then copied to pinned host
+  memory on the current stream;
+* ready (``ready``): after the copy, Top-16 (and fixed5) payloads whose byte 0 is
+  255 are re-encoded as fixed6, and fixed6 overflow falls back to raw mode 6
+  (``[6] + raw bytes``) (:4526-4665);
+* load (``load_kv_layer`` / ``load_kv_layer_batch``): the restore validation of
+  ``_copy_splitzip_bf16_native_blocks`` (:5098-5313) and GPU decode + scatter of
+  modes 3, 4 and 5, raw copy of mode 6.
+
+Everything runs on the HIP library; there is no CPU codec path. Modes 0, 1 and 2
+(the reference's torch-op codecs) are not produced and are refused on load.
+Payloads below 1 MiB use fixed6, as the reference does when its codec buffer pool
+is in use. The KV blocks of a saved layer must stay unchanged until ``ready``
+returns: the fallback re-encodes read them again (the reference keeps a gathered
+copy instead).
+"""
+
+from __future__ import annotations
+
+import os
+import threading
+from dataclasses import dataclass, field
+
+from . import codec_format
+from .trace import TraceWriter
+
+TOP16_MIN_BYTES = 1 << 20
+
+
+def _env_int(env, name: str, default: int) -> int:
+    value = env.get(name, "")
+    return int(value) if value not in {None, ""} else default
+
+
+def _env_int_set(env, name: str) -> set[int]:
+    value = env.get(name, "")
+    return {int(item) for item in value.replace(" ", ",").split(",") if item}
+
+
+@dataclass
+class CodecConfig:
+    """Codec knobs of the connector (vllm_connector.py:384-449)."""
+    top16: bool = False                   # UNCHAIN_KV_SPLITZIP_TOP16
+    fixed5: bool = False                  # UNCHAIN_KV_SPLITZIP_FIXED5
+    fixed5_layers: set = field(default_factory=set)  # UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS
+    top16_max_cooldown: int = 32          # UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN
+    native_decode: bool = True            # UNCHAIN_KV_SPLITZIP_NATIVE_DECODE (decode is always GPU)
+
+    @classmethod
+    def from_env(cls, env=None) -> "CodecConfig":
+        env = os.environ if env is None else env
+        return cls(
+            top16=_env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16", 0) > 0,
+            fixed5=_env_int(env, "UNCHAIN_KV_SPLITZIP_FIXED5", 0) > 0,
+            fixed5_layers=_env_int_set(env, "UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS"),
+            top16_max_cooldown=max(1, _env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN", 32)),
+            native_decode=_env_int(env, "UNCHAIN_KV_SPLITZIP_NATIVE_DECODE", 1) > 0,
+        )
+
+
+# bits of a payload as the reference's _SplitzipCudaPayload records them
+BITS_TOP16, BITS_FIXED5, BITS_FIXED6, BITS_RAW = 4, 5, 6, 16
+_MODE_OF_BITS = {BITS_TOP16: codec_format.MODE_TOP16, BITS_FIXED5: codec_format.MODE_FIXED5,
+                 BITS_FIXED6: codec_format.MODE_FIXED6, BITS_RAW: codec_format.MODE_RAW}
+
+
+@dataclass
+class LayerPayload:
+    """One request's payload of a layer (the fields of the reference's
+    ``_SplitzipCudaPayload`` that the transport and the policy use)."""
+    request: int
+    block_ids: list
+    raw_bytes: int
+    bits: int
+    requested_bits: int
+    epoch: int = -1
+    probe: bool = False
+    fallback: bool = False
+    encoded_bytes: int = 0
+    view: memoryview | None = None
+    _group: int = -1
+    _offset: int = 0
+
+    def metadata(self, layer_index: int, block_words: int) -> dict:
+        """Receiver metadata of a compressed-native layer payload."""
+        return {"block_count": len(self.block_ids), "raw_block_size": 2 * 2 * block_words,
+                "raw_bytes": self.raw_bytes, "codec": "splitzip_bf16",
+                "encoded_bytes": self.encoded_bytes, "_layer_index": layer_index}
+
+
+@dataclass
+class PendingLayer:
+    layer_index: int
+    kv_layer: object
+    block_words: int
+    payloads: list
+    groups: list = field(default_factory=list)  # (host tensor, event)
+
+
+class SplitzipLayerCodec:
+    """Per-layer save/load codec hooks of one connector worker."""
+
+    def __init__(self, config: CodecConfig | None = None, *, trace=None, codebooks=None,
+                 lib=None) -> None:
+        config = CodecConfig.from_env() if config is None else config
+        self.config = config
+        self.trace = trace if trace is not None else TraceWriter(None)
+        self.codebooks = {int(k): bytes(v) for k, v in (codebooks or {}).items()}
+        self._sz = lib
+        # policy state, under the reference connector's names
+        self.splitzip_top16 = config.top16
+        self.splitzip_fixed5 = config.fixed5
+        self.splitzip_fixed5_layers = set(config.fixed5_layers)
+        self.splitzip_top16_max_cooldown_payloads = max(1, int(config.top16_max_cooldown))
+        self._splitzip_fixed6_layers: set[int] = set()
+        self._splitzip_top16_unavailable_layers: set[int] = set()
+        self._splitzip_top16_cooldowns: dict[int, int] = {}
+        self._splitzip_top16_windows: dict[int, int] = {}
+        self._splitzip_top16_probe_layers: set[int] = set()
+        self._splitzip_top16_epochs: dict[int, int] = {}
+        self._splitzip_top16_lock = threading.Lock()
+
+    # ------------------------------------------------------------------
+    # library
+
+    def _lib(self):
+        if self._sz is None:
+            from . import splitzip_cuda
+
+            self._sz = splitzip_cuda
+        if not self._sz.available():
+            raise RuntimeError(f"splitzip HIP library unavailable: {self._sz.load_error()}")
+        return self._sz
+
+    def _top16_tables(self, layer_index: int, device):
+        import torch
+
+        sz = self._lib()
+        if layer_index in self.codebooks:
+            return sz.top16_tables_for(self.codebooks[layer_index], device, torch)
+        return sz._top16_tables(layer_index, device, torch)
+
+    def _layer_codebooks(self, layer_index: int) -> bytes | None:
+        if layer_index in self.codebooks:
+            return self.codebooks[layer_index]
+        sz = self._lib()
+        if 0 <= layer_index < len(sz._TOP16_CODEBOOKS) // 32:
+            return sz._TOP16_CODEBOOKS[32 * layer_index:32 * (layer_index + 1)]
+        return None
+
+    # ------------------------------------------------------------------
+    # Top-16 backoff (vllm_connector.py:2906-3021)
+
+    def _should_try_splitzip_top16(self, layer_index: int, raw_bytes: int):
+        if not self.splitzip_top16 or raw_bytes < TOP16_MIN_BYTES:
+            return False, -1, False
+        event, fields = None, {}
+        with self._splitzip_top16_lock:
+            epoch = self._splitzip_top16_epochs.get(layer_index, 0)
+            if layer_index in self._splitzip_top16_unavailable_layers:
+                return False, epoch, False
+            remaining = self._splitzip_top16_cooldowns.get(layer_index)
+            if remaining is None:
+                return True, epoch, False
+            if remaining > 0:
+                remaining -= 1
+                self._splitzip_top16_cooldowns[layer_index] = remaining
+                event = "splitzip_top16_cooldown_skip"
+                fields = {"layer": layer_index, "remaining": remaining,
+                          "window": self._splitzip_top16_windows[layer_index]}
+            elif layer_index in self._splitzip_top16_probe_layers:
+                event = "splitzip_top16_probe_wait_skip"
+                fields = {"layer": layer_index}
+            else:
+                epoch += 1
+                self._splitzip_top16_epochs[layer_index] = epoch
+                self._splitzip_top16_probe_layers.add(layer_index)
+                event = "splitzip_top16_probe"
+                fields = {"layer": layer_index,
+                          "window": self._splitzip_top16_windows[layer_index]}
+        self.trace.event(event, **fields)
+        if event == "splitzip_top16_probe":
+            return True, epoch, True
+        return False, epoch, False
+
+    def _finish_splitzip_top16_attempt(self, layer_index: int, epoch: int, probe: bool,
+                                       overflow: bool) -> None:
+        if layer_index < 0 or epoch < 0:
+            return
+        event, fields = None, {"layer": layer_index}
+        with self._splitzip_top16_lock:
+            if self._splitzip_top16_epochs.get(layer_index, 0) != epoch:
+                event = "splitzip_top16_stale_result"
+            elif overflow:
+                previous = self._splitzip_top16_windows.get(layer_index, 0)
+                window = (min(max(1, previous * 2), self.splitzip_top16_max_cooldown_payloads)
+                          if probe else 1)
+                self._splitzip_top16_windows[layer_index] = window
+                self._splitzip_top16_cooldowns[layer_index] = window
+                self._splitzip_top16_probe_layers.discard(layer_index)
+                self._splitzip_top16_epochs[layer_index] = epoch + 1
+                event = "splitzip_top16_overflow"
+                fields.update(window=window, probe=probe)
+            elif probe:
+                self._splitzip_top16_windows.pop(layer_index, None)
+                self._splitzip_top16_cooldowns.pop(layer_index, None)
+                self._splitzip_top16_probe_layers.discard(layer_index)
+                self._splitzip_top16_epochs[layer_index] = epoch + 1
+                event = "splitzip_top16_probe_success"
+        if event is not None:
+            self.trace.event(event, **fields)
+
+    def _disable_splitzip_top16(self, layer_index: int, epoch: int) -> None:
+        if layer_index < 0 or epoch < 0:
+            return
+        disabled = False
+        with self._splitzip_top16_lock:
+            if self._splitzip_top16_epochs.get(layer_index, 0) == epoch:
+                self._splitzip_top16_unavailable_layers.add(layer_index)
+                self._splitzip_top16_cooldowns.pop(layer_index, None)
+                self._splitzip_top16_windows.pop(layer_index, None)
+                self._splitzip_top16_probe_layers.discard(layer_index)
+                self._splitzip_top16_epochs[layer_index] = epoch + 1
+                disabled = True
+        self.trace.event("splitzip_top16_unavailable" if disabled else "splitzip_top16_stale_result",
+                         layer=layer_index)
+
+    def _cancel_splitzip_top16_probe(self, layer_index: int, epoch: int, probe: bool) -> None:
+        if not probe:
+            return
+        with self._splitzip_top16_lock:
+            if self._splitzip_top16_epochs.get(layer_index, 0) != epoch:
+                return
+            self._splitzip_top16_probe_layers.discard(layer_index)
+        self.trace.event("splitzip_top16_probe_error", layer=layer_index)
+
+    def _choose_bits(self, layer_index: int, raw_bytes: int):
+        """Codec choice of _splitzip_bf16_native_blocks (vllm_connector.py:3078-3094)."""
+        top16_requested = self.splitzip_top16 and raw_bytes >= TOP16_MIN_BYTES
+        try_top16, epoch, probe = self._should_try_splitzip_top16(layer_index, raw_bytes)
+        if try_top16:
+            bits = BITS_TOP16
+        elif top16_requested:
+            bits = BITS_FIXED6
+        elif (self.splitzip_fixed5 and layer_index not in self._splitzip_fixed6_layers
+              and (not self.splitzip_fixed5_layers or layer_index in self.splitzip_fixed5_layers)):
+            bits = BITS_FIXED5
+        else:
+            bits = BITS_FIXED6
+        return bits, epoch, probe
+
+    # ------------------------------------------------------------------
+    # save
+
+    @staticmethod
+    def _layer_geometry(kv_layer, torch):
+        if kv_layer.dim() < 3 or kv_layer.shape[0] != 2 or kv_layer.dtype != torch.bfloat16:
+            raise ValueError("a KV layer is a bf16 (2, num_blocks, ...) paged cache")
+        return kv_layer[0, 0].numel()
+
+    def _encode_group(self, kind: int, kv_layer, members: list, block_words: int, layer_index: int):
+        """Batched encode of `members` with codec `kind`; returns (device buffer,
+        offsets, sizes) or None when the library declines."""
+        sz = self._lib()
+        batch = sz.PagedBatch([p.block_ids for p in members], block_words, kv_layer.device)
+        if kind == BITS_TOP16:
+            tables = self._top16_tables(layer_index, kv_layer.device)
+            if tables is None:
+                return None
+            out = batch.new_payload_buffer()
+            got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(), tables=tables)
+            return (out, batch.out_offsets, batch.encoded_bytes) if got else None
+        offsets, sizes, _ = batch.palette_layout(kind)
+        out = batch.new_palette_buffer(kind)
+        got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind)
+        return (out, offsets, sizes) if got else None
+
+    @staticmethod
+    def _stage(pending: PendingLayer, device_buffer, torch) -> int:
+        """Asynchronous copy of a payload buffer into pinned host memory."""
+        host = torch.empty(device_buffer.numel(), dtype=torch.uint8, pin_memory=True)
+        host.copy_(device_buffer, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(device_buffer.device))
+        pending.groups.append((host, event, device_buffer))
+        return len(pending.groups) - 1
+
+    def save_kv_layer(self, layer_index: int, kv_layer, block_tables) -> PendingLayer:
+        """Encode every request's blocks of one layer (the save hook's codec step) and
+        start the copies to host. ``ready`` returns the payloads."""
+        import torch
+
+        block_words = self._layer_geometry(kv_layer, torch)
+        payloads = []
+        for r, ids in enumerate(block_tables):
+            ids = [int(b) for b in ids]
+            if not ids:
+                raise ValueError("every request needs at least one block")
+            raw = 2 * len(ids) * block_words * 2
+            bits, epoch, probe = self._choose_bits(layer_index, raw)
+            payloads.append(LayerPayload(r, ids, raw, bits, bits, epoch, probe))
+        pending = PendingLayer(layer_index, kv_layer, block_words, payloads)
+
+        top = [p for p in payloads if p.bits == BITS_TOP16]
+        if top:
+            try:
+                result = self._encode_group(BITS_TOP16, kv_layer, top, block_words, layer_index)
+            except Exception:
+                for p in top:
+                    self._cancel_splitzip_top16_probe(layer_index, p.epoch, p.probe)
+                raise
+            if result is None:
+                for p in top:
+                    self._disable_splitzip_top16(layer_index, p.epoch)
+                    p.bits, p.fallback = BITS_FIXED6, True
+                self.trace.event("splitzip_top16_fallback", layer=layer_index)
+            else:
+                self._assign(pending, top, result, torch)
+        five = [p for p in payloads if p.bits == BITS_FIXED5]
+        if five:
+            result = self._encode_group(BITS_FIXED5, kv_layer, five, block_words, layer_index)
+            if result is None:
+                self._splitzip_fixed6_layers.add(layer_index)
+                for p in five:
+                    p.bits, p.fallback = BITS_FIXED6, True
+                self.trace.event("splitzip_fixed5_overflow", layer=layer_index)
+            else:
+                self._assign(pending, five, result, torch)
+        six = [p for p in payloads if p.bits == BITS_FIXED6]
+        if six:
+            result = self._encode_group(BITS_FIXED6, kv_layer, six, block_words, layer_index)
+            if result is None:
+                for p in six:
+                    p.bits = BITS_RAW
+            else:
+                self._assign(pending, six, result, torch)
+        self.trace.event("codec_encode_submitted", layer=layer_index, requests=len(payloads),
+                         raw_bytes=sum(p.raw_bytes for p in payloads))
+        return pending
+
+    def _assign(self, pending, members, result, torch) -> None:
+        out, offsets, sizes = result
+        group = self._stage(pending, out, torch)
+        for p, off, size in zip(members, offsets, sizes):
+            p._group, p._offset, p.encoded_bytes = group, int(off), int(size)
+
+    # ------------------------------------------------------------------
+    # ready: overflow fallback chain (vllm_connector.py:4526-4665)
+
+    def ready(self, pending: PendingLayer) -> list:
+        import torch
+
+        for host, event, _ in pending.groups:
+            event.synchronize()
+        layer = pending.layer_index
+        for p in pending.payloads:
+            if p._group >= 0:
+                host = pending.groups[p._group][0]
+                p.view = memoryview(host.numpy())[p._offset:p._offset + p.encoded_bytes]
+        for p in pending.payloads:
+            if p.bits == BITS_TOP16:
+                self._finish_splitzip_top16_attempt(layer, p.epoch, p.probe,
+                                                    p.view[0] == codec_format.MODE_OVERFLOW)
+        overflowed = [p for p in pending.payloads
+                      if p.view is not None and p.view[0] == codec_format.MODE_OVERFLOW
+                      and p.bits in {BITS_TOP16, BITS_FIXED5}]
+        if any(p.bits == BITS_FIXED5 for p in overflowed):
+            self._splitzip_fixed6_layers.add(layer)
+            self.trace.event("splitzip_fixed5_overflow", layer=layer)
+        if overflowed:
+            result = self._encode_group(BITS_FIXED6, pending.kv_layer, overflowed,
+                                        pending.block_words, layer)
+            if result is not None:
+                out, offsets, sizes = result
+                host = out.cpu()
+                for p, off, size in zip(overflowed, offsets, sizes):
+                    p.view = memoryview(host.numpy())[off:off + size]
+                    p.encoded_bytes = int(size)
+            for p in overflowed:
+                p.bits, p.fallback = BITS_FIXED6, True
+        for p in pending.payloads:
+            if p.bits == BITS_RAW or (p.view is not None and p.view[0] == codec_format.MODE_OVERFLOW):
+                ids = torch.as_tensor(p.block_ids, dtype=torch.long, device=pending.kv_layer.device)
+                raw = pending.kv_layer.index_select(1, ids).contiguous().view(torch.int16).cpu()
+                payload = bytearray(p.raw_bytes + 1)
+                payload[0] = codec_format.MODE_RAW
+                payload[1:] = memoryview(raw.numpy()).cast("B")
+                p.view, p.bits, p.encoded_bytes = memoryview(payload), BITS_RAW, len(payload)
+                self.trace.event("splitzip_fixed6_overflow", layer=layer)
+        self.trace.event("splitzip_payload_ready", layer=layer,
+                         raw_bytes=sum(p.raw_bytes for p in pending.payloads),
+                         encoded_bytes=sum(p.encoded_bytes for p in pending.payloads))
+        return pending.payloads
+
+    # ------------------------------------------------------------------
+    # load: restore validation and dispatch (vllm_connector.py:5098-5313)
+
+    @staticmethod
+    def _validate(kv_layer, block_ids, payload, metadata, torch):
+        """(mode, raw_bytes, view) for a payload the restore accepts, else None."""
+        if kv_layer.dim() < 3 or kv_layer.shape[0] != 2 or not block_ids:
+            return None
+        if len(set(block_ids)) != len(block_ids) or any(
+                b < 0 or b >= kv_layer.shape[1] for b in block_ids):
+            return None
+        first = kv_layer[:, block_ids[0]]
+        raw_bytes = int(metadata.get("raw_bytes", 0))
+        n = raw_bytes // 2
+        encoded_bytes = int(metadata.get("encoded_bytes", 0))
+        expected = len(block_ids) * first.numel() * first.element_size()
+        if (kv_layer.dtype != torch.bfloat16 or raw_bytes <= 0 or raw_bytes % 2
+                or raw_bytes != expected):
+            return None
+        view = memoryview(payload).cast("B")
+        if encoded_bytes < 1 or len(view) != encoded_bytes:
+            return None
+        mode = int(view[0])
+        if mode not in range(7):
+            return None
+        if mode == codec_format.MODE_FIXED6 and encoded_bytes != codec_format.fixed6_encoded_size(n):
+            return None
+        if mode == codec_format.MODE_FIXED5 and encoded_bytes != codec_format.fixed5_encoded_size(n):
+            return None
+        if mode == codec_format.MODE_TOP16 and encoded_bytes != codec_format.top16_encoded_size(n):
+            return None
+        if mode == codec_format.MODE_RAW and encoded_bytes != raw_bytes + 1:
+            return None
+        return mode, raw_bytes, view
+
+    def load_kv_layer(self, kv_layer, block_ids, payloads, metadata) -> tuple[int, int]:
+        """Restore one request's layer payload into its blocks; (blocks, bytes) or
+        (0, 0) when the payload is refused."""
+        if len(payloads) != 1:
+            return 0, 0
+        return self.load_kv_layer_batch(int(metadata.get("_layer_index", -1)), kv_layer,
+                                        [(block_ids, payloads[0], metadata)])[0]
+
+    def load_kv_layer_batch(self, layer_index: int, kv_layer, requests) -> list:
+        """Restore every request of a layer: ``requests`` holds (block_ids, payload
+        bytes, metadata). Payloads are copied to the GPU in one transfer and decoded
+        with one launch per payload mode. Returns (blocks, bytes) per request."""
+        import torch
+
+        sz = self._lib()
+        results = [(0, 0)] * len(requests)
+        groups: dict[int, list] = {}
+        for k, (block_ids, payload, metadata) in enumerate(requests):
+            block_ids = [int(b) for b in block_ids]
+            checked = self._validate(kv_layer, block_ids, payload, metadata, torch)
+            if checked is None:
+                continue
+            mode, raw_bytes, view = checked
+            if mode not in {codec_format.MODE_FIXED6, codec_format.MODE_FIXED5,
+                            codec_format.MODE_TOP16, codec_format.MODE_RAW}:
+                self.trace.event("splitzip_mode_unsupported", mode=mode)
+                continue
+            groups.setdefault(mode, []).append((k, block_ids, raw_bytes, view))
+        if not groups:
+            return results
+        block_words = kv_layer[0, 0].numel()
+        # one pinned staging buffer, each payload placed where the decode kernels
+        # find its sections aligned
+        header = {codec_format.MODE_TOP16: 5, codec_format.MODE_FIXED6: 65,
+                  codec_format.MODE_FIXED5: 33, codec_format.MODE_RAW: 1}
+        layout, end = [], 0
+        for mode, members in groups.items():
+            for member in members:
+                start = -(-(end + header[mode]) // 256) * 256 - header[mode]
+                layout.append((mode, member, start))
+                end = start + len(member[3])
+        host = torch.empty(max(end, 1), dtype=torch.uint8, pin_memory=True)
+        host_view = memoryview(host.numpy())
+        for mode, member, start in layout:
+            host_view[start:start + len(member[3])] = member[3]
+        device = host.to(kv_layer.device, non_blocking=True)
+        for mode, members in groups.items():
+            starts = [start for m, _, start in layout if m == mode]
+            batch = sz.PagedBatch([m[1] for m in members], block_words, kv_layer.device)
+            sizes = [len(m[3]) for m in members]
+            if mode == codec_format.MODE_TOP16:
+                books = self._layer_codebooks(layer_index)
+                if books is None:
+                    continue
+                copied = sz.decode_top16_paged(device, starts, sizes, kv_layer, batch,
+                                               codebooks=books)
+            elif mode == codec_format.MODE_RAW:
+                copied = 0
+                for (k, ids, raw_bytes, _), start in zip(members, starts):
+                    words = device[start + 1:start + 1 + raw_bytes].view(torch.bfloat16)
+                    source = words.reshape((2, len(ids)) + tuple(kv_layer.shape[2:]))
+                    index = torch.as_tensor(ids, dtype=torch.long, device=kv_layer.device)
+                    kv_layer.index_copy_(1, index, source)
+                    copied += raw_bytes
+            else:
+                bits = 6 if mode == codec_format.MODE_FIXED6 else 5
+                copied = sz.decode_bf16_paged(device, starts, sizes, kv_layer, batch, bits=bits)
+            if copied:
+                for k, ids, raw_bytes, _ in members:
+                    results[k] = (len(ids), raw_bytes)
+                self.trace.event("splitzip_native_decode", blocks=sum(len(m[1]) for m in members),
+                                 bytes=int(copied), mode=mode)
+        return results
