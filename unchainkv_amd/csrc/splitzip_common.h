@@ -24,9 +24,9 @@ static_assert((1 << kTileShift) == kTileWords, "tile size");
 // vector memory instruction of a wave covers 64 consecutive chunks.
 constexpr int kChunkWords = 8;
 
-// Escapes staged per tile by the encode kernel; tiles with more are re-scanned
-// by the finalize kernel.
-constexpr int kStageSlots = 32;
+// Escapes staged per tile by the encode kernel (1.6% of a 4096-word tile); tiles
+// with more are re-scanned by the finalize kernel.
+constexpr int kStageSlots = 64;
 // Payload descriptors passed by value in the kernel arguments.
 constexpr int kMaxPayloads = 64;
 
@@ -35,6 +35,7 @@ struct PayloadDesc {
   unsigned long long ids_offset;  // first block id of this payload inside `ids`
   unsigned int block_count;       // blocks per plane
   unsigned int tile_begin;        // first tile of this payload within the launch
+  unsigned int slot_group_begin;  // first escape-patch workgroup of this payload
 };
 
 // One launch covers up to kMaxPayloads payloads of one paged layer (or one
@@ -110,12 +111,28 @@ __device__ __forceinline__ unsigned int xcd_remap(unsigned int wg, unsigned int 
   return xcd * q + min(xcd, rem) + local;
 }
 
+// Payload of a (wave-uniform) tile. Equal-size payloads: one division. Otherwise
+// lane k reads payload k's first tile (kMaxPayloads == wave size) and a ballot
+// counts the payloads that start at or before the tile: one round trip instead of
+// a chain of dependent loads. Every lane of the wave must be active.
+static_assert(kMaxPayloads == 64, "one payload descriptor per lane");
 __device__ __forceinline__ unsigned int find_payload(const LaunchArgs& a, unsigned int tile) {
   if (a.uniform_tiles) return tile / a.uniform_tiles;
-  unsigned int r = 0;
-  for (unsigned int k = 1; k < a.payload_count; ++k)
-    if (a.p[k].tile_begin <= tile) r = k;
-  return r;
+  if (a.payload_count <= 1) return 0;
+  const unsigned int lane = __lane_id();
+  const unsigned int begin = lane < a.payload_count ? a.p[lane].tile_begin : 0xFFFFFFFFu;
+  const unsigned long long starts = __ballot(begin <= tile);
+  return __builtin_amdgcn_readfirstlane((unsigned int)__popcll(starts) - 1u);
+}
+
+// Same search over the escape-patch workgroups of each payload.
+__device__ __forceinline__ unsigned int find_slot_payload(const LaunchArgs& a, unsigned int group) {
+  if (a.payload_count <= 1) return 0;
+  const unsigned int lane = __lane_id();
+  const unsigned int begin =
+      lane < a.payload_count ? a.p[lane].slot_group_begin : 0xFFFFFFFFu;
+  const unsigned long long starts = __ballot(begin <= group);
+  return __builtin_amdgcn_readfirstlane((unsigned int)__popcll(starts) - 1u);
 }
 
 __device__ __forceinline__ unsigned long long payload_words(const LaunchArgs& a,

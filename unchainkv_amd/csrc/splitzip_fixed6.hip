@@ -136,10 +136,28 @@ __global__ __launch_bounds__(kThreads) void palette_reduce(LaunchArgs a, unsigne
   const unsigned long long count = groups ? groups : payload_tiles(a, n);
   if (tid < 8) s_mask[tid] = 0;
   __syncthreads();
-  unsigned int part = 0;
-  for (unsigned long long s = tid >> 3; s < count; s += kThreads / 8)
-    part |= masks[(first + s) * 8 + (tid & 7)];
-  if (part) atomicOr(&s_mask[tid & 7], part);
+  // thread tid ORs whole 32-byte masks of slots tid, tid + 256, ... (loads of four
+  // slots are issued together)
+  u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+  const u32x4* m4 = reinterpret_cast<const u32x4*>(masks + first * 8);
+  for (unsigned long long s = tid; s < count; s += 4 * kThreads) {
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const unsigned long long slot = s + (unsigned long long)k * kThreads;
+      a[k] = slot < count ? m4[2 * slot] : u32x4{0, 0, 0, 0};
+      b[k] = slot < count ? m4[2 * slot + 1] : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo |= a[k];
+      hi |= b[k];
+    }
+  }
+  const unsigned int part[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (part[k]) atomicOr(&s_mask[k], part[k]);
   __syncthreads();
   PaletteInfo& out = info[r];
   unsigned int distinct = 0;

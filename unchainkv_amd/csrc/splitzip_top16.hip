@@ -646,55 +646,36 @@ __device__ __forceinline__ u32x4 decode_run8(u32x2 body, uint32_t cd, const uint
                assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x07030602u))};
 }
 
-// 1024-word chunks per wave of the decode tile kernel (two per wave measured
-// slower on MI355X than one).
-constexpr int kDecodeChunks = 1;
-constexpr int kDecodeTileShift = 12;
-static_assert((kThreads / kWave) * kDecodeChunks * 1024 == (1 << kDecodeTileShift), "decode tile");
-
 template <bool kIds>
 __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = uniform(threadIdx.x >> 6);
-  const PlaneTile t = plane_tile<kDecodeTileShift>(a, group_index());
-  const unsigned int chunk0 = wave * kDecodeChunks;
-  if (chunk0 * 1024 >= t.words) return;  // whole chunks; no barrier in this kernel
+  const PlaneTile t = plane_tile<kTileShift>(a, group_index());
+  const unsigned int in_plane = t.in_plane0 + wave * 1024;
+  const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
+  if (wave * 1024 >= t.words) return;  // whole waves; no barrier in this kernel
   const unsigned int mode = t.payload[0];
   const uint32_t* cbw = reinterpret_cast<const uint32_t*>(a.tables + 512 + t.plane * 16);
   const uint32_t cb[4] = {cbw[0], cbw[1], cbw[2], cbw[3]};
-  bool act[kDecodeChunks];
-  u32x4 out_a[kDecodeChunks], out_b[kDecodeChunks];
-  uint16_t* dst[kDecodeChunks];
-#pragma unroll
-  for (int k = 0; k < kDecodeChunks; ++k) {
-    act[k] = (chunk0 + k) * 1024 < t.words;
-    if (!act[k]) continue;
-    const unsigned int in_plane = t.in_plane0 + (chunk0 + k) * 1024;
-    const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
-    const unsigned char* pbody = t.payload + 5 + wstart;
-    const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
-    const u32x2 body_a = load_stream8(pbody + 8 * lane);
-    const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
-    const uint32_t code_a = load_stream4(pcode + 4 * lane);
-    const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
-    dst[k] = a.kv + wave_source<kIds>(a, t, geo, in_plane);
-    out_a[k] = decode_run8(body_a, code_a, cb);
-    out_b[k] = decode_run8(body_b, code_b, cb);
-  }
-#pragma unroll
-  for (int k = 0; k < kDecodeChunks; ++k) {
-    // Keeps the payload loads ahead of the mode test below: without this use the
-    // compiler sinks them under the test and the mode byte's round trip comes first.
-    if (act[k]) asm volatile("" ::"v"(out_a[k]), "v"(out_b[k]));
-  }
+  const unsigned char* pbody = t.payload + 5 + wstart;
+  const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+  const u32x2 body_a = load_stream8(pbody + 8 * lane);
+  const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
+  const uint32_t code_a = load_stream4(pcode + 4 * lane);
+  const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
+  // The block-id load and the destination address come after the payload loads
+  // are issued, so the two round trips overlap.
+  __builtin_amdgcn_sched_barrier(0);
+  uint16_t* dst = a.kv + wave_source<kIds>(a, t, geo, in_plane);
+  const u32x4 out_a = decode_run8(body_a, code_a, cb);
+  const u32x4 out_b = decode_run8(body_b, code_b, cb);
+  // Keeps the payload loads ahead of the mode test below: without this use the
+  // compiler sinks them under the test and the mode byte's round trip comes first.
+  asm volatile("" ::"v"(out_a), "v"(out_b));
   // the reference decoder leaves a payload whose byte 0 is not 5 untouched
   if (mode != 5) return;
-#pragma unroll
-  for (int k = 0; k < kDecodeChunks; ++k) {
-    if (!act[k]) continue;
-    store_stream16(dst[k] + 8 * lane, out_a[k]);
-    store_stream16(dst[k] + 512 + 8 * lane, out_b[k]);
-  }
+  store_stream16(dst + 8 * lane, out_a);
+  store_stream16(dst + 512 + 8 * lane, out_b);
 }
 
 // Scans the escapes of one tile from the source words (tiles with more escapes
@@ -888,13 +869,12 @@ __global__ __launch_bounds__(kThreads) void top16_decode_generic(LaunchArgs a) {
 // min(count, cap) with position < n, the word gets the escape's exponent bits.
 // The decode kernel wrote sign and mantissa from the body byte, so the patched word
 // is rebuilt from that byte and stored (no read of the destination). One thread
-// per escape slot: grid = payload_count x slot_groups.
-__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a,
-                                                                unsigned int slot_groups) {
-  const unsigned int r = blockIdx.x / slot_groups;
-  const unsigned long long s =
-      (unsigned long long)(blockIdx.x % slot_groups) * kThreads + threadIdx.x;
+// per escape slot; payload r owns workgroups [slot_group_begin, + ceil(cap_r/256)).
+__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
+  const unsigned int r = find_slot_payload(a, blockIdx.x);
   const PayloadDesc d = a.p[r];
+  const unsigned long long s =
+      (unsigned long long)(blockIdx.x - d.slot_group_begin) * kThreads + threadIdx.x;
   const unsigned long long n = payload_words(a, d);
   const unsigned long long cap = escape_capacity(n);
   if (s >= cap) return;
@@ -964,11 +944,10 @@ Plan make_plan(bool geometry_fast, bool tile_ok, bool sequential) {
   return p;
 }
 
-// Decode tiles every payload per plane; the tile kernel's tiles are larger.
+// Decode tiles every payload per plane.
 Plan make_decode_plan(bool geometry_fast, bool tile_ok) {
   Plan p = make_plan(geometry_fast, tile_ok, false);
   p.per_plane = true;
-  if (p.kernel == Kernel::kTile) p.tile_shift = kDecodeTileShift;
   return p;
 }
 
@@ -1039,15 +1018,14 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     }
   }
   if (long long rc = check_launch("top16_decode")) return rc;
-  unsigned long long max_cap = 0;
+  unsigned long long groups = 0;
   for (unsigned int r = 0; r < a.payload_count; ++r) {
     const unsigned long long n =
         a.linear_words ? a.linear_words : 2ull * a.p[r].block_count * a.block_words;
-    max_cap = std::max(max_cap, escape_capacity(n));
+    a.p[r].slot_group_begin = (unsigned int)groups;
+    groups += (escape_capacity(n) + kThreads - 1) / kThreads;
   }
-  const unsigned int slot_groups = (unsigned int)((max_cap + kThreads - 1) / kThreads);
-  hipLaunchKernelGGL(top16_patch_escapes, dim3(a.payload_count * slot_groups), block, 0, stream,
-                     a, slot_groups);
+  hipLaunchKernelGGL(top16_patch_escapes, dim3((unsigned int)groups), block, 0, stream, a);
   return check_launch("top16_patch_escapes");
 }
 

@@ -373,6 +373,13 @@ class PagedBatch:
         self._encoded = (ctypes.c_ulonglong * len(self.encoded_bytes))(*self.encoded_bytes)
         self.max_block = max(flat)
         self.unique_blocks = len(set(flat)) == len(flat)
+        self._palette = {}
+
+    def _c_array(self, values, own, own_array):
+        """ctypes u64 array of `values` (the batch's own array when it is the same list)."""
+        if values is own:
+            return own_array
+        return (ctypes.c_ulonglong * self.payload_count)(*map(int, values))
 
     @property
     def total_raw_bytes(self) -> int:
@@ -407,14 +414,19 @@ class PagedBatch:
         """(offsets, encoded sizes, buffer bytes) of the batch's fixed6 (bits 6) or
         fixed5 (bits 5) payloads; each payload's low-byte section starts on a
         256-byte boundary."""
-        header = codec_format.palette_header_bytes(bits)
-        sizes = [codec_format.palette_encoded_size(n, bits) for n in self.count_words]
-        offsets, end = [], 0
-        for size in sizes:
-            start = -(-(end + header) // 256) * 256 - header
-            offsets.append(start)
-            end = start + size
-        return offsets, sizes, end
+        cached = self._palette.get(bits)
+        if cached is None:
+            header = codec_format.palette_header_bytes(bits)
+            sizes = [codec_format.palette_encoded_size(n, bits) for n in self.count_words]
+            offsets, end = [], 0
+            for size in sizes:
+                start = -(-(end + header) // 256) * 256 - header
+                offsets.append(start)
+                end = start + size
+            cached = (offsets, sizes, end, (ctypes.c_ulonglong * len(offsets))(*offsets),
+                      (ctypes.c_ulonglong * len(sizes))(*sizes))
+            self._palette[bits] = cached
+        return cached[0], cached[1], cached[2]
 
     def palette_workspace_bytes(self) -> int:
         lib = _load()
@@ -438,10 +450,20 @@ class PagedBatch:
 def _paged_layout_ok(kv_layer, batch: PagedBatch, torch) -> bool:
     if not _is_cuda(kv_layer) or kv_layer.dtype != torch.bfloat16:
         return False
-    if kv_layer.dim() < 3 or kv_layer.shape[0] != 2 or not kv_layer.is_contiguous():
+    shape = kv_layer.shape
+    if len(shape) < 3 or shape[0] != 2 or not kv_layer.is_contiguous():
         return False
-    block_words = kv_layer[0, 0].numel()
-    return block_words == batch.block_words and batch.max_block < kv_layer.shape[1]
+    block_words = 1
+    for extent in shape[2:]:
+        block_words *= extent
+    return block_words == batch.block_words and batch.max_block < shape[1]
+
+
+def _payloads_fit(source, src_offsets, encoded_bytes, batch: PagedBatch) -> bool:
+    if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
+        return False
+    size = source.numel()
+    return all(o + e <= size for o, e in zip(src_offsets, encoded_bytes))
 
 
 def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index: int = -1, *,
@@ -490,16 +512,14 @@ def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Page
         return None
     if source.dtype != torch.uint8 or not source.is_contiguous() or source.device != kv_layer.device:
         return None
-    if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
-        return None
-    if any(o + e > source.numel() for o, e in zip(src_offsets, encoded_bytes)):
+    if not _payloads_fit(source, src_offsets, encoded_bytes, batch):
         return None
     if tables is None:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
     if tables is None:
         return None
-    offs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, src_offsets))
-    encs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, encoded_bytes))
+    offs = batch._c_array(src_offsets, batch.out_offsets, batch._out_offsets)
+    encs = batch._c_array(encoded_bytes, batch.encoded_bytes, batch._encoded)
     stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
     copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
                     int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
@@ -529,8 +549,8 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
         return None
     if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
         return None
-    offsets, _, _ = batch.palette_layout(bits)
-    offs = (ctypes.c_ulonglong * batch.payload_count)(*offsets)
+    batch.palette_layout(bits)
+    offs = batch._palette[bits][3]
     stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
@@ -558,12 +578,14 @@ def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Paged
         return None
     if source.dtype != torch.uint8 or not source.is_contiguous() or source.device != kv_layer.device:
         return None
-    if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
+    if not _payloads_fit(source, src_offsets, encoded_bytes, batch):
         return None
-    if any(o + e > source.numel() for o, e in zip(src_offsets, encoded_bytes)):
-        return None
-    offs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, src_offsets))
-    encs = (ctypes.c_ulonglong * batch.payload_count)(*map(int, encoded_bytes))
+    layout = batch._palette.get(bits)
+    if layout is not None and src_offsets is layout[0] and encoded_bytes is layout[1]:
+        offs, encs = layout[3], layout[4]
+    else:
+        offs = batch._c_array(src_offsets, None, None)
+        encs = batch._c_array(encoded_bytes, None, None)
     stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
     copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
                     int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
