@@ -181,6 +181,39 @@ long long kvq_splitzip_bf16_decode_mode_paged(
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long stream_ptr, int bits);
 
+/* ------------------------------------------------------------------------------
+ * Fused Top-16 decode + decode attention (no counterpart in the reference, whose
+ * consumer decodes each payload into the paged KV cache and then runs attention;
+ * scripts/bench_codec_attention.py times that pairing).
+ *
+ * One query token per sequence. Sequence r's KV is the Top-16 payload (mode 5) at
+ * payloads + payload_offsets[r] of its block table in token order: span_r =
+ * ceil(context_tokens[r] / block_tokens) * block_tokens tokens, its K plane then
+ * its V plane, words ordered [token][kv head][dim] (the batched encoder's payload
+ * of the table, block = (block_tokens, kv heads, head_dim)); attention covers the
+ * first context_tokens[r] tokens. q and out are bf16 [batch][q_heads][head_dim]
+ * device arrays; tables_ptr is the layer's 544-byte table. Requires head_dim 128,
+ * q_heads = 4 * kv_heads (GQA groups of 4), escapes in ascending order (this
+ * library's encoder), body sections 16-byte aligned ((payloads + offset + 5) % 16
+ * == 0) and 2 * span_r * kv_heads * 128 < 2^32. payload_offsets and context_tokens
+ * are HOST arrays of batch entries.
+ * A payload whose byte 0 is not 5, or whose escapes are found out of order, gives
+ * NaN outputs for its heads. Returns the bytes of out, or 0 when a precondition
+ * fails.
+ * ---------------------------------------------------------------------------- */
+
+/* Workspace bytes kvq_splitzip_top16_decode_attention needs (split partials). */
+unsigned long long kvq_splitzip_top16_decode_attention_workspace_bytes(
+    unsigned long long batch, unsigned long long kv_heads, unsigned long long max_ctx);
+
+long long kvq_splitzip_top16_decode_attention(
+    unsigned long long q_ptr, unsigned long long out_ptr, unsigned long long payloads_ptr,
+    const unsigned long long* payload_offsets, const unsigned long long* context_tokens,
+    unsigned long long block_tokens, unsigned long long batch, unsigned long long q_heads,
+    unsigned long long kv_heads, unsigned long long head_dim, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes, float scale,
+    unsigned long long stream_ptr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -64,6 +64,14 @@ _SIGNATURES = (
         False,
     ),
     ("kvq_splitzip_palette_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
+    ("kvq_splitzip_top16_decode_attention_workspace_bytes", [_U64] * 3, _U64, False),
+    (
+        "kvq_splitzip_top16_decode_attention",
+        [_U64, _U64, _U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64, _U64,
+         ctypes.c_float, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
     (
         "kvq_splitzip_bf16_encode_mode_paged",
         [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64,
@@ -594,3 +602,61 @@ def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Paged
     if copied < 0:
         _raise_last(lib, "splitzip palette paged decode failed")
     return int(copied) or None
+
+
+# ---------------------------------------------------------------------------
+# fused Top-16 decode + decode attention
+
+def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_heads: int,
+                           layer_index: int = -1, *, block_tokens: int = 16,
+                           codebooks: bytes | None = None, tables=None,
+                           scale: float | None = None, out=None, workspace=None):
+    """Attention of one query token per sequence over Top-16 packed KV, decoded
+    in LDS (no bf16 KV is written). ``q`` is (batch, q_heads, 128) bf16 with
+    q_heads = 4 * kv_heads; sequence r's payload starts at ``payload_offsets[r]``
+    of the uint8 tensor ``payloads`` and is the encoder's payload of its block
+    table in token order (ceil(context_tokens[r] / block_tokens) whole blocks),
+    words ordered [token][kv head][dim] for the K plane, then the V plane; the
+    first ``context_tokens[r]`` tokens are attended. Returns the (batch, q_heads,
+    128) bf16 output, or ``None`` when the kernel declines."""
+    lib = _load()
+    attend = getattr(lib, "kvq_splitzip_top16_decode_attention", None) if lib else None
+    if attend is None:
+        return None
+    import torch
+
+    if not _is_cuda(q) or q.dtype != torch.bfloat16 or not q.is_contiguous() or q.dim() != 3:
+        return None
+    if payloads.dtype != torch.uint8 or not payloads.is_contiguous() or payloads.device != q.device:
+        return None
+    batch, q_heads, head_dim = q.shape
+    if len(payload_offsets) != batch or len(context_tokens) != batch:
+        return None
+    if block_tokens <= 0:
+        return None
+    for off, ctx in zip(payload_offsets, context_tokens):
+        span = -(-int(ctx) // block_tokens) * block_tokens
+        n = 2 * span * kv_heads * head_dim
+        if int(off) < 0 or int(off) + codec_format.top16_encoded_size(n) > payloads.numel():
+            return None
+    if tables is None:
+        tables = _resolve_tables(layer_index, codebooks, q.device, torch)
+    if tables is None:
+        return None
+    if scale is None:
+        scale = head_dim ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    max_ctx = max(int(c) for c in context_tokens)
+    need = int(lib.kvq_splitzip_top16_decode_attention_workspace_bytes(batch, kv_heads, max_ctx))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
+    offs = (ctypes.c_ulonglong * batch)(*map(int, payload_offsets))
+    ctxs = (ctypes.c_ulonglong * batch)(*map(int, context_tokens))
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    got = attend(int(q.data_ptr()), int(out.data_ptr()), int(payloads.data_ptr()), offs, ctxs,
+                 int(block_tokens), batch, q_heads, kv_heads, head_dim, int(tables.data_ptr()),
+                 int(workspace.data_ptr()), int(workspace.numel()), float(scale), int(stream))
+    if got < 0:
+        _raise_last(lib, "splitzip top16 decode attention failed")
+    return out if got else None
