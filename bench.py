@@ -15,10 +15,14 @@ Workloads (seeded synthetic bf16 KV: K = N(0,1) x per-channel scale log-uniform 
   re-encoded as fixed6; the decode is then fixed6 decode + scatter.
 * ``llama3-70b-tp8-mixed``: one GPU's share of Llama-3-70B under TP=8 (80 layers,
   1 KV head, 128); 64 requests of log-uniform 128 .. 32768 tokens.
+* ``llama3-8b-decode-attention``: fused Top-16 decode + decode attention, Llama-3-8B
+  GQA (32 query heads, 8 KV heads, 128), 32 sequences x 8192 tokens per layer, KV
+  held only as Top-16 payloads (~0.1% escapes: 0.1% outliers injected), Q = N(0, 1)
+  bf16. One step = one decode-attention call per layer over 32 layers.
 
-One step = for every layer, gather + encode every request into packed payloads
-(one batched launch per codec and layer), then decode + scatter every payload into
-a receiver cache through an independent random block table.
+One codec step = for every layer, gather + encode every request into packed
+payloads (one batched launch per codec and layer), then decode + scatter every
+payload into a receiver cache through an independent random block table.
 
 The JSON line reports raw bf16 bytes through the round trip per second as
 ``value``, the encode and decode rates separately, the HBM roofline fraction of
@@ -42,7 +46,8 @@ HBM_PEAK_GBPS = 8000.0
 CALIBRATION_BYTES = 256 << 20
 METRIC = "codec encode/decode GB/s of raw bf16 KV (% HBM peak) + compression ratio"
 WORKLOADS = ["llama3-8b-paged", "llama32-1b-contiguous", "llama3-8b-outliers",
-             "llama3-70b-tp8-mixed"]
+             "llama3-70b-tp8-mixed", "llama3-8b-decode-attention"]
+ATTN_BATCH, ATTN_CONTEXT, ATTN_OUTLIERS = 32, 8192, 0.001
 
 
 def parse_args():
@@ -275,6 +280,270 @@ def cpu_baseline(torch, w, layers: int):
 
 
 # ---------------------------------------------------------------------------
+# fused decode attention workload
+
+def build_attention(torch, sz, workloads, seed: int):
+    """32 layers of Llama-3-8B KV for 32 sequences x 8192 tokens, kept only as
+    Top-16 payloads (the raw cache of a layer is freed after its encode)."""
+    shape = workloads.LLAMA3_8B
+    blocks = ATTN_CONTEXT // shape.block_size
+    pool = ATTN_BATCH * blocks
+    tables = workloads.random_block_tables(torch, pool, [blocks] * ATTN_BATCH, seed=seed)
+    device = torch.device("cuda", 0)
+    batch = sz.PagedBatch(tables, shape.block_words, device)
+    ws = batch.new_workspace()
+    w = {"shape": shape, "batch": batch, "device": device, "layers": shape.layers,
+         "payloads": [], "tables": [], "books": [], "q": [], "out": []}
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    q_heads = 4 * shape.kv_heads
+    for layer in range(shape.layers):
+        kv = workloads.make_kv_layer(torch, shape, pool, seed=seed, layer=layer, device=device,
+                                     outlier_rate=ATTN_OUTLIERS)
+        book = workloads.fit_codebook(torch, kv, tables)
+        tab = sz.top16_tables_for(book, device, torch)
+        payload = batch.new_payload_buffer()
+        if sz.encode_top16_paged(kv, batch, payload, ws, tables=tab) != batch.total_encoded_bytes:
+            raise RuntimeError(f"layer {layer}: encode declined")
+        if layer in (0, shape.layers - 1):
+            back = torch.zeros_like(kv)
+            sz.decode_top16_paged(payload, batch.out_offsets, batch.encoded_bytes, back, batch,
+                                  tables=tab)
+            if not torch.equal(back.view(torch.int16), kv.view(torch.int16)):
+                raise RuntimeError(f"layer {layer}: Top-16 round trip differs")
+            del back
+        del kv
+        w["payloads"].append(payload)
+        w["tables"].append(tab)
+        w["books"].append(book)
+        w["q"].append(torch.randn((ATTN_BATCH, q_heads, shape.head_dim), generator=g,
+                                  device=device).to(torch.bfloat16))
+        w["out"].append(torch.empty((ATTN_BATCH, q_heads, shape.head_dim), dtype=torch.bfloat16,
+                                    device=device))
+    need = sz.decode_attention_workspace_bytes(ATTN_BATCH, shape.kv_heads, ATTN_CONTEXT)
+    w["attn_ws"] = torch.empty(need, dtype=torch.uint8, device=device)
+    return w
+
+
+def attend_layer(sz, w, layer):
+    got = sz.decode_attention_top16(w["q"][layer], w["payloads"][layer], w["batch"].out_offsets,
+                                    [ATTN_CONTEXT] * ATTN_BATCH, w["shape"].kv_heads,
+                                    tables=w["tables"][layer], out=w["out"][layer],
+                                    workspace=w["attn_ws"])
+    if got is None:
+        raise RuntimeError(f"layer {layer}: decode attention declined")
+
+
+def attention_reference(torch, sz, w, layer):
+    """Decode-then-attend on the GPU: the codec's decoder restores the bf16 KV, then
+    float32 attention (contiguous operands)."""
+    shape, batch = w["shape"], w["batch"]
+    hkv, d = shape.kv_heads, shape.head_dim
+    blocks = ATTN_CONTEXT // shape.block_size
+    kv = torch.zeros((2, ATTN_BATCH * blocks, shape.block_size, hkv, d), dtype=torch.bfloat16,
+                     device=w["device"])
+    sz.decode_top16_paged(w["payloads"][layer], batch.out_offsets, batch.encoded_bytes, kv, batch,
+                          tables=w["tables"][layer])
+    ids = torch.tensor([b for t in batch.block_tables for b in t], device=w["device"])
+    k = kv[0].index_select(0, ids).reshape(ATTN_BATCH, ATTN_CONTEXT, hkv, d).float()
+    v = kv[1].index_select(0, ids).reshape(ATTN_BATCH, ATTN_CONTEXT, hkv, d).float()
+    del kv
+    qf = w["q"][layer].float().reshape(ATTN_BATCH, hkv, 4, d)
+    s = torch.matmul(qf, k.permute(0, 2, 3, 1).contiguous()) / d ** 0.5
+    p = torch.softmax(s, dim=-1)
+    out = torch.matmul(p, v.permute(0, 2, 1, 3).contiguous())
+    return out.reshape(ATTN_BATCH, 4 * hkv, d)
+
+
+def verify_attention(torch, sz, w, layer):
+    ref = attention_reference(torch, sz, w, layer)
+    got = w["out"][layer].float()
+    err = (got - ref).abs().amax(dim=-1) / ref.abs().amax(dim=-1).clamp_min(1e-6)
+    worst = float(err.max())
+    if not worst <= 1e-2:
+        raise RuntimeError(f"layer {layer}: fused attention off by {worst:.3g} relative")
+    return worst
+
+
+def attention_escapes(torch, w):
+    batch, total = w["batch"], 0
+    for layer in range(w["layers"]):
+        host = w["payloads"][layer].cpu()
+        for off in batch.out_offsets:
+            head = bytes(host[off:off + 5].tolist())
+            if head[0] != 5:
+                raise RuntimeError(f"layer {layer}: a payload overflowed its escape capacity")
+            total += int.from_bytes(head[1:5], "little")
+    return total
+
+
+def cpu_attention_baseline(torch, w, ref_layer_out):
+    """The oracle's C decoder (one payload per thread) then numpy float32 attention,
+    over every sequence of layer 0, on this host's cores; checked against the GPU."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    import oracle
+
+    shape, batch = w["shape"], w["batch"]
+    hkv, d = shape.kv_heads, shape.head_dim
+    threads = oracle.default_threads()
+    host = w["payloads"][0].cpu().numpy()
+    tab = oracle.top16_tables(w["books"][0])
+    q = w["q"][0].float().cpu().numpy()
+    n = 2 * ATTN_CONTEXT * hkv * d
+
+    def one(r):
+        off = batch.out_offsets[r]
+        words = oracle.top16_decode(host[off:off + batch.encoded_bytes[r]], n, tab)
+        kv = (words.astype(np.uint32) << 16).view(np.float32).reshape(2, ATTN_CONTEXT, hkv, d)
+        k = kv[0].transpose(1, 0, 2)                       # (h, t, d)
+        v = kv[1].transpose(1, 0, 2)
+        qg = q[r].reshape(hkv, 4, d)
+        sc = np.matmul(k, qg.transpose(0, 2, 1)) / np.sqrt(d)   # (h, t, 4)
+        sc = np.exp(sc - sc.max(axis=1, keepdims=True))
+        p = sc / sc.sum(axis=1, keepdims=True)
+        return np.matmul(p.transpose(0, 2, 1), v).reshape(4 * hkv, d)
+
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as pool:
+        outs = list(pool.map(one, range(ATTN_BATCH)))
+    elapsed = time.perf_counter() - t0
+    got = np.stack(outs)
+    ref = ref_layer_out.float().cpu().numpy()
+    rel = np.abs(got - ref).max(axis=-1) / np.maximum(np.abs(ref).max(axis=-1), 1e-6)
+    if not rel.max() <= 1e-2:
+        raise RuntimeError("CPU decode-then-attend disagrees with the GPU output")
+    raw = 2 * n * ATTN_BATCH
+    return {
+        "value": round(raw / elapsed / 1e9, 3),
+        "unit": "GB/s raw bf16 KV attended (decode-then-attend)",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"layer 0 of {w['layers']}: {ATTN_BATCH} sequences x {ATTN_CONTEXT} tokens "
+                  f"({raw / 2**30:.2f} GiB raw bf16)",
+    }
+
+
+def run_attention(args, torch, sz, workloads) -> int:
+    w = build_attention(torch, sz, workloads, args.seed)
+    layers, batch, shape = w["layers"], w["batch"], w["shape"]
+    stream = torch.cuda.current_stream(w["device"])
+
+    def step():
+        for layer in range(layers):
+            attend_layer(sz, w, layer)
+
+    if args.profile_steps:
+        for _ in range(args.profile_steps):
+            step()
+        torch.cuda.synchronize()
+        verify_attention(torch, sz, w, 0)
+        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload}))
+        return 0
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    worst = max(verify_attention(torch, sz, w, layer) for layer in (0, layers - 1))
+
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(end) / args.steps
+    call_ms = ms_per_step / layers
+
+    # the decode half of decode-then-attend, for comparison: the codec's decoder
+    # writing one layer's bf16 KV (1 GiB) per call
+    receiver = torch.empty((2, ATTN_BATCH * ATTN_CONTEXT // shape.block_size, shape.block_size,
+                            shape.kv_heads, shape.head_dim), dtype=torch.bfloat16,
+                           device=w["device"])
+    for layer in range(2):
+        sz.decode_top16_paged(w["payloads"][layer], batch.out_offsets, batch.encoded_bytes,
+                              receiver, batch, tables=w["tables"][layer])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for layer in range(layers):
+        sz.decode_top16_paged(w["payloads"][layer], batch.out_offsets, batch.encoded_bytes,
+                              receiver, batch, tables=w["tables"][layer])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    decode_only_ms = e0.elapsed_time(e1) / layers
+    del receiver
+
+    escapes = attention_escapes(torch, w) / layers
+    from unchainkv_amd import codec_format
+
+    cap_bytes = sum(5 * codec_format.top16_escape_capacity(n) for n in batch.count_words)
+    used_payload = batch.total_encoded_bytes - cap_bytes + 5 * escapes
+    q_heads = 4 * shape.kv_heads
+    partial = w["attn_ws"].numel()  # the split partials (m, l, acc[128]) in float32
+    qo = 2 * ATTN_BATCH * q_heads * shape.head_dim * 2
+    # algorithmic HBM bytes per call: packed K and V (used escape entries only), Q
+    # and out, the split partials written and read back once
+    b_call = used_payload + qo + 2 * partial
+    achieved = b_call / (call_ms * 1e-3) / 1e9
+    raw_layer = batch.total_raw_bytes
+    flops = 2 * 2 * ATTN_BATCH * q_heads * ATTN_CONTEXT * shape.head_dim
+    result = {
+        "metric": METRIC,
+        "value": round(raw_layer * layers / (ms_per_step * 1e-3) / 1e9, 2),
+        "unit": "GB/s raw bf16 KV attended (fused Top-16 decode + decode attention)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 MFMA, f32 softmax/accumulate (codec: u16 bit patterns)",
+        "data": (f"synthetic seeded (seed {args.seed}); K=N(0,1)*logU[0.1,10] per channel, "
+                 f"V=N(0,0.5), {ATTN_OUTLIERS:.1%} outliers +-logU[1e2,1e4]; Q=N(0,1) bf16"),
+        "config": {
+            "workload": args.workload,
+            "layers": layers,
+            "batch": ATTN_BATCH,
+            "context": ATTN_CONTEXT,
+            "q_heads": q_heads,
+            "kv_heads": shape.kv_heads,
+            "head_dim": shape.head_dim,
+            "block_size": shape.block_size,
+            "raw_bytes_per_step": raw_layer * layers,
+        },
+        "ms_per_layer_call": round(call_ms, 5),
+        "context_splits": partial // (ATTN_BATCH * shape.kv_heads * 4 * (shape.head_dim + 2) * 4),
+        "escape_fraction": round(escapes / (raw_layer / 2), 6),
+        "compression_ratio": round(raw_layer / used_payload, 5),
+        "max_rel_error_vs_decode_then_attend": round(worst, 6),
+        "decode_only_ms_per_layer": round(decode_only_ms, 5),
+        "mfma_TFLOPs": round(flops / (call_ms * 1e-3) / 1e12, 2),
+        "roofline": {
+            "kernel": "top16_attention_split+top16_attention_combine",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_call": int(b_call),
+            "ms_per_call": round(call_ms, 5),
+        },
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_attention_baseline(torch, w, w["out"][0])
+    print(json.dumps(result))
+    return 0
+
+
+# ---------------------------------------------------------------------------
 # main
 
 def main() -> int:
@@ -291,6 +560,8 @@ def main() -> int:
 
     if not sz.available():
         raise RuntimeError(f"HIP codec library not loaded: {sz.load_error()}")
+    if args.workload == "llama3-8b-decode-attention":
+        return run_attention(args, torch, sz, workloads)
     w = build_workload(torch, sz, workloads, args.workload, args.seed)
     layers = w["layers"]
     stream = torch.cuda.current_stream(w["device"])

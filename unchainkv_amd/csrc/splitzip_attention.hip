@@ -4,24 +4,34 @@
 // The KV of each sequence is one Top-16 payload (mode 5) of its K plane then its V
 // plane, words ordered [token][kv head][dim] (what the batched encoder produces for
 // a sequence's block table in token order). The kernel never materialises bf16 KV
-// in HBM: it reads the packed body and code bytes once, decodes 64-token chunks
-// into LDS, patches the chunk's escapes there, and runs QK^T and PV on the MFMA
-// units (v_mfma_f32_16x16x32_bf16) with an online softmax.
+// in HBM: it reads the packed body and code bytes once, decodes 16-token steps into
+// LDS, patches the step's escapes there, and runs QK^T and PV on the MFMA units
+// with an online softmax.
 //
-// Work split: one workgroup per (context split, kv head, sequence); wave w owns
-// tokens 16w .. 16w+15 of a chunk for QK and output dims 32w .. 32w+31 for PV. The
-// GQA group (4 query heads per kv head) fills rows 0..3 of the 16-row MFMA A tile.
-// A second kernel merges the splits (flash-decoding) and writes bf16.
+// Work split (flash-decoding): one workgroup per (context split, kv head, sequence);
+// its 4 waves take 4 consecutive token ranges of the split and run independently
+// (wave-private LDS, no workgroup barrier until the final merge). Per 16-token
+// step, lane l decodes token l%16, dims 32*(l/16) .. +31 of K and V:
+//   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16 with K as the A operand (rows =
+//     tokens) and the GQA group's 4 query heads as B columns; the dims are taken in
+//     the order lane-group-major so the A operand is the lane's own row of sK;
+//   * the result leaves lane l with tokens 4*(l/16)+j of head l%16, which is
+//     exactly the A operand (P) of v_mfma_f32_16x16x16_bf16 for O = P V, whose B
+//     operand (4 tokens of one dim) is read from the transposed V in LDS.
+// The 4 waves' softmax states are merged in LDS; a second kernel merges the splits
+// and writes bf16.
 //
 // Escapes: the kernel needs the escape list in ascending position order (what the
-// encoder of this library writes). Each workgroup finds its first escape with a
-// 64-way search and then walks the list with its chunks; a decrease between
-// neighbouring entries it reads, or a payload whose byte 0 is not 5, makes its
-// output NaN rather than silently wrong.
+// encoder of this library writes). Each wave finds its first K and V escape with a
+// 64-way search and then walks the list with its steps, one 64-entry window per
+// plane prefetched a step ahead. An entry found below the current step or a
+// decrease between neighbouring entries, or a payload whose byte 0 is not 5, makes
+// the sequence's output NaN rather than silently wrong.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "splitzip_common.h"
 
@@ -29,16 +39,22 @@ namespace unchainkv {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kHeadDim = 128;
-constexpr int kGroup = 4;                  // query heads per kv head
-constexpr int kChunk = 64;                 // tokens per inner step
-constexpr int kKStride = kHeadDim + 8;     // bf16 per row of sK (bank spread)
-constexpr int kVtStride = kChunk + 8;      // bf16 per row of the transposed V
-constexpr int kPStride = kChunk + 8;       // bf16 per row of P
-constexpr int kMaxSeqs = 64;               // sequences per launch (kernel arguments)
-constexpr int kPartial = kHeadDim + 2;     // m, l, acc[128] per (split, query head)
+constexpr int kGroup = 4;                   // query heads per kv head
+constexpr int kStep = 16;                   // tokens per wave step
+constexpr int kKStride = kHeadDim + 8;      // u16 per row of sK (bank spread, 16 B aligned)
+constexpr int kVtStride = kStep + 4;        // u16 per row of the transposed V (8 B aligned)
+// transposed V: row = dim, 16 tokens; each 32-dim part starts 16 u16 further so the
+// four parts' rows of one write land on different banks
+constexpr int kVtWords = kHeadDim * kVtStride + 3 * 16 + 16;
+constexpr int kWaveLds = kStep * kKStride + kVtWords;   // u16 per wave
+constexpr int kMaxSeqs = 64;                // sequences per launch (kernel arguments)
+constexpr int kPartial = kHeadDim + 2;      // m, l, acc[128] per (split, query head)
+constexpr int kMaxSplits = 64;
+static_assert(4 * kGroup * kPartial * 4 <= 4 * kWaveLds * 2, "merge area fits the wave LDS");
 
 struct AttnArgs {
   const uint16_t* q;             // [batch][q_heads][128] bf16
@@ -46,8 +62,8 @@ struct AttnArgs {
   const unsigned char* payloads;
   const unsigned char* tables;   // 544 B; K codebook at +512, V at +528
   float* partial;                // [batch][kv_heads][splits][kGroup][kPartial]
-  unsigned int batch, q_heads, kv_heads, splits, tokens_per_split;
-  float scale_log2;              // log2(e) / sqrt(head_dim)
+  unsigned int batch, q_heads, kv_heads, splits, tokens_per_wave;
+  float scale_log2;              // scale * log2(e)
   unsigned long long offset[kMaxSeqs];  // payload byte offset of each sequence
   unsigned int ctx[kMaxSeqs];           // context tokens of each sequence
   unsigned int span[kMaxSeqs];          // tokens the payload holds (whole blocks, >= ctx)
@@ -57,31 +73,25 @@ __device__ __forceinline__ unsigned int bf16_bits(float v) {
   return __builtin_bit_cast(unsigned short, (__bf16)v);  // round to nearest even
 }
 
-// Exponents of four 4-bit codes (one per byte of s) from a 16-byte codebook.
-__device__ __forceinline__ uint32_t lookup4(uint32_t s, const uint32_t (&cb)[4]) {
-  const uint32_t s7 = s & 0x07070707u;
-  const uint32_t lo = __builtin_amdgcn_perm(cb[1], cb[0], s7);
-  const uint32_t hi = __builtin_amdgcn_perm(cb[3], cb[2], s7);
-  const uint32_t mask = __builtin_amdgcn_perm(s << 12, s << 4, 0x090B080Au);
-  return (hi & mask) | (lo & ~mask);
+// Decode table of one plane in LDS: entry x (a byte of two 4-bit codes, even word
+// in the low nibble) = (cb[x & 15] << 7) | (cb[x >> 4] << 23), i.e. both words'
+// exponents already in place inside a dword of two bf16 words.
+__device__ __forceinline__ uint32_t table_entry(const unsigned char* cb, unsigned int x) {
+  return ((uint32_t)cb[x & 15] << 7) | ((uint32_t)cb[x >> 4] << 23);
 }
 
-__device__ __forceinline__ uint32_t pair_of(uint32_t x) {
-  const uint32_t y = (x & 0x007F007Fu) | ((x >> 1) & ~0x007F007Fu);
-  return ((x << 8) & 0x80008000u) | (y & ~0x80008000u);
-}
-
-// 8 words (4 dwords of bf16 pairs) from 8 body bytes and 4 code bytes.
+// 8 words (4 dwords of bf16 pairs) from 8 body bytes (mantissa | sign << 7) and 4
+// code bytes: exponent bits 7..14 of each word come from the table, bits 0..6 and
+// 15 from the body byte repeated into both bytes of its word.
 __device__ __forceinline__ void decode8(uint32_t b0, uint32_t b1, uint32_t cd,
-                                        const uint32_t (&cb)[4], uint32_t* o) {
-  const uint32_t u = cd >> 4;
-  const uint32_t sa = __builtin_amdgcn_perm(u, cd, 0x05010400u) & 0x0F0F0F0Fu;
-  const uint32_t sb = __builtin_amdgcn_perm(u, cd, 0x07030602u) & 0x0F0F0F0Fu;
-  const uint32_t ea = lookup4(sa, cb), eb = lookup4(sb, cb);
-  o[0] = pair_of(__builtin_amdgcn_perm(ea, b0, 0x05010400u));
-  o[1] = pair_of(__builtin_amdgcn_perm(ea, b0, 0x07030602u));
-  o[2] = pair_of(__builtin_amdgcn_perm(eb, b1, 0x05010400u));
-  o[3] = pair_of(__builtin_amdgcn_perm(eb, b1, 0x07030602u));
+                                        const uint32_t* tab, uint32_t* o) {
+  constexpr uint32_t kExp = 0x7F807F80u;
+  const uint32_t t0 = tab[cd & 0xFFu], t1 = tab[(cd >> 8) & 0xFFu];
+  const uint32_t t2 = tab[(cd >> 16) & 0xFFu], t3 = tab[cd >> 24];
+  o[0] = (t0 & kExp) | (__builtin_amdgcn_perm(b0, b0, 0x01010000u) & ~kExp);
+  o[1] = (t1 & kExp) | (__builtin_amdgcn_perm(b0, b0, 0x03030202u) & ~kExp);
+  o[2] = (t2 & kExp) | (__builtin_amdgcn_perm(b1, b1, 0x01010000u) & ~kExp);
+  o[3] = (t3 & kExp) | (__builtin_amdgcn_perm(b1, b1, 0x03030202u) & ~kExp);
 }
 
 // Position (u32 LE) of escape entry i.
@@ -91,27 +101,31 @@ __device__ __forceinline__ unsigned int entry_pos(const unsigned char* entries, 
          ((unsigned int)e[3] << 24);
 }
 
-// Packed bytes of one thread's share of a chunk: 32 body bytes and 16 code bytes
-// of the K plane and of the V plane (32 words each).
+// Packed bytes of one lane's share of a step, per plane: 16 body bytes (mantissa |
+// sign << 7) and 8 code bytes of 16 consecutive words of each of two tokens.
+// Lane l takes tokens l/8 and l/8 + 8 of the step, dims 16*(l%8) .. +15, so that
+// 8 consecutive lanes read a token's whole 128-byte body row and 64-byte code row.
 struct RawShare {
-  u32x4 kb0, kb1, kc, vb0, vb1, vc;
+  u32x4 kb[2], vb[2];
+  u32x2 kc[2], vc[2];
 };
 
+// `w0`, `w1` = payload word of the share's first K word for each token. Every lane
+// loads (no branch): a lane whose token is past the range passes a clamped,
+// in-range token instead and its words are ignored.
 __device__ __forceinline__ RawShare load_share(const unsigned char* body,
                                                const unsigned char* codes,
-                                               unsigned long long w, unsigned int half,
-                                               bool live) {
+                                               unsigned long long w0, unsigned long long w1,
+                                               unsigned int half) {
   RawShare r;
-  if (live) {
-    r.kb0 = load_stream16(body + w);
-    r.kb1 = load_stream16(body + w + 16);
-    r.kc = load_stream16(codes + w / 2);
-    r.vb0 = load_stream16(body + half + w);
-    r.vb1 = load_stream16(body + half + w + 16);
-    r.vc = load_stream16(codes + (half + w) / 2);
-  } else {
-    r.kb0 = r.kb1 = r.kc = r.vb0 = r.vb1 = r.vc = u32x4{0, 0, 0, 0};
-  }
+  r.kb[0] = load_stream16(body + w0);
+  r.kb[1] = load_stream16(body + w1);
+  r.kc[0] = load_stream8(codes + w0 / 2);
+  r.kc[1] = load_stream8(codes + w1 / 2);
+  r.vb[0] = load_stream16(body + half + w0);
+  r.vb[1] = load_stream16(body + half + w1);
+  r.vc[0] = load_stream8(codes + (half + w0) / 2);
+  r.vc[1] = load_stream8(codes + (half + w1) / 2);
   return r;
 }
 
@@ -136,14 +150,188 @@ __device__ unsigned int lower_bound_escapes(const unsigned char* entries, unsign
   return __builtin_amdgcn_readfirstlane(lo + (unsigned int)__popcll(__ballot(below)));
 }
 
-__global__ __launch_bounds__(kThreads) void top16_attention_split(AttnArgs a) {
-  __shared__ __align__(16) uint16_t sK[kChunk * kKStride];
-  __shared__ __align__(16) uint16_t sVt[kHeadDim * kVtStride];
-  __shared__ __align__(16) uint16_t sP[16 * kPStride];
-  __shared__ float sRed[4][2 * kGroup];
-  __shared__ unsigned int sCount[4];
-  __shared__ unsigned int sPtr[2];
-  __shared__ unsigned int sBad;
+// One 64-entry window of a plane's escape list (entry ptr + lane); positions past
+// the list read as 0xFFFFFFFF.
+struct Window {
+  unsigned int pos, exp;
+};
+
+__device__ __forceinline__ Window load_window(const unsigned char* entries, unsigned int count,
+                                              unsigned int i) {
+  Window w{0xFFFFFFFFu, 0u};
+  if (i < count) {
+    w.pos = entry_pos(entries, i);
+    w.exp = entries[5ull * i + 4];
+  }
+  return w;
+}
+
+// Index of a (dim, token-in-step) element in the transposed V of a wave.
+__device__ __forceinline__ unsigned int vt_index(unsigned int dim, unsigned int tt) {
+  return dim * kVtStride + (dim >> 5) * 16 + tt;
+}
+
+// Applies the escapes of one plane that fall in tokens [ts, t_stop) to the wave's
+// LDS copy of the step and advances the plane's list pointer past them. `base` is
+// the plane's first position (0 or n/2), `row_words` the payload words per token.
+// Returns false when the list is found out of order. Wave-uniform control flow.
+template <bool kV>
+__device__ __forceinline__ bool apply_escapes(Window& win, unsigned int& ptr,
+                                              const unsigned char* entries, unsigned int count,
+                                              unsigned int base, unsigned int ts,
+                                              unsigned int t_stop, unsigned int row_words,
+                                              unsigned int head, uint16_t* sK, uint16_t* sVt) {
+  const unsigned int lane = __lane_id();
+  const unsigned int lo = base + ts * row_words, hi = base + t_stop * row_words;
+  bool ok = true;
+  for (;;) {
+    const bool in = win.pos < hi;
+    if (in) {
+      if (win.pos < lo) {
+        ok = false;  // below this step: the list is not ascending
+      } else {
+        const unsigned int q = win.pos - base;
+        const unsigned int t = q / row_words, rem = q - t * row_words;
+        if (rem / kHeadDim == head) {
+          const unsigned int dim = rem % kHeadDim, tt = t - ts;
+          uint16_t* w = kV ? &sVt[vt_index(dim, tt)] : &sK[tt * kKStride + dim];
+          *w = (uint16_t)((*w & 0x807Fu) | (win.exp << 7));
+        }
+      }
+    }
+    const unsigned int next = __shfl_down(win.pos, 1, 64);
+    if (lane < 63 && next < win.pos) ok = false;
+    const unsigned int taken = (unsigned int)__popcll(__ballot(in));
+    ptr += taken;
+    if (taken < 64) break;
+    win = load_window(entries, count, ptr + lane);  // > 64 escapes in one step
+  }
+  return ok;
+}
+
+// Per-wave state of the walk over a token range.
+struct WaveWalk {
+  float m_run;      // running max (log2 units) of head l%16
+  float l_run;      // this lane's share of the running sum of head l%16
+  f32x4 acc[8];     // O rows 4*(l/16)+j (heads on lanes 0..15), dims 16*nt + l%16
+  Window wk, wv;    // escape windows of the K and V planes
+  unsigned int ptr_k, ptr_v;
+  bool ok;
+};
+
+struct StepConst {
+  const unsigned char* entries;
+  unsigned int count, half, row_words, head, we;
+  float scale_log2;
+  const uint32_t* tab_k;
+  const uint32_t* tab_v;
+  uint16_t* sK;
+  uint16_t* sVt;
+};
+
+// One 16-token step of a wave: decode into the wave's LDS, patch escapes, S^T on
+// MFMA, online softmax, O += P V on MFMA.
+__device__ __forceinline__ void attend_step(const RawShare& cur, unsigned int ts,
+                                            const StepConst& c, const bf16x8 (&qb)[4],
+                                            WaveWalk& w) {
+  const unsigned int lane = __lane_id(), col = lane % 16, grp = lane / 16;
+  const bool tail = ts + kStep > c.we;  // wave-uniform
+  {
+    const unsigned int tt0 = lane / 8, part = lane % 8;  // tokens tt0 and tt0 + 8
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const unsigned int tt = tt0 + 8 * i;
+      uint32_t o[8];
+      decode8(cur.kb[i].x, cur.kb[i].y, cur.kc[i].x, c.tab_k, o);
+      decode8(cur.kb[i].z, cur.kb[i].w, cur.kc[i].y, c.tab_k, o + 4);
+      u32x4* dstk = reinterpret_cast<u32x4*>(c.sK + tt * kKStride + part * 16);
+      dstk[0] = u32x4{o[0], o[1], o[2], o[3]};
+      dstk[1] = u32x4{o[4], o[5], o[6], o[7]};
+      decode8(cur.vb[i].x, cur.vb[i].y, cur.vc[i].x, c.tab_v, o);
+      decode8(cur.vb[i].z, cur.vb[i].w, cur.vc[i].y, c.tab_v, o + 4);
+      if (tail && ts + tt >= c.we) {
+        // a token past the range: zero V so that p = 0 cannot meet an Inf or NaN
+#pragma unroll
+        for (int r = 0; r < 8; ++r) o[r] = 0u;
+      }
+#pragma unroll
+      for (int d = 0; d < 16; ++d)
+        c.sVt[vt_index(part * 16 + d, tt)] = (uint16_t)(o[d >> 1] >> (16 * (d & 1)));
+    }
+  }
+
+  // escapes of this step; then prefetch the windows of the next one
+  const unsigned int t_stop = min(ts + kStep, c.we);
+  w.ok &= apply_escapes<false>(w.wk, w.ptr_k, c.entries, c.count, 0u, ts, t_stop, c.row_words,
+                               c.head, c.sK, c.sVt);
+  w.ok &= apply_escapes<true>(w.wv, w.ptr_v, c.entries, c.count, c.half, ts, t_stop, c.row_words,
+                              c.head, c.sK, c.sVt);
+  w.wk = load_window(c.entries, c.count, w.ptr_k + lane);
+  w.wv = load_window(c.entries, c.count, w.ptr_v + lane);
+  // LDS accesses of one wave complete in order; this keeps the compiler from
+  // moving the reads below above the writes
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- S^T = K Q^T: lane l gets tokens 4*(l/16)+j of head l%16 ----
+  f32x4 st = {0, 0, 0, 0};
+  {
+    const uint16_t* krow = c.sK + col * kKStride + grp * 32;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 ka = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + 8 * ks));
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], st, 0, 0, 0);
+    }
+  }
+  // columns 4..15 (zero query rows) stay finite and only feed output rows that are
+  // never read
+  float sc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sc[j] = st[j] * c.scale_log2;
+  if (tail) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = ts + grp * 4 + j < c.we ? sc[j] : -INFINITY;
+  }
+  float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  const float m_new = fmaxf(w.m_run, mloc);  // finite: every step holds a token
+  if (__ballot(m_new > w.m_run) & 0xFull) {
+    // a head's max moved: rescale its sum share and its acc row
+    const float alpha = __builtin_amdgcn_exp2f(w.m_run - m_new);
+    w.l_run *= alpha;
+    float al[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      al[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), j));
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w.acc[nt][j] *= al[j];
+    w.m_run = m_new;
+  }
+  float p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - w.m_run);
+  w.l_run += (p[0] + p[1]) + (p[2] + p[3]);
+
+  // ---- O += P V: P is already the A operand (head l%16, tokens 4*(l/16)+j) ----
+  i16x4 pa;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pa[j] = (short)bf16_bits(p[j]);
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const uint16_t* vrow = c.sVt + vt_index(nt * 16 + col, grp * 4);
+    const i16x4 vb = __builtin_bit_cast(i16x4, *reinterpret_cast<const u32x2*>(vrow));
+    w.acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, w.acc[nt], 0, 0, 0);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void
+top16_attention_split(AttnArgs a) {
+  __shared__ __align__(16) uint16_t lds[4 * kWaveLds];
+  __shared__ uint32_t sTab[2][256];
+  __shared__ unsigned int sBad[4];
 
   const unsigned int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const unsigned int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -158,216 +346,125 @@ __global__ __launch_bounds__(kThreads) void top16_attention_split(AttnArgs a) {
   const unsigned int header_count = (unsigned int)payload[1] | ((unsigned int)payload[2] << 8) |
                                     ((unsigned int)payload[3] << 16) |
                                     ((unsigned int)payload[4] << 24);
-  const unsigned int count = min(header_count, cap);
-  const unsigned int mode = payload[0];
-  const unsigned int t_begin = split * a.tokens_per_split;
-  const unsigned int t_end = min(ctx, t_begin + a.tokens_per_split);
   const unsigned int row_words = hkv * kHeadDim;  // payload words per token per plane
-  const unsigned int half = (unsigned int)(n / 2);
+  const unsigned int wb = (split * 4 + wave) * a.tokens_per_wave;
+  StepConst c;
+  c.entries = entries;
+  c.count = min(header_count, cap);
+  c.half = (unsigned int)(n / 2);
+  c.row_words = row_words;
+  c.head = h;
+  c.we = min(ctx, wb + a.tokens_per_wave);
+  c.scale_log2 = a.scale_log2;
+  c.tab_k = sTab[0];
+  c.tab_v = sTab[1];
+  c.sK = static_cast<uint16_t*>(__builtin_assume_aligned(lds + wave * kWaveLds, 16));
+  c.sVt = static_cast<uint16_t*>(__builtin_assume_aligned(c.sK + kStep * kKStride, 16));
+  const unsigned int col = lane % 16, grp = lane / 16;
 
-  // Q rows of the GQA group as the MFMA A operand: lane l holds row l%16 (rows 0..3
-  // are the group's query heads, the rest zero), k = 32ks + (l/16)*8 + j
-  bf16x8 qa[4];
+  sTab[0][tid] = table_entry(a.tables + 512, tid);
+  sTab[1][tid] = table_entry(a.tables + 528, tid);
+
+  // query heads of the group as the B operand of S^T = K Q^T: lane l holds head
+  // l%16 (columns 4..15 zero), dims 32*(l/16) + 8*ks + j
+  bf16x8 qb[4];
   {
-    const unsigned int row = lane % 16, kq = (lane / 16) * 8;
-    const uint16_t* qrow = a.q + ((unsigned long long)b * a.q_heads + h * kGroup + row) * kHeadDim;
+    const uint16_t* qrow = a.q + ((unsigned long long)b * a.q_heads + h * kGroup + col) * kHeadDim +
+                           grp * 32;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       u32x4 v = {0, 0, 0, 0};
-      if (row < kGroup) v = *reinterpret_cast<const u32x4*>(qrow + 32 * ks + kq);
-      qa[ks] = __builtin_bit_cast(bf16x8, v);
-    }
-  }
-  // P rows 4..15 stay zero
-  for (unsigned int i = tid; i < 16 * kPStride; i += kThreads) sP[i] = 0;
-  if (tid == 0) sBad = mode != 5 ? 1u : 0u;
-  if (wave < 2) {
-    const unsigned int target = (wave ? half : 0u) + t_begin * row_words;
-    const unsigned int ptr = lower_bound_escapes(entries, count, target);
-    if (lane == 0) sPtr[wave] = ptr;
-  }
-  uint32_t cbk[4], cbv[4];
-  {
-    const uint32_t* t32 = reinterpret_cast<const uint32_t*>(a.tables + 512);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      cbk[k] = t32[k];
-      cbv[k] = t32[4 + k];
+      if (col < kGroup) v = *reinterpret_cast<const u32x4*>(qrow + 8 * ks);
+      qb[ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
 
-  // per-lane online-softmax state: lanes 0..15 own rows 0..3 (the query heads)
-  float m_run[kGroup], l_run[kGroup];
+  WaveWalk w;
+  w.m_run = -INFINITY;
+  w.l_run = 0.f;
 #pragma unroll
-  for (int j = 0; j < kGroup; ++j) {
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.f;
-  }
-  f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  for (int nt = 0; nt < 8; ++nt) w.acc[nt] = f32x4{0, 0, 0, 0};
+  w.ok = payload[0] == 5;
+  __syncthreads();  // decode tables
 
-  // this thread's share of a chunk: token tid/4, dims (tid%4)*32 .. +32
-  const unsigned int tok = tid >> 2, part = tid & 3;
-  const unsigned long long share_word = (unsigned long long)tok * row_words + h * kHeadDim + part * 32;
-  RawShare next = load_share(body, codes, (unsigned long long)t_begin * row_words + share_word,
-                             half, t_begin + tok < t_end);
-  __syncthreads();
-  unsigned int ptr[2] = {sPtr[0], sPtr[1]};
-
-  for (unsigned int t0 = t_begin; t0 < t_end; t0 += kChunk) {
-    // ---- decode this chunk into LDS, prefetch the next one ----
-    const RawShare cur = next;
-    const unsigned int tn = t0 + kChunk;
-    next = load_share(body, codes, (unsigned long long)tn * row_words + share_word, half,
-                      tn + tok < t_end);
-    const u32x4 k0 = cur.kb0, k1 = cur.kb1, k2 = cur.kc, v0 = cur.vb0, v1 = cur.vb1, v2 = cur.vc;
-    {
-      // tokens past the context are written as zeros (their scores are masked)
-      const bool live = t0 + tok < t_end;
-      const uint32_t bk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const uint32_t ck[4] = {k2.x, k2.y, k2.z, k2.w};
-      uint32_t o[16];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) decode8(bk[2 * r], bk[2 * r + 1], ck[r], cbk, o + 4 * r);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[r] = live ? o[r] : 0u;
-      u32x4* dstk = reinterpret_cast<u32x4*>(sK + tok * kKStride + part * 32);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dstk[r] = u32x4{o[4 * r], o[4 * r + 1], o[4 * r + 2], o[4 * r + 3]};
-      const uint32_t bv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      const uint32_t cv[4] = {v2.x, v2.y, v2.z, v2.w};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) decode8(bv[2 * r], bv[2 * r + 1], cv[r], cbv, o + 4 * r);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[r] = live ? o[r] : 0u;
-#pragma unroll
-      for (int d = 0; d < 32; ++d)
-        sVt[(part * 32 + d) * kVtStride + tok] = (uint16_t)(o[d >> 1] >> (16 * (d & 1)));
+  if (wb < c.we) {
+    const unsigned int we = c.we;
+    w.ptr_k = lower_bound_escapes(entries, c.count, wb * row_words);
+    w.ptr_v = lower_bound_escapes(entries, c.count, c.half + wb * row_words);
+    w.wk = load_window(entries, c.count, w.ptr_k + lane);
+    w.wv = load_window(entries, c.count, w.ptr_v + lane);
+    const unsigned int share = h * kHeadDim + (lane % 8) * 16;
+    // two register sets of raw bytes alternate: one is decoded while the next
+    // step's loads are in flight
+    auto load_step = [&](unsigned int ts) {
+      const unsigned int t0 = ts + lane / 8;
+      return load_share(body, codes, (unsigned long long)min(t0, we - 1) * row_words + share,
+                        (unsigned long long)min(t0 + 8, we - 1) * row_words + share, c.half);
+    };
+    RawShare r0 = load_step(wb);
+    for (unsigned int ts = wb;;) {
+      const unsigned int t1 = ts + kStep;
+      const RawShare r1 = load_step(t1);
+      attend_step(r0, ts, c, qb, w);
+      ts = t1;
+      if (ts >= we) break;
+      r0 = load_step(ts + kStep);
+      attend_step(r1, ts, c, qb, w);
+      ts += kStep;
+      if (ts >= we) break;
     }
-    __syncthreads();
-
-    // ---- escapes of this chunk (K plane, then V plane) ----
-    const unsigned int t_stop = min(t0 + kChunk, t_end);
-#pragma unroll
-    for (int plane = 0; plane < 2; ++plane) {
-      const unsigned int base = plane ? half : 0u;
-      const unsigned int hi = base + t_stop * row_words;
-      for (;;) {
-        const unsigned int i = ptr[plane] + tid;
-        const bool valid = i < count;
-        const unsigned int p = valid ? entry_pos(entries, i) : 0xFFFFFFFFu;
-        const bool in = p < hi;
-        // p >= base holds for an ascending list; checked so that an out-of-order
-        // entry can never address outside the chunk
-        if (in && p >= base) {
-          const unsigned int e = entries[5ull * i + 4];
-          const unsigned int q = p - base;
-          const unsigned int t = q / row_words, rem = q - t * row_words;
-          if (rem / kHeadDim == h && t >= t0) {
-            const unsigned int dim = rem % kHeadDim, tt = t - t0;
-            uint16_t* w = plane ? &sVt[dim * kVtStride + tt] : &sK[tt * kKStride + dim];
-            *w = (uint16_t)((*w & 0x807F) | (e << 7));
-          }
-        }
-        // ascending order check between this entry and the next one read
-        const unsigned int next = __shfl_down(p, 1, 64);
-        if (valid && lane < 63 && i + 1 < count && next < p) sBad = 1;
-        const unsigned int wave_in = (unsigned int)__popcll(__ballot(in));
-        if (lane == 0) sCount[wave] = wave_in;
-        __syncthreads();
-        const unsigned int total = sCount[0] + sCount[1] + sCount[2] + sCount[3];
-        ptr[plane] += total;
-        __syncthreads();
-        if (total < kThreads) break;
-      }
-    }
-
-    // ---- S = Q K^T for tokens 16w .. 16w+15 of the chunk ----
-    f32x4 s = {0, 0, 0, 0};
-    {
-      const uint16_t* krow = sK + (wave * 16 + lane % 16) * kKStride + (lane / 16) * 8;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 kb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + 32 * ks));
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kb, s, 0, 0, 0);
-      }
-    }
-    // lane l < 16 holds rows 0..3 (query heads) of token 16w + l
-    const bool tok_ok = t0 + wave * 16 + (lane % 16) < t_end;
-    float sc[kGroup], mx[kGroup];
-#pragma unroll
-    for (int j = 0; j < kGroup; ++j) {
-      sc[j] = (lane < 16 && tok_ok) ? s[j] * a.scale_log2 : -INFINITY;
-      mx[j] = sc[j];
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], o, 16));
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int j = 0; j < kGroup; ++j) sRed[wave][j] = mx[j];
-    }
-    __syncthreads();
-    float alpha[kGroup], pr[kGroup], sum[kGroup];
-#pragma unroll
-    for (int j = 0; j < kGroup; ++j) {
-      const float cmax = fmaxf(fmaxf(sRed[0][j], sRed[1][j]), fmaxf(sRed[2][j], sRed[3][j]));
-      const float m_new = fmaxf(m_run[j], cmax);
-      alpha[j] = exp2f(m_run[j] - m_new);
-      m_run[j] = m_new;
-      pr[j] = lane < 16 && tok_ok ? exp2f(sc[j] - m_new) : 0.f;
-      sum[j] = pr[j];
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) sum[j] += __shfl_xor(sum[j], o, 16);
-    }
-    if (lane < 16) {
-#pragma unroll
-      for (int j = 0; j < kGroup; ++j)
-        sP[j * kPStride + wave * 16 + lane] = (uint16_t)bf16_bits(pr[j]);
-    }
-    if (lane == 0) {
-#pragma unroll
-      for (int j = 0; j < kGroup; ++j) sRed[wave][kGroup + j] = sum[j];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kGroup; ++j) {
-      l_run[j] = l_run[j] * alpha[j] + sRed[0][kGroup + j] + sRed[1][kGroup + j] +
-                 sRed[2][kGroup + j] + sRed[3][kGroup + j];
-    }
-    // rows held by this lane: (lane/16)*4 + j; only lanes 0..15 hold real rows
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[nt][j] *= lane < 16 ? alpha[j] : 0.f;
-
-    // ---- O += P V for dims 32w .. 32w+31 ----
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8 pa = __builtin_bit_cast(
-          bf16x8, *reinterpret_cast<const u32x4*>(sP + (lane % 16) * kPStride + 32 * ks + (lane / 16) * 8));
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const uint16_t* vrow = sVt + (wave * 32 + nt * 16 + lane % 16) * kVtStride + 32 * ks + (lane / 16) * 8;
-        const bf16x8 vb = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(vrow));
-        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, vb, acc[nt], 0, 0, 0);
-      }
-    }
-    __syncthreads();  // sK, sVt and sP are rewritten by the next chunk
   }
 
-  // ---- partial results of this split ----
-  const bool bad = sBad != 0;
-  float* out = a.partial +
-               (((unsigned long long)b * hkv + h) * a.splits + split) * kGroup * kPartial;
+  // ---- merge the 4 waves (m, l, acc per head), then write this split's partial ----
+  float l_run = w.l_run;
+  const float m_run = w.m_run;
+  l_run += __shfl_xor(l_run, 16, 64);
+  l_run += __shfl_xor(l_run, 32, 64);
+  const bool wave_bad = __ballot(!w.ok) != 0;
+  if (lane == 0) sBad[wave] = wave_bad ? 1u : 0u;
+  __syncthreads();  // every wave is done with its LDS region
+  float* sm = reinterpret_cast<float*>(lds);  // [wave][head][kPartial]
+  if (lane < kGroup) {
+    sm[(wave * kGroup + lane) * kPartial] = m_run;
+    sm[(wave * kGroup + lane) * kPartial + 1] = l_run;
+  }
   if (lane < 16) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-      for (int j = 0; j < kGroup; ++j)
-        out[j * kPartial + 2 + wave * 32 + nt * 16 + lane] = bad ? NAN : acc[nt][j];
+      for (int j = 0; j < 4; ++j) sm[(wave * kGroup + j) * kPartial + 2 + nt * 16 + lane] = w.acc[nt][j];
   }
-  if (wave == 0 && lane < kGroup) {
-    out[lane * kPartial] = bad ? NAN : m_run[lane];
-    out[lane * kPartial + 1] = bad ? NAN : l_run[lane];
+  __syncthreads();
+  const bool bad = (sBad[0] | sBad[1] | sBad[2] | sBad[3]) != 0;
+  float* out = a.partial + (((unsigned long long)b * hkv + h) * a.splits + split) * kGroup * kPartial;
+  (void)grp;
+  {
+    const unsigned int head = tid / 64, d0 = (tid % 64) * 2;
+    float mw[4], big = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = sm[(w * kGroup + head) * kPartial];
+      big = fmaxf(big, mw[w]);
+    }
+    float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
+    if (big != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if (mw[w] == -INFINITY) continue;  // a wave with no tokens
+        const float* src = sm + (w * kGroup + head) * kPartial;
+        const float wgt = exp2f(mw[w] - big);
+        l_sum += src[1] * wgt;
+        o0 += src[2 + d0] * wgt;
+        o1 += src[3 + d0] * wgt;
+      }
+    }
+    float* dst = out + head * kPartial;
+    dst[2 + d0] = bad ? NAN : o0;
+    dst[3 + d0] = bad ? NAN : o1;
+    if (tid % 64 == 0) {
+      dst[0] = bad ? NAN : big;
+      dst[1] = bad ? NAN : l_sum;
+    }
   }
 }
 
@@ -399,9 +496,53 @@ using namespace unchainkv;
 
 namespace {
 
-unsigned int attention_splits(unsigned long long max_ctx) {
-  const unsigned long long s = (max_ctx + 1023) / 1024;
-  return (unsigned int)(s < 1 ? 1 : (s > 64 ? 64 : s));
+// Split-kernel workgroups the current device keeps resident at once (CUs x
+// workgroups per CU at this kernel's register and LDS use), cached per device.
+unsigned long long resident_workgroups() {
+  static std::mutex mu;
+  static unsigned long long cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(top16_attention_split), kThreads, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 2;
+    cached[dev] = (unsigned long long)cus * (unsigned long long)per_cu;
+  }
+  return cached[dev];
+}
+
+struct SplitPlan {
+  unsigned int splits, tokens_per_wave;
+};
+
+// Context splits per (sequence, kv head): the count whose workgroups fill whole
+// rounds of the resident slots with the fewest tokens per wave (a wave walks its
+// range serially; a round that is partly empty wastes the rest of the chip).
+SplitPlan plan_splits(unsigned long long pairs, unsigned long long max_ctx) {
+  const unsigned long long slots = resident_workgroups();
+  constexpr unsigned long long kWaveOverhead = 32;  // start-up cost in token steps
+  SplitPlan best{1, 0};
+  unsigned long long best_cost = ~0ull;
+  for (unsigned int s = 1; s <= kMaxSplits; ++s) {
+    const unsigned long long per_wave = (max_ctx + 4ull * s - 1) / (4ull * s);
+    const unsigned long long tpw = (per_wave + kStep - 1) / kStep * kStep;
+    if (s > 1 && (unsigned long long)(s - 1) * 4 * tpw >= max_ctx) break;  // empty splits
+    const unsigned long long rounds = (pairs * s + slots - 1) / slots;
+    const unsigned long long cost = rounds * (tpw + kWaveOverhead);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = SplitPlan{s, (unsigned int)tpw};
+    }
+  }
+  return best;
 }
 
 }  // namespace
@@ -410,8 +551,10 @@ unsigned int attention_splits(unsigned long long max_ctx) {
 // the reference).
 extern "C" unsigned long long kvq_splitzip_top16_decode_attention_workspace_bytes(
     unsigned long long batch, unsigned long long kv_heads, unsigned long long max_ctx) {
+  if (batch == 0 || kv_heads == 0 || max_ctx == 0) return 0;
   const unsigned long long per_launch = batch < kMaxSeqs ? batch : kMaxSeqs;
-  return per_launch * kv_heads * attention_splits(max_ctx) * kGroup * kPartial * sizeof(float);
+  const SplitPlan plan = plan_splits(per_launch * kv_heads, max_ctx);
+  return per_launch * kv_heads * plan.splits * kGroup * kPartial * sizeof(float);
 }
 
 // Decode attention of one query token per sequence over Top-16 packed KV (no
@@ -443,8 +586,8 @@ extern "C" long long kvq_splitzip_top16_decode_attention(
   if (kvq_splitzip_top16_decode_attention_workspace_bytes(batch, kv_heads, max_ctx) >
       workspace_bytes)
     return 0;
-  const unsigned int splits = attention_splits(max_ctx);
-  const unsigned int per = (unsigned int)(((max_ctx + splits - 1) / splits + kChunk - 1) / kChunk * kChunk);
+  const unsigned long long per_launch = batch < kMaxSeqs ? batch : kMaxSeqs;
+  const SplitPlan plan = plan_splits(per_launch * kv_heads, max_ctx);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < batch; first += kMaxSeqs) {
     const unsigned int count = (unsigned int)(batch - first < kMaxSeqs ? batch - first : kMaxSeqs);
@@ -457,8 +600,8 @@ extern "C" long long kvq_splitzip_top16_decode_attention(
     a.batch = count;
     a.q_heads = (unsigned int)q_heads;
     a.kv_heads = (unsigned int)kv_heads;
-    a.splits = splits;
-    a.tokens_per_split = per;
+    a.splits = plan.splits;
+    a.tokens_per_wave = plan.tokens_per_wave;
     a.scale_log2 = scale * 1.4426950408889634f;
     for (unsigned int r = 0; r < count; ++r) {
       a.offset[r] = payload_offsets[first + r];
@@ -466,7 +609,7 @@ extern "C" long long kvq_splitzip_top16_decode_attention(
       a.ctx[r] = (unsigned int)ctx;
       a.span[r] = (unsigned int)((ctx + block_tokens - 1) / block_tokens * block_tokens);
     }
-    hipLaunchKernelGGL(top16_attention_split, dim3(splits, (unsigned int)kv_heads, count),
+    hipLaunchKernelGGL(top16_attention_split, dim3(plan.splits, (unsigned int)kv_heads, count),
                        dim3(kThreads), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("top16_attention_split", st);

@@ -607,6 +607,15 @@ def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Paged
 # ---------------------------------------------------------------------------
 # fused Top-16 decode + decode attention
 
+def decode_attention_workspace_bytes(batch: int, kv_heads: int, max_context: int) -> int:
+    """Bytes of the workspace decode_attention_top16 uses (split partials)."""
+    lib = _load()
+    if lib is None or not hasattr(lib, "kvq_splitzip_top16_decode_attention_workspace_bytes"):
+        raise RuntimeError(f"HIP codec library not loaded: {load_error()}")
+    return int(lib.kvq_splitzip_top16_decode_attention_workspace_bytes(batch, kv_heads,
+                                                                        max_context))
+
+
 def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_heads: int,
                            layer_index: int = -1, *, block_tokens: int = 16,
                            codebooks: bytes | None = None, tables=None,
