@@ -332,6 +332,17 @@ def test_paged_escape_heavy_tiles(sz, codebooks, label):
         assert bytes(got) == bytes(ref), f"payload {r}"
         if label == "overflow":
             assert got[0] == 255
+    # decode: 300 escapes in one tile are all patched; overflowed payloads stay
+    # untouched (the reference decoder skips a payload whose byte 0 is not 5)
+    target = torch.zeros_like(kv)
+    sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, target, batch,
+                          codebooks=books)
+    got = u16(target).reshape(2, pool, bw)
+    for r, t in enumerate(block_tables):
+        if label == "overflow":
+            assert not got[:, t].any(), r
+        else:
+            assert np.array_equal(got[:, t], kv_host[:, t]), r
 
 
 def test_paged_full_size_llama3_8b_layer(sz):
