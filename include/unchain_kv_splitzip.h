@@ -182,6 +182,30 @@ long long kvq_splitzip_bf16_decode_mode_paged(
     const unsigned long long* block_offsets, unsigned long long stream_ptr, int bits);
 
 /* ------------------------------------------------------------------------------
+ * bf16 exponent histograms of a paged layer: the statistics Top-16 codebooks are
+ * fit from (no counterpart in the reference as a native call: it runs
+ * torch.bincount((word >> 7) & 0xFF) per plane of a gathered request,
+ * src/unchain_kv/vllm_connector.py:2871-2904, and ranks the counts offline,
+ * scripts/extract_llama_top16_codebooks.py:15-60).
+ * ---------------------------------------------------------------------------- */
+
+/* Workspace bytes kvq_splitzip_exponent_histogram_paged needs. */
+unsigned long long kvq_splitzip_exponent_histogram_workspace_bytes(
+    unsigned long long block_count, unsigned long long block_words);
+
+/* counts (device, 512 x u64, overwritten): [b] = K-plane words of blocks
+ * ids[0 .. block_count) whose exponent bits (word >> 7) & 0xFF equal b, [256 + b]
+ * the same for the V plane. block_ids_ptr: device int64 array; plane_stride and
+ * block_stride in elements. Returns the words counted (2 * block_count *
+ * block_words), 0 on a failed precondition. Deterministic (no global atomics). */
+long long kvq_splitzip_exponent_histogram_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    unsigned long long block_count, unsigned long long counts_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long stream_ptr);
+
+/* ------------------------------------------------------------------------------
  * Fused Top-16 decode + decode attention (no counterpart in the reference, whose
  * consumer decodes each payload into the paged KV cache and then runs attention;
  * scripts/bench_codec_attention.py times that pairing).

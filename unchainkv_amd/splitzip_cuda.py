@@ -65,6 +65,8 @@ _SIGNATURES = (
     ),
     ("kvq_splitzip_palette_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
     ("kvq_splitzip_top16_decode_attention_workspace_bytes", [_U64] * 3, _U64, False),
+    ("kvq_splitzip_exponent_histogram_workspace_bytes", [_U64] * 2, _U64, False),
+    ("kvq_splitzip_exponent_histogram_paged", [_U64] * 10, ctypes.c_longlong, False),
     (
         "kvq_splitzip_top16_decode_attention",
         [_U64, _U64, _U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64, _U64,
@@ -669,3 +671,51 @@ def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_head
     if got < 0:
         _raise_last(lib, "splitzip top16 decode attention failed")
     return out if got else None
+
+
+# ---------------------------------------------------------------------------
+# exponent histograms (codebook fitting)
+
+def exponent_histogram_paged(kv_layer, batch: PagedBatch, *, workspace=None, counts=None):
+    """(2, 256) int64 device tensor: per K/V plane, the count of every bf16 exponent
+    (bits 7..14) over all blocks of ``batch`` in the paged layer ``kv_layer`` (what
+    the reference's exponent trace bins with torch.bincount per plane,
+    src/unchain_kv/vllm_connector.py:2871-2904). ``None`` when the kernel declines."""
+    lib = _load()
+    hist = getattr(lib, "kvq_splitzip_exponent_histogram_paged", None) if lib else None
+    if hist is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    count = len(batch.ids)
+    need = int(lib.kvq_splitzip_exponent_histogram_workspace_bytes(count, batch.block_words))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=kv_layer.device)
+    if counts is None:
+        counts = torch.empty((2, 256), dtype=torch.int64, device=kv_layer.device)
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    got = hist(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+               batch.block_words, int(batch.ids.data_ptr()), count, int(counts.data_ptr()),
+               int(workspace.data_ptr()), int(workspace.numel()), int(stream))
+    if got < 0:
+        _raise_last(lib, "splitzip exponent histogram failed")
+    return counts if got else None
+
+
+def fit_top16_codebook_paged(kv_layer, batch: PagedBatch) -> bytes | None:
+    """The layer's 32-byte Top-16 codebook (16 K exponents, then 16 V) fit on the
+    GPU histogram of ``batch``'s blocks with the reference's rule: the 16 most
+    frequent exponents by (-count, value) (scripts/extract_llama_top16_codebooks.py
+    :15-60). ``None`` when a plane has fewer than 16 distinct exponents."""
+    from . import codebooks as cb
+
+    counts = exponent_histogram_paged(kv_layer, batch)
+    if counts is None:
+        return None
+    k, v = counts.cpu().tolist()
+    try:
+        return cb.fit_layer_codebook(k, v)
+    except ValueError:
+        return None
