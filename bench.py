@@ -211,6 +211,38 @@ def verify(torch, w):
             raise RuntimeError(f"layer {layer}: decoded KV differs from the source")
 
 
+def time_histogram(torch, sz, w, reps: int = 10):
+    """Per-layer GPU exponent histograms of every request's blocks (the codebook
+    fit statistics), checked against torch.bincount on layer 0, then timed with
+    HIP events over `reps` calls per layer on the first layers."""
+    send = w["send"]
+    kv0 = w["kv"][0]
+    counts = sz.exponent_histogram_paged(kv0, send)
+    ids = send.ids
+    for plane in range(2):
+        words = kv0[plane].index_select(0, ids).reshape(-1).view(torch.int16).to(torch.int32)
+        ref = torch.bincount(torch.bitwise_and(torch.bitwise_right_shift(words, 7), 0xFF),
+                             minlength=256)
+        if not torch.equal(counts[plane], ref):
+            raise RuntimeError("exponent histogram differs from torch.bincount")
+    layers = min(w["layers"], 8)
+    ws = torch.empty(int(sz.exponent_histogram_workspace_bytes(len(ids), send.block_words)),
+                     dtype=torch.uint8, device=w["device"])
+    out = torch.empty((2, 256), dtype=torch.int64, device=w["device"])
+    stream = torch.cuda.current_stream(w["device"])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        for layer in range(layers):
+            sz.exponent_histogram_paged(w["kv"][layer], send, workspace=ws, counts=out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * layers)
+    gbps = send.total_raw_bytes / (ms * 1e-3) / 1e9
+    return {"ms_per_layer_call": round(ms, 5), "raw_GBps": round(gbps, 2),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle's C codec, test infrastructure, timed on this host)
 
@@ -624,6 +656,7 @@ def main() -> int:
     verify(torch, w)
     enc_call = sum(enc_ms) / len(enc_ms)
     dec_call = sum(dec_ms) / len(dec_ms)
+    hist = time_histogram(torch, sz, w)
 
     send = w["send"]
     raw_layer = send.total_raw_bytes
@@ -693,6 +726,7 @@ def main() -> int:
             "hbm_frac": round(dec_hbm / HBM_PEAK_GBPS, 4),
             "ms_per_layer_call": round(dec_call, 5),
         },
+        "exponent_histogram": hist,
         "compression_ratio": round(raw_layer / final, 5),
         "escapes_per_layer": round(escapes / layers, 1),
         "overflowed_payloads": overflowed,

@@ -3,6 +3,7 @@ environment knobs and restore validation. The backoff cases follow the
 reference's tests/test_vllm_connector.py:2966-3045."""
 
 from concurrent.futures import ThreadPoolExecutor
+from types import SimpleNamespace
 
 import pytest
 
@@ -142,3 +143,62 @@ def test_restore_rejects_unsupported_torch_modes_and_bad_blocks():
     assert c.load_kv_layer_batch(0, kv, [([0, 0], b"\x06" + bytes(16), raw)]) == [(0, 0)]
     assert c.load_kv_layer_batch(0, kv, [([0, 9], b"\x06" + bytes(16), raw)]) == [(0, 0)]
     assert codec_format.MODE_RAW == 6
+
+
+def test_exponent_trace_once_per_transfer_layer_and_retry_after_error():
+    """bf16_exponent_stats is emitted once per (transfer, layer) with the
+    summarised K and V histograms; a failure emits bf16_exponent_stats_error and
+    leaves the key free for a retry (vllm_connector.py:2871-2904)."""
+    import numpy as np
+
+    class FakeCounts:
+        def __init__(self, rows):
+            self.rows = rows
+
+        def cpu(self):
+            return self
+
+        def tolist(self):
+            return self.rows
+
+    k = [0] * 256
+    v = [0] * 256
+    k[120], k[121], v[110] = 30, 10, 40
+    calls = []
+
+    class FakeLib:
+        fail = True
+
+        def available(self):
+            return True
+
+        def PagedBatch(self, tables, block_words, device):
+            calls.append((tables, block_words))
+            return SimpleNamespace()
+
+        def exponent_histogram_paged(self, kv, batch):
+            if FakeLib.fail:
+                raise RuntimeError("boom")
+            return FakeCounts([k, v])
+
+    class FakeLayer:
+        device = "cuda:0"
+
+        def __getitem__(self, index):
+            return SimpleNamespace(numel=lambda: 2048)
+
+    trace = RecordingTrace()
+    c = SplitzipLayerCodec(CodecConfig(), trace=trace, lib=FakeLib())
+    c._trace_bf16_exponents(FakeLayer(), [[3, 4]], "t1", 2)
+    assert trace.names()[-1] == "bf16_exponent_stats_error"
+    FakeLib.fail = False
+    c._trace_bf16_exponents(FakeLayer(), [[3, 4]], "t1", 2)
+    c._trace_bf16_exponents(FakeLayer(), [[3, 4]], "t1", 2)  # traced already
+    stats = [e for e in trace.rows if e[0] == "bf16_exponent_stats"]
+    assert len(stats) == 1
+    fields = stats[0][1]
+    assert fields["transfer"] == "t1" and fields["layer"] == 2
+    assert fields["k"]["words"] == 40 and fields["k"]["top8_exponents"][:2] == [120, 121]
+    assert fields["v"]["unique_exponents"] == 1
+    assert np.isclose(fields["k"]["top16_coverage"], 1.0)
+    assert calls[-1] == ([[3, 4]], 2048)

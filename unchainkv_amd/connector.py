@@ -34,6 +34,7 @@ import threading
 from dataclasses import dataclass, field
 
 from . import codec_format
+from .codebooks import summarize_symbol_counts
 from .trace import TraceWriter
 
 TOP16_MIN_BYTES = 1 << 20
@@ -131,6 +132,7 @@ class SplitzipLayerCodec:
         self._splitzip_top16_probe_layers: set[int] = set()
         self._splitzip_top16_epochs: dict[int, int] = {}
         self._splitzip_top16_lock = threading.Lock()
+        self._traced_bf16_exponents: set[tuple[str, int]] = set()
 
     # ------------------------------------------------------------------
     # library
@@ -159,6 +161,34 @@ class SplitzipLayerCodec:
         if 0 <= layer_index < len(sz._TOP16_CODEBOOKS) // 32:
             return sz._TOP16_CODEBOOKS[32 * layer_index:32 * (layer_index + 1)]
         return None
+
+    # ------------------------------------------------------------------
+    # exponent statistics (vllm_connector.py:2871-2904)
+
+    def _trace_bf16_exponents(self, kv_layer, block_tables, transfer_id: str,
+                              layer_index: int) -> None:
+        """Once per (transfer, layer): the ``bf16_exponent_stats`` trace event with
+        the K and V exponent histograms of the request's blocks, counted on the GPU
+        in place (the reference gathers the blocks and runs torch.bincount per
+        plane). Failures become ``bf16_exponent_stats_error`` and allow a retry."""
+        key = (transfer_id, layer_index)
+        if key in self._traced_bf16_exponents:
+            return
+        self._traced_bf16_exponents.add(key)
+        try:
+            sz = self._lib()
+            batch = sz.PagedBatch(block_tables, kv_layer[0, 0].numel(), kv_layer.device)
+            counts = sz.exponent_histogram_paged(kv_layer, batch)
+            if counts is None:
+                raise RuntimeError("exponent histogram declined")
+            k_counts, v_counts = counts.cpu().tolist()
+            self.trace.event("bf16_exponent_stats", transfer=transfer_id, layer=layer_index,
+                             k=summarize_symbol_counts(k_counts),
+                             v=summarize_symbol_counts(v_counts))
+        except Exception as exc:  # noqa: BLE001 - the trace must not break the save path
+            self._traced_bf16_exponents.discard(key)
+            self.trace.event("bf16_exponent_stats_error", transfer=transfer_id,
+                             layer=layer_index, error=str(exc)[:160])
 
     # ------------------------------------------------------------------
     # Top-16 backoff (vllm_connector.py:2906-3021)

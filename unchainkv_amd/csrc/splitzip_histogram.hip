@@ -8,12 +8,13 @@
 // straight from the cache (no gather copy).
 //
 // Two kernels, no global atomics, deterministic output:
-//   exponent_hist_partial: each wave streams 1024-word chunks (one KV block each)
-//     and adds every word's exponent into an LDS histogram of its own; a bin is
-//     kept in 4 copies selected by lane % 4, interleaved so the copies sit in
-//     different banks, which cuts the serialisation of same-bin LDS atomics (a
-//     bf16 plane concentrates on ~16 exponents). The workgroup then writes one
-//     512-bin partial (K bins, then V bins).
+//   exponent_hist_partial: each wave streams batches of four 1024-word chunks
+//     (block ids fetched a batch ahead) and adds every word's exponent into the
+//     workgroup's LDS histogram. Lane l of every wave counts into copy l of the
+//     histogram, two 16-bit bins per dword, laid out so that copy l sits in bank
+//     l: an LDS atomic instruction never has two lanes on one bank (a bf16 plane
+//     concentrates on ~16 exponents, and colliding LDS atomics serialise). The
+//     workgroup then writes one 512-bin partial (K bins, then V bins).
 //   exponent_hist_reduce: sums the partials into 64-bit counts.
 // Layouts that the chunk kernel cannot take (block words not a multiple of 1024,
 // misaligned cache) go through a one-word-per-thread kernel with the same output.
@@ -28,96 +29,153 @@ namespace unchainkv {
 namespace {
 
 constexpr int kBins = 256;
-constexpr int kCopies = 4;
+constexpr int kCopies = 64;                    // one per lane
+// 16-bit counters: a workgroup counts at most kCopies * 65535 words
 constexpr int kChunk = 1024;                   // words per wave step (one block)
 constexpr unsigned int kMaxPartials = 2048;    // workgroups of the partial kernel
+
+constexpr int kBatch = 4;                     // chunks per wave step (8 KiB of loads)
 
 struct HistArgs {
   const uint16_t* kv;
   const long long* ids;
   unsigned int* partial;  // [workgroup][2 * kBins]
   unsigned long long plane_stride, block_stride, block_words, block_count;
-  unsigned long long chunks_per_plane;  // block_count * block_words / kChunk (chunk kernel)
+  // chunk kernel: chunks of one plane, chunks per block and its divider
+  unsigned int chunks_per_plane, chunks_per_block;
+  unsigned long long cpb_magic;
 };
 
-// LDS histogram of one wave: [plane][bin][copy]
-__device__ __forceinline__ unsigned int hist_index(unsigned int plane, unsigned int bin,
-                                                   unsigned int copy) {
-  return (plane * kBins + bin) * kCopies + copy;
-}
+constexpr unsigned long long kMaxWordsPerGroup = (unsigned long long)kCopies * 65535;
+constexpr int kHistWords = kBins * kCopies;     // dwords: 2 planes x 256 bins / 2 per dword
 
+// LDS histogram of a workgroup: dword [plane][bin / 2][copy], bin parity selects
+// the 16-bit half.
 __device__ __forceinline__ void add_word(unsigned int* h, unsigned int plane, uint32_t w,
                                          unsigned int copy) {
-  atomicAdd(&h[hist_index(plane, (w >> 7) & 0xFFu, copy)], 1u);
+  const unsigned int bin = (w >> 7) & 0xFFu;
+  atomicAdd(&h[(plane * (kBins / 2) + (bin >> 1)) * kCopies + copy], 1u << (16 * (bin & 1)));
 }
 
-// Sums the 4 waves x 4 copies of every bin and writes the workgroup's partial.
-__device__ __forceinline__ void write_partial(const unsigned int (*h)[2 * kBins * kCopies],
-                                              unsigned int* partial) {
-  for (unsigned int b = threadIdx.x; b < 2 * kBins; b += kThreads) {
-    unsigned int s = 0;
-#pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w)
-#pragma unroll
-      for (int c = 0; c < kCopies; ++c) s += h[w][b * kCopies + c];
-    partial[(unsigned long long)blockIdx.x * 2 * kBins + b] = s;
+__device__ __forceinline__ void zero_hist(unsigned int* h) {
+  for (unsigned int i = threadIdx.x; i < kHistWords; i += kThreads) h[i] = 0;
+  __syncthreads();
+}
+
+// Sums the copies of every bin and writes the workgroup's partial: thread t sums
+// the bin pair t (both halves of the 64 copies' dwords).
+__device__ __forceinline__ void write_partial(const unsigned int* h, unsigned int* partial) {
+  __syncthreads();
+  const unsigned int pair = threadIdx.x;  // 256 pairs = 512 bins
+  unsigned int lo = 0, hi = 0;
+#pragma unroll 8
+  for (int c = 0; c < kCopies; ++c) {
+    const unsigned int v = h[pair * kCopies + (c + pair) % kCopies];
+    lo += v & 0xFFFFu;
+    hi += v >> 16;
   }
+  unsigned int* out = partial + (unsigned long long)blockIdx.x * 2 * kBins + 2 * pair;
+  out[0] = lo;
+  out[1] = hi;
 }
 
-__device__ __forceinline__ u32x4 load_chunk_part(const HistArgs& a, unsigned long long chunk,
-                                                 unsigned int half_lane_word) {
-  const unsigned int plane = chunk >= a.chunks_per_plane ? 1u : 0u;
-  const unsigned long long word = (chunk - plane * a.chunks_per_plane) * kChunk;
-  const unsigned long long j = word / a.block_words;
-  const unsigned long long within = word - j * a.block_words;
-  const uint16_t* src = a.kv + plane * a.plane_stride +
-                        (unsigned long long)a.ids[j] * a.block_stride + within;
-  return load_stream16(src + half_lane_word);
+// Block id of chunk c (lanes 0..kBatch-1 of a wave each fetch one chunk of a batch).
+__device__ __forceinline__ long long chunk_block_id(const HistArgs& a, unsigned int c) {
+  const unsigned int plane = c >= a.chunks_per_plane ? 1u : 0u;
+  const unsigned int cin = c - plane * a.chunks_per_plane;
+  return a.ids[div_u32(cin, a.cpb_magic, a.chunks_per_block)];
+}
+
+// Element offset of chunk c's first word, given its block id.
+__device__ __forceinline__ unsigned long long chunk_offset(const HistArgs& a, unsigned int c,
+                                                           unsigned long long id) {
+  const unsigned int plane = c >= a.chunks_per_plane ? 1u : 0u;
+  const unsigned int cin = c - plane * a.chunks_per_plane;
+  const unsigned int j = div_u32(cin, a.cpb_magic, a.chunks_per_block);
+  return plane * a.plane_stride + id * a.block_stride +
+         (unsigned long long)(cin - j * a.chunks_per_block) * kChunk;
+}
+
+struct Batch {
+  u32x4 d[2 * kBatch];
+};
+
+// Issues the loads of batch b (chunks kBatch*b ..): block ids from `idv`, lane k's
+// value for chunk k.
+__device__ __forceinline__ Batch load_batch(const HistArgs& a, unsigned int b, long long idv,
+                                            unsigned int total, unsigned int lane) {
+  Batch r;
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) {
+    const unsigned int c = b * kBatch + k;
+    const long long id = __builtin_amdgcn_readlane((int)idv, k) |
+                         ((long long)__builtin_amdgcn_readlane((int)(idv >> 32), k) << 32);
+    if (c < total) {
+      const uint16_t* src = a.kv + chunk_offset(a, c, (unsigned long long)id);
+      r.d[2 * k] = load_stream16(src + 8 * lane);
+      r.d[2 * k + 1] = load_stream16(src + 512 + 8 * lane);
+    } else {
+      r.d[2 * k] = r.d[2 * k + 1] = u32x4{0, 0, 0, 0};
+    }
+  }
+  return r;
+}
+
+__device__ __forceinline__ long long load_ids(const HistArgs& a, unsigned int b,
+                                              unsigned int total, unsigned int lane) {
+  const unsigned int c = b * kBatch + lane;
+  return lane < (unsigned int)kBatch && c < total ? chunk_block_id(a, c) : 0;
 }
 
 __global__ __launch_bounds__(kThreads) void exponent_hist_partial(HistArgs a) {
-  __shared__ unsigned int h[kThreads / kWave][2 * kBins * kCopies];
+  __shared__ unsigned int h[kHistWords];
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = threadIdx.x / kWave;
-  unsigned int* mine = h[wave];
-  for (unsigned int i = lane; i < 2 * kBins * kCopies; i += kWave) mine[i] = 0;
-  const unsigned int copy = lane % kCopies;
-  const unsigned long long chunks = 2 * a.chunks_per_plane;
-  const unsigned long long stride = (unsigned long long)gridDim.x * (kThreads / kWave);
-  unsigned long long chunk = (unsigned long long)blockIdx.x * (kThreads / kWave) + wave;
-  // one chunk ahead in registers: its loads are in flight while this one is counted
-  u32x4 cur0 = {0, 0, 0, 0}, cur1 = {0, 0, 0, 0};
-  if (chunk < chunks) {
-    cur0 = load_chunk_part(a, chunk, 8 * lane);
-    cur1 = load_chunk_part(a, chunk, 512 + 8 * lane);
-  }
-  for (; chunk < chunks; chunk += stride) {
-    const unsigned long long next = chunk + stride;
-    u32x4 nxt0 = {0, 0, 0, 0}, nxt1 = {0, 0, 0, 0};
-    if (next < chunks) {
-      nxt0 = load_chunk_part(a, next, 8 * lane);
-      nxt1 = load_chunk_part(a, next, 512 + 8 * lane);
-    }
-    const unsigned int plane = chunk >= a.chunks_per_plane ? 1u : 0u;
-    const uint32_t x[8] = {cur0.x, cur0.y, cur0.z, cur0.w, cur1.x, cur1.y, cur1.z, cur1.w};
+  zero_hist(h);
+  const unsigned int copy = lane;
+  const unsigned int total = 2 * a.chunks_per_plane;
+  const unsigned int batches = (total + kBatch - 1) / kBatch;
+  const unsigned int stride = gridDim.x * (kThreads / kWave);
+  unsigned int b0 = blockIdx.x * (kThreads / kWave) + wave;
+  if (b0 < batches) {
+    // batch b0 in flight, block ids of the next batch loaded one step ahead
+    Batch cur = load_batch(a, b0, load_ids(a, b0, total, lane), total, lane);
+    unsigned int b1 = b0 + stride;
+    long long id1 = b1 < batches ? load_ids(a, b1, total, lane) : 0;
+    for (;;) {
+      const bool more = b1 < batches;
+      Batch nxt;
+      if (more) nxt = load_batch(a, b1, id1, total, lane);
+      const unsigned int b2 = b1 + stride;
+      const long long id2 = more && b2 < batches ? load_ids(a, b2, total, lane) : 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      add_word(mine, plane, x[k], copy);
-      add_word(mine, plane, x[k] >> 16, copy);
+      for (int k = 0; k < kBatch; ++k) {
+        const unsigned int c = b0 * kBatch + k;
+        if (c >= total) break;
+        const unsigned int plane = c >= a.chunks_per_plane ? 1u : 0u;
+        const u32x4 x0 = cur.d[2 * k], x1 = cur.d[2 * k + 1];
+        const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          add_word(h, plane, x[q], copy);
+          add_word(h, plane, x[q] >> 16, copy);
+        }
+      }
+      if (!more) break;
+      cur = nxt;
+      b0 = b1;
+      b1 = b2;
+      id1 = id2;
     }
-    cur0 = nxt0;
-    cur1 = nxt1;
   }
-  __syncthreads();
   write_partial(h, a.partial);
 }
 
 // Any layout: one word per thread, grid-stride.
 __global__ __launch_bounds__(kThreads) void exponent_hist_generic(HistArgs a) {
-  __shared__ unsigned int h[kThreads / kWave][2 * kBins * kCopies];
+  __shared__ unsigned int h[kHistWords];
   const unsigned int lane = threadIdx.x & (kWave - 1);
-  unsigned int* mine = h[threadIdx.x / kWave];
-  for (unsigned int i = lane; i < 2 * kBins * kCopies; i += kWave) mine[i] = 0;
+  zero_hist(h);
   const unsigned long long plane_words = a.block_count * a.block_words;
   const unsigned long long total = 2 * plane_words;
   for (unsigned long long i = (unsigned long long)blockIdx.x * kThreads + threadIdx.x; i < total;
@@ -128,9 +186,8 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_generic(HistArgs a) {
     const unsigned long long within = in_plane - j * a.block_words;
     const uint32_t w = a.kv[plane * a.plane_stride + (unsigned long long)a.ids[j] * a.block_stride +
                             within];
-    add_word(mine, plane, w, lane % kCopies);
+    add_word(h, plane, w, lane);
   }
-  __syncthreads();
   write_partial(h, a.partial);
 }
 
@@ -146,15 +203,19 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_reduce(const unsigned 
 unsigned int partial_groups(unsigned long long block_count, unsigned long long block_words,
                             bool chunked) {
   const unsigned long long words = 2 * block_count * block_words;
-  const unsigned long long per_group = chunked ? 4ull * kChunk * 8 : (unsigned long long)kThreads * 64;
-  const unsigned long long g = (words + per_group - 1) / per_group;
-  return (unsigned int)(g < 1 ? 1 : (g > kMaxPartials ? kMaxPartials : g));
+  const unsigned long long per_group =
+      chunked ? (unsigned long long)(kThreads / kWave) * kBatch * kChunk * 8 : (unsigned long long)kThreads * 64;
+  unsigned long long g = (words + per_group - 1) / per_group;
+  g = g > kMaxPartials ? kMaxPartials : (g < 1 ? 1 : g);
+  // every group's share stays within the 16-bit counters (checked by the caller)
+  return (unsigned int)g;
 }
 
 bool chunk_layout(unsigned long long kv_ptr, unsigned long long plane_stride,
-                  unsigned long long block_stride, unsigned long long block_words) {
+                  unsigned long long block_stride, unsigned long long block_words,
+                  unsigned long long block_count) {
   return block_words % kChunk == 0 && kv_ptr % 16 == 0 && plane_stride % 8 == 0 &&
-         block_stride % 8 == 0;
+         block_stride % 8 == 0 && 2 * block_count * (block_words / kChunk) < (1ull << 31);
 }
 
 }  // namespace
@@ -191,7 +252,11 @@ extern "C" long long kvq_splitzip_exponent_histogram_paged(
     return 0;
   if (kvq_splitzip_exponent_histogram_workspace_bytes(block_count, block_words) > workspace_bytes)
     return 0;
-  const bool chunked = chunk_layout(kv_ptr, plane_stride, block_stride, block_words);
+  // a workgroup's share of the words must fit its 16-bit counters (every lane
+  // counts at most one word in 64 of the group's words)
+  if ((2 * block_count * block_words + kMaxPartials - 1) / kMaxPartials > kMaxWordsPerGroup / 2)
+    return 0;
+  const bool chunked = chunk_layout(kv_ptr, plane_stride, block_stride, block_words, block_count);
   HistArgs a{};
   a.kv = reinterpret_cast<const uint16_t*>(kv_ptr);
   a.ids = reinterpret_cast<const long long*>(block_ids_ptr);
@@ -200,7 +265,11 @@ extern "C" long long kvq_splitzip_exponent_histogram_paged(
   a.block_stride = block_stride;
   a.block_words = block_words;
   a.block_count = block_count;
-  a.chunks_per_plane = block_count * block_words / kChunk;
+  if (chunked) {
+    a.chunks_per_plane = (unsigned int)(block_count * block_words / kChunk);
+    a.chunks_per_block = (unsigned int)(block_words / kChunk);
+    a.cpb_magic = make_divider(a.chunks_per_block).m;
+  }
   const unsigned int groups = partial_groups(block_count, block_words, chunked);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   if (chunked)

@@ -676,6 +676,13 @@ def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_head
 # ---------------------------------------------------------------------------
 # exponent histograms (codebook fitting)
 
+def exponent_histogram_workspace_bytes(block_count: int, block_words: int) -> int:
+    lib = _load()
+    if lib is None or not hasattr(lib, "kvq_splitzip_exponent_histogram_workspace_bytes"):
+        raise RuntimeError(f"HIP codec library not loaded: {load_error()}")
+    return int(lib.kvq_splitzip_exponent_histogram_workspace_bytes(block_count, block_words))
+
+
 def exponent_histogram_paged(kv_layer, batch: PagedBatch, *, workspace=None, counts=None):
     """(2, 256) int64 device tensor: per K/V plane, the count of every bf16 exponent
     (bits 7..14) over all blocks of ``batch`` in the paged layer ``kv_layer`` (what
