@@ -202,3 +202,50 @@ def test_single_request_load_signature_matches_reference(sz, codebooks):
     assert np.array_equal(u16(target).reshape(2, pool, BW)[:, dst],
                           u16(kv).reshape(2, pool, BW)[:, src])
     assert codec.load_kv_layer(target, dst[:2], [bytes(payload.view)], meta) == (0, 0)
+
+
+def test_layer_travels_in_compressed_native_frames(sz, codebooks):
+    """save -> ready -> KVC1 frames on the wire -> parse -> restore into the
+    receiver's own blocks; plus one request sent as two KVC2 halves and a
+    raw_passthrough frame (tcp_data.py:612-652, vllm_connector.py:4785-4810)."""
+    from unchainkv_amd import frames
+
+    say("connector frames")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(9)
+    pool = 96
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.001), pool)
+    tables = disjoint_tables(rng, pool, [16, 20, 18])
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=RecordingTrace())
+    payloads = codec.ready(codec.save_kv_layer(5, kv, tables))
+    names = ["r0", "r1", "r2"]
+    wire = b"".join(b"".join(p) for p in SplitzipLayerCodec.frames(5, payloads, BW, "x", names))
+    # request r2 again, as two halves in KVC2 frames
+    halves = [tables[2][:9], tables[2][9:]]
+    half_payloads = codec.ready(codec.save_kv_layer(5, kv, halves))
+    for i, p in enumerate(half_payloads):
+        wire += b"".join(frames.pack_compressed_native(
+            "x", "r2h", 5, p.view, raw_block_size=4 * BW, block_count=18,
+            raw_bytes=4 * BW * 18, codec="splitzip_bf16", chunk_index=i, chunks_in_layer=2))
+    # request r1 as raw native words
+    raw = u16(kv[:, tables[1]]).tobytes()
+    wire += b"".join(frames.pack_compressed_native("x", "r1raw", 5, raw, raw_block_size=4 * BW,
+                                                   block_count=20, raw_bytes=len(raw),
+                                                   codec="raw_passthrough"))
+    bodies, at = [], 0
+    while at < len(wire):
+        body, used = frames.split_frame(memoryview(wire)[at:])
+        bodies.append(body)
+        at += used
+    assert len(bodies) == 6
+    recv_perm = rng.permutation(pool).tolist()
+    recv = {"r0": recv_perm[0:16], "r1": recv_perm[16:36], "r2": recv_perm[36:54],
+            "r2h": recv_perm[54:72], "r1raw": recv_perm[72:92]}
+    target = torch.zeros_like(kv)
+    got = codec.restore_frames(target, bodies, recv)
+    torch.cuda.synchronize()
+    src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
+    for name, t in (("r0", tables[0]), ("r1", tables[1]), ("r2", tables[2]),
+                    ("r2h", tables[2]), ("r1raw", tables[1])):
+        assert got[name] == (len(t), 4 * BW * len(t)), name
+        assert np.array_equal(dst[:, recv[name]], src[:, t]), name

@@ -33,7 +33,7 @@ import os
 import threading
 from dataclasses import dataclass, field
 
-from . import codec_format
+from . import codec_format, frames
 from .codebooks import summarize_symbol_counts
 from .trace import TraceWriter
 
@@ -468,6 +468,64 @@ class SplitzipLayerCodec:
         if mode == codec_format.MODE_RAW and encoded_bytes != raw_bytes + 1:
             return None
         return mode, raw_bytes, view
+
+    # ------------------------------------------------------------------
+    # wire frames (tcp_data.py:612-652 send, :282-361 receive)
+
+    @staticmethod
+    def frames(layer_index: int, payloads, block_words: int, transfer_id: str,
+               request_ids) -> list:
+        """Compressed-native KVC1 frames (one per request, parts as
+        ``frames.pack_compressed_native`` returns them) carrying the ready payloads
+        of a layer; ``request_ids[p.request]`` names each request."""
+        out = []
+        for p in payloads:
+            if p.view is None:
+                raise ValueError("payload is not ready")
+            meta = p.metadata(layer_index, block_words)
+            out.append(frames.pack_compressed_native(
+                transfer_id, request_ids[p.request], layer_index, p.view,
+                raw_block_size=meta["raw_block_size"], block_count=meta["block_count"],
+                raw_bytes=meta["raw_bytes"], codec=meta["codec"]))
+        return out
+
+    def restore_frames(self, kv_layer, bodies, block_tables: dict) -> dict:
+        """Restore received compressed-native frame bodies of one layer into the
+        blocks ``block_tables[request_id]``: KVC1 frames whole, KVC2 chunks
+        (chunks_in_layer 2) into their half of the block list with raw_bytes
+        raw_block_size * blocks (vllm_connector.py:4785-4810), raw_passthrough
+        payloads as raw words. Returns {request_id: (blocks, bytes)}; every frame of
+        a call must carry the same layer."""
+        parsed = [frames.parse_compressed_native(b) for b in bodies]
+        if not parsed:
+            return {}
+        layer = parsed[0].layer_index
+        if any(f.layer_index != layer for f in parsed):
+            raise ValueError("frames of different layers")
+        requests, keys = [], []
+        for f in parsed:
+            ids = [int(b) for b in block_tables[f.request_id]]
+            meta = f.metadata()
+            payload = f.payload
+            if f.chunks_in_layer > 1:
+                if f.chunks_in_layer != 2 or len(ids) % 2:
+                    continue
+                half = len(ids) // 2
+                ids = ids[f.chunk_index * half:(f.chunk_index + 1) * half]
+                meta = dict(meta, raw_bytes=f.raw_block_size * len(ids),
+                            encoded_bytes=f.encoded_bytes)
+            if f.codec == "raw_passthrough":
+                # the native words themselves: restored as a mode-6 payload
+                payload = bytes([codec_format.MODE_RAW]) + bytes(payload)
+                meta = dict(meta, encoded_bytes=len(payload))
+            requests.append((ids, payload, meta))
+            keys.append(f.request_id)
+        results = self.load_kv_layer_batch(layer, kv_layer, requests)
+        out: dict = {}
+        for key, (blocks, nbytes) in zip(keys, results):
+            prev = out.get(key, (0, 0))
+            out[key] = (prev[0] + blocks, prev[1] + nbytes)
+        return out
 
     def load_kv_layer(self, kv_layer, block_ids, payloads, metadata) -> tuple[int, int]:
         """Restore one request's layer payload into its blocks; (blocks, bytes) or
