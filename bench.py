@@ -62,7 +62,102 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-steps", type=int, default=0,
                    help="only run this many untimed steps (for rocprofv3), then exit")
+    p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="summarise two rocprofv3 --pmc runs of --profile-steps (FETCH_SIZE, "
+                        "then WRITE_SIZE) into HBM bytes per dispatch, print JSON and exit")
     return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic from hardware counters
+
+PROFILES = ROOT / "profiles"
+# kernels of one call of each direction (the roofline's unit of work)
+CALL_KERNELS = {
+    "encode": ("top16_encode_tile", "top16_encode_finalize"),
+    "decode": ("top16_decode_tile", "top16_patch_escapes"),
+    "attention": ("top16_attention_split", "top16_attention_combine"),
+}
+
+
+def calibration_copy(torch, device):
+    """One plain device copy of CALIBRATION_BYTES (read + write) in the profiled
+    process: the reference the FETCH_SIZE / WRITE_SIZE counters are scaled by."""
+    src = torch.empty(CALIBRATION_BYTES // 2, dtype=torch.int16, device=device)
+    src.fill_(3)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def _counter_rows(directory):
+    import csv
+
+    rows = []
+    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
+        with path.open() as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _short_name(kernel_name: str) -> str:
+    name = kernel_name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    for stop in ("<", "("):
+        name = name.split(stop)[0]
+    return name.split("::")[-1].strip()
+
+
+def pmc_summary(fetch_dir, write_dir) -> dict:
+    """Average FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of every kernel, each
+    scaled by what the same counter reads for the calibration copy (the last device
+    copy of the run: CALIBRATION_BYTES read and written): HBM bytes per dispatch =
+    1024 * (fetch / f_fetch + write / f_write)."""
+    per, calibration = {}, {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        last = None
+        for row in _counter_rows(directory):
+            if row["Counter_Name"] != counter:
+                continue
+            name = _short_name(row["Kernel_Name"])
+            value = float(row["Counter_Value"])
+            per.setdefault(name, {}).setdefault(counter, []).append(value)
+            if "copyBuffer" in name:
+                dispatch = int(row["Dispatch_Id"])
+                if last is None or dispatch > last[0]:
+                    last = (dispatch, value)
+        if last is None:
+            raise RuntimeError("no calibration copy kernel in the counter runs")
+        calibration[counter] = last[1] / (CALIBRATION_BYTES / 1024)
+    f_fetch, f_write = calibration["FETCH_SIZE"], calibration["WRITE_SIZE"]
+    kernels = {}
+    for name, counters in per.items():
+        if "FETCH_SIZE" not in counters or "WRITE_SIZE" not in counters:
+            continue
+        fetch = sum(counters["FETCH_SIZE"]) / len(counters["FETCH_SIZE"])
+        write = sum(counters["WRITE_SIZE"]) / len(counters["WRITE_SIZE"])
+        kernels[name] = {"dispatches": len(counters["FETCH_SIZE"]),
+                         "fetch_KiB": round(fetch, 1), "write_KiB": round(write, 1),
+                         "hbm_bytes": int(1024 * (fetch / f_fetch + write / f_write))}
+    return {"calibration": {"copy_bytes": CALIBRATION_BYTES, "fetch_factor": round(f_fetch, 4),
+                            "write_factor": round(f_write, 4)},
+            "kernels": kernels}
+
+
+def measured_traffic(workload: str, direction: str):
+    """HBM bytes of one call (its kernels' counter bytes) from the committed summary
+    profiles/pmc_<workload>.json, or None when there is none."""
+    path = PROFILES / f"pmc_{workload}.json"
+    if not path.exists():
+        return None, None
+    summary = json.loads(path.read_text())
+    kernels = summary.get("kernels", {})
+    names = CALL_KERNELS[direction]
+    if not all(n in kernels for n in names):
+        return None, path.name
+    return sum(kernels[n]["hbm_bytes"] for n in names), path.name
 
 
 # ---------------------------------------------------------------------------
@@ -472,7 +567,9 @@ def run_attention(args, torch, sz, workloads) -> int:
             step()
         torch.cuda.synchronize()
         verify_attention(torch, sz, w, 0)
-        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload}))
+        calibration_copy(torch, w["device"])
+        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload,
+                          "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
 
     for _ in range(args.warmup):
@@ -524,6 +621,7 @@ def run_attention(args, torch, sz, workloads) -> int:
     achieved = b_call / (call_ms * 1e-3) / 1e9
     raw_layer = batch.total_raw_bytes
     flops = 2 * 2 * ATTN_BATCH * q_heads * ATTN_CONTEXT * shape.head_dim
+    traffic, traffic_source = measured_traffic(args.workload, "attention")
     result = {
         "metric": METRIC,
         "value": round(raw_layer * layers / (ms_per_step * 1e-3) / 1e9, 2),
@@ -563,7 +661,8 @@ def run_attention(args, torch, sz, workloads) -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes_per_call": int(b_call),
             "ms_per_call": round(call_ms, 5),
         },
@@ -580,6 +679,9 @@ def run_attention(args, torch, sz, workloads) -> int:
 
 def main() -> int:
     args = parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                           "(per-request and per-layer payloads shard with no exchange)"}))
@@ -615,14 +717,7 @@ def main() -> int:
             step()
         torch.cuda.synchronize()
         verify(torch, w)
-        # calibration for HBM counters: one plain copy of a known size (256 MiB
-        # read + 256 MiB written) in the same process
-        src = torch.empty(CALIBRATION_BYTES // 2, dtype=torch.int16, device=w["device"])
-        src.fill_(3)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
+        calibration_copy(torch, w["device"])
         print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload,
                           "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
@@ -688,6 +783,8 @@ def main() -> int:
         kernels = {"encode": "top16 encode + palette_presence/reduce/encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
+    traffic, traffic_source = (None, None) if overflowed else measured_traffic(args.workload,
+                                                                                 dominant[0])
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -737,7 +834,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(dominant[2] / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes_per_call": int(dominant[3]),
             "ms_per_call": round(dominant[1], 5),
         },

@@ -334,8 +334,18 @@ top16_attention_split(AttnArgs a) {
   __shared__ unsigned int sBad[4];
 
   const unsigned int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const unsigned int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // work item = (sequence, split, head pair) with the pair fastest, each XCD taking
+  // a contiguous run of items (xcd_remap). Waves 0-1 serve head 2p and waves 2-3
+  // head 2p+1 over the same two token ranges: the two heads' 64-byte code rows
+  // share one 128-byte cache line, which the two waves then read together.
   const unsigned int hkv = a.kv_heads;
+  const unsigned int pairs = (hkv + 1) / 2;
+  const unsigned int w_item = xcd_remap(blockIdx.x, gridDim.x);
+  const unsigned int hp = w_item % pairs;
+  const unsigned int split = (w_item / pairs) % a.splits;
+  const unsigned int b = w_item / (pairs * a.splits);
+  const unsigned int h = 2 * hp + (wave >> 1);
+  const bool head_ok = h < hkv;  // an odd head count leaves the last pair half empty
   const unsigned int ctx = a.ctx[b];
   const unsigned char* payload = a.payloads + a.offset[b];
   const unsigned long long n = 2ull * a.span[b] * hkv * kHeadDim;
@@ -347,14 +357,14 @@ top16_attention_split(AttnArgs a) {
                                     ((unsigned int)payload[3] << 16) |
                                     ((unsigned int)payload[4] << 24);
   const unsigned int row_words = hkv * kHeadDim;  // payload words per token per plane
-  const unsigned int wb = (split * 4 + wave) * a.tokens_per_wave;
+  const unsigned int wb = (split * 2 + (wave & 1)) * a.tokens_per_wave;
   StepConst c;
   c.entries = entries;
   c.count = min(header_count, cap);
   c.half = (unsigned int)(n / 2);
   c.row_words = row_words;
   c.head = h;
-  c.we = min(ctx, wb + a.tokens_per_wave);
+  c.we = head_ok ? min(ctx, wb + a.tokens_per_wave) : wb;
   c.scale_log2 = a.scale_log2;
   c.tab_k = sTab[0];
   c.tab_v = sTab[1];
@@ -374,7 +384,7 @@ top16_attention_split(AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       u32x4 v = {0, 0, 0, 0};
-      if (col < kGroup) v = *reinterpret_cast<const u32x4*>(qrow + 8 * ks);
+      if (col < kGroup && head_ok) v = *reinterpret_cast<const u32x4*>(qrow + 8 * ks);
       qb[ks] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -415,7 +425,7 @@ top16_attention_split(AttnArgs a) {
     }
   }
 
-  // ---- merge the 4 waves (m, l, acc per head), then write this split's partial ----
+  // ---- merge each head's 2 waves (m, l, acc), then write the split's partials ----
   float l_run = w.l_run;
   const float m_run = w.m_run;
   l_run += __shfl_xor(l_run, 16, 64);
@@ -436,34 +446,33 @@ top16_attention_split(AttnArgs a) {
   }
   __syncthreads();
   const bool bad = (sBad[0] | sBad[1] | sBad[2] | sBad[3]) != 0;
-  float* out = a.partial + (((unsigned long long)b * hkv + h) * a.splits + split) * kGroup * kPartial;
   (void)grp;
   {
-    const unsigned int head = tid / 64, d0 = (tid % 64) * 2;
-    float mw[4], big = -INFINITY;
+    // thread t: head 2p + (t >> 7), query row (t >> 5) & 3, dims 4 * (t & 31) .. +3
+    const unsigned int m = tid >> 7, j = (tid >> 5) & 3, d0 = (tid & 31) * 4;
+    const unsigned int hm = 2 * hp + m;
+    if (hm < hkv) {
+      const float* s0 = sm + ((2 * m) * kGroup + j) * kPartial;
+      const float* s1 = sm + ((2 * m + 1) * kGroup + j) * kPartial;
+      const float m0 = s0[0], m1 = s1[0];
+      const float big = fmaxf(m0, m1);
+      float l_sum = 0.f, o[4] = {0.f, 0.f, 0.f, 0.f};
+      if (big != -INFINITY) {
+        // a wave with no tokens has m = -inf and weight 0
+        const float w0 = m0 == -INFINITY ? 0.f : exp2f(m0 - big);
+        const float w1 = m1 == -INFINITY ? 0.f : exp2f(m1 - big);
+        l_sum = s0[1] * w0 + s1[1] * w1;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      mw[w] = sm[(w * kGroup + head) * kPartial];
-      big = fmaxf(big, mw[w]);
-    }
-    float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
-    if (big != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        if (mw[w] == -INFINITY) continue;  // a wave with no tokens
-        const float* src = sm + (w * kGroup + head) * kPartial;
-        const float wgt = exp2f(mw[w] - big);
-        l_sum += src[1] * wgt;
-        o0 += src[2 + d0] * wgt;
-        o1 += src[3 + d0] * wgt;
+        for (int k = 0; k < 4; ++k) o[k] = s0[2 + d0 + k] * w0 + s1[2 + d0 + k] * w1;
       }
-    }
-    float* dst = out + head * kPartial;
-    dst[2 + d0] = bad ? NAN : o0;
-    dst[3 + d0] = bad ? NAN : o1;
-    if (tid % 64 == 0) {
-      dst[0] = bad ? NAN : big;
-      dst[1] = bad ? NAN : l_sum;
+      float* dst = a.partial +
+                   ((((unsigned long long)b * hkv + hm) * a.splits + split) * kGroup + j) * kPartial;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) dst[2 + d0 + k] = bad ? NAN : o[k];
+      if ((tid & 31) == 0) {
+        dst[0] = bad ? NAN : big;
+        dst[1] = bad ? NAN : l_sum;
+      }
     }
   }
 }
@@ -526,16 +535,18 @@ struct SplitPlan {
 // Context splits per (sequence, kv head): the count whose workgroups fill whole
 // rounds of the resident slots with the fewest tokens per wave (a wave walks its
 // range serially; a round that is partly empty wastes the rest of the chip).
-SplitPlan plan_splits(unsigned long long pairs, unsigned long long max_ctx) {
+SplitPlan plan_splits(unsigned long long groups, unsigned long long max_ctx) {
+  // groups: workgroups per split (sequences x head pairs); a split gives every head
+  // 2 token ranges of tokens_per_wave
   const unsigned long long slots = resident_workgroups();
   constexpr unsigned long long kWaveOverhead = 32;  // start-up cost in token steps
   SplitPlan best{1, 0};
   unsigned long long best_cost = ~0ull;
   for (unsigned int s = 1; s <= kMaxSplits; ++s) {
-    const unsigned long long per_wave = (max_ctx + 4ull * s - 1) / (4ull * s);
+    const unsigned long long per_wave = (max_ctx + 2ull * s - 1) / (2ull * s);
     const unsigned long long tpw = (per_wave + kStep - 1) / kStep * kStep;
-    if (s > 1 && (unsigned long long)(s - 1) * 4 * tpw >= max_ctx) break;  // empty splits
-    const unsigned long long rounds = (pairs * s + slots - 1) / slots;
+    if (s > 1 && (unsigned long long)(s - 1) * 2 * tpw >= max_ctx) break;  // empty splits
+    const unsigned long long rounds = (groups * s + slots - 1) / slots;
     const unsigned long long cost = rounds * (tpw + kWaveOverhead);
     if (cost < best_cost) {
       best_cost = cost;
@@ -553,7 +564,7 @@ extern "C" unsigned long long kvq_splitzip_top16_decode_attention_workspace_byte
     unsigned long long batch, unsigned long long kv_heads, unsigned long long max_ctx) {
   if (batch == 0 || kv_heads == 0 || max_ctx == 0) return 0;
   const unsigned long long per_launch = batch < kMaxSeqs ? batch : kMaxSeqs;
-  const SplitPlan plan = plan_splits(per_launch * kv_heads, max_ctx);
+  const SplitPlan plan = plan_splits(per_launch * ((kv_heads + 1) / 2), max_ctx);
   return per_launch * kv_heads * plan.splits * kGroup * kPartial * sizeof(float);
 }
 
@@ -587,7 +598,7 @@ extern "C" long long kvq_splitzip_top16_decode_attention(
       workspace_bytes)
     return 0;
   const unsigned long long per_launch = batch < kMaxSeqs ? batch : kMaxSeqs;
-  const SplitPlan plan = plan_splits(per_launch * kv_heads, max_ctx);
+  const SplitPlan plan = plan_splits(per_launch * ((kv_heads + 1) / 2), max_ctx);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < batch; first += kMaxSeqs) {
     const unsigned int count = (unsigned int)(batch - first < kMaxSeqs ? batch - first : kMaxSeqs);
@@ -609,7 +620,8 @@ extern "C" long long kvq_splitzip_top16_decode_attention(
       a.ctx[r] = (unsigned int)ctx;
       a.span[r] = (unsigned int)((ctx + block_tokens - 1) / block_tokens * block_tokens);
     }
-    hipLaunchKernelGGL(top16_attention_split, dim3(plan.splits, (unsigned int)kv_heads, count),
+    hipLaunchKernelGGL(top16_attention_split,
+                       dim3(plan.splits * (unsigned int)((kv_heads + 1) / 2) * count),
                        dim3(kThreads), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("top16_attention_split", st);
