@@ -55,7 +55,7 @@ namespace {
 constexpr int kFinGroups = 8;                          // finalize workgroups per payload
 constexpr int kFinPerThread = 8;                       // tile counts per thread per pass
 constexpr int kFinChunk = kThreads * kFinPerThread;    // tiles scanned per finalize pass
-constexpr int kFinPreload = 4;                         // staged escapes loaded with the counts
+constexpr int kFinPreload = 8;                         // staged escapes loaded with the counts
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
   return (n + 199) / 200;
@@ -516,6 +516,19 @@ __device__ __forceinline__ void encode_run8(const uint32_t* x, const unsigned ch
   }
 }
 
+// Zeroes the payload's escape section in 4 KiB spans of 16-byte stores, one span per
+// tile of the payload from its first tile on (a section is at most n / 40 + 5 bytes,
+// fewer than the payload's 4096-word tiles can cover): wide, line-filling stores
+// instead of a sliver per tile.
+__device__ __forceinline__ void zero_escape_span(unsigned char* payload, unsigned long long n,
+                                                 unsigned int local_tile) {
+  const unsigned long long len = 5 * escape_capacity(n);
+  const unsigned long long lo = (unsigned long long)local_tile * (kThreads * 16);
+  if (lo >= len) return;
+  const unsigned long long hi = min(lo + kThreads * 16, len);
+  zero_fill(payload + 5 + n + (n + 1) / 2 + lo, hi - lo);
+}
+
 template <bool kIds>
 __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
   __shared__ uint32_t s_tab[64];  // this tile's plane, 4 code bytes per dword
@@ -606,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
       ++idx;
     }
   }
-  zero_escape_share(t.payload, t.n, t.local_tile, t.payload_tiles);
+  zero_escape_span(t.payload, t.n, t.local_tile);
 }
 
 // Per-byte 0xFF/0x00 masks from bit 3 of each byte of s (byte permute with the
@@ -775,16 +788,21 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       } else {
         unsigned long long start, end;
         tile_range(a, d, chunk0 + own, n, start, end);
-        for (unsigned int q = 0; q < c && base + q < cap; ++q) {
-          unsigned int v = pre[0];
-          if (q < (unsigned int)kFinPreload) {
+        // batches of kFinPreload entries: the first came with the counts, later
+        // batches are loaded together before they are stored
+        for (unsigned int q0 = 0; q0 < c && base + q0 < cap; q0 += kFinPreload) {
+          unsigned int v[kFinPreload];
 #pragma unroll
-            for (int e = 1; e < kFinPreload; ++e)
-              if (q == (unsigned int)e) v = pre[e];
-          } else {
-            v = st[q];
+          for (int e = 0; e < kFinPreload; ++e) {
+            const unsigned int q = q0 + e;
+            v[e] = q0 == 0 ? pre[e] : (q < c ? st[q] : 0u);
           }
-          put_entry(entries, base + q, (unsigned int)(start + (v >> 8)), v & 0xFF);
+#pragma unroll
+          for (int e = 0; e < kFinPreload; ++e) {
+            const unsigned int q = q0 + e;
+            if (q < c && base + q < cap)
+              put_entry(entries, base + q, (unsigned int)(start + (v[e] >> 8)), v[e] & 0xFF);
+          }
         }
       }
     }
