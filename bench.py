@@ -338,6 +338,46 @@ def time_histogram(torch, sz, w, reps: int = 10):
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
+def time_writeback(torch, sz, w, reps: int = 10):
+    """Codec writeback (payloads moved into the sender's own contiguous block runs)
+    per layer call, into a scratch copy of each layer so the sender's blocks stay
+    intact for the next step; checked byte for byte on layer 0. ``None`` when a
+    request's blocks are not one contiguous run (the reference skips those)."""
+    send = w["send"]
+    if any(sz.contiguous_run(t) is None for t in send.block_tables):
+        return None
+    members = list(range(send.payload_count))
+    scratch = torch.empty_like(w["kv"][0])
+    status = torch.empty(len(members), dtype=torch.uint8, device=w["device"])
+    moved, _ = sz.writeback_top16_paged(w["payloads"][0], send, scratch, members, status=status)
+    torch.cuda.synchronize()
+    flat = scratch.view(-1).view(torch.uint8)
+    plane = 2 * scratch.stride(0)
+    for r, (off, size) in enumerate(zip(send.out_offsets, send.encoded_bytes)):
+        start, count = sz.contiguous_run(send.block_tables[r])
+        seg = 2 * count * send.block_words
+        k = 2 * start * scratch.stride(1)
+        payload = w["payloads"][0][off:off + size]
+        head = min(size, seg)
+        if int(payload[0]) == 5 and not (
+                torch.equal(flat[k:k + head], payload[:head])
+                and torch.equal(flat[plane + k:plane + k + size - head], payload[head:])):
+            raise RuntimeError("writeback bytes differ from the payload")
+    layers = min(w["layers"], 8)
+    stream = torch.cuda.current_stream(w["device"])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        for layer in range(layers):
+            sz.writeback_top16_paged(w["payloads"][layer], send, scratch, members, status=status)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * layers)
+    gbps = 2 * moved / (ms * 1e-3) / 1e9  # payload read + written once
+    return {"ms_per_layer_call": round(ms, 5), "bytes_moved": moved, "hbm_GBps": round(gbps, 2),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle's C codec, test infrastructure, timed on this host)
 
@@ -752,6 +792,7 @@ def main() -> int:
     enc_call = sum(enc_ms) / len(enc_ms)
     dec_call = sum(dec_ms) / len(dec_ms)
     hist = time_histogram(torch, sz, w)
+    writeback = time_writeback(torch, sz, w)
 
     send = w["send"]
     raw_layer = send.total_raw_bytes
@@ -824,6 +865,8 @@ def main() -> int:
             "ms_per_layer_call": round(dec_call, 5),
         },
         "exponent_histogram": hist,
+        "codec_writeback": writeback if writeback is not None else
+        "not applicable: block tables are not contiguous runs",
         "compression_ratio": round(raw_layer / final, 5),
         "escapes_per_layer": round(escapes / layers, 1),
         "overflowed_payloads": overflowed,

@@ -206,6 +206,32 @@ long long kvq_splitzip_exponent_histogram_paged(
     unsigned long long stream_ptr);
 
 /* ------------------------------------------------------------------------------
+ * Codec writeback: encoded payloads moved into the sending request's own KV
+ * blocks so the codec buffer is free before the host copy (replaces the two
+ * segment copies per request of _try_splitzip_writeback,
+ * src/unchain_kv/vllm_connector.py:3460-3563, segments from
+ * _kv_writeback_segments :3720-3738).
+ * ---------------------------------------------------------------------------- */
+
+/* For r < payload_count: if byte 0 of payload r (payloads_ptr +
+ * payload_offsets[r], encoded_bytes[r] bytes) is 5, its bytes are written to the
+ * K-plane run of blocks [run_starts[r], run_starts[r] + run_blocks[r]) and, past
+ * that run's 2 * run_blocks[r] * block_words bytes, to the V-plane run of the same
+ * blocks (kv_ptr: bf16 layer, plane_stride and block_stride in elements; a run of
+ * several blocks needs block_stride == block_words). Any other mode byte (255, an
+ * overflow) leaves the blocks unchanged. status_ptr: device u8 array, [r] = byte 0
+ * of payload r. Host arrays of payload_count entries. Returns the sum of
+ * encoded_bytes, 0 on a failed precondition (a payload longer than its two runs,
+ * runs overlapping each other or the payload range), -1 on a launch error. */
+long long kvq_splitzip_top16_writeback_paged(
+    unsigned long long payloads_ptr, const unsigned long long* payload_offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, const unsigned long long* run_starts,
+    const unsigned long long* run_blocks, unsigned long long status_ptr,
+    unsigned long long stream_ptr);
+
+/* ------------------------------------------------------------------------------
  * Fused Top-16 decode + decode attention (no counterpart in the reference, whose
  * consumer decodes each payload into the paged KV cache and then runs attention;
  * scripts/bench_codec_attention.py times that pairing).

@@ -111,6 +111,27 @@ def test_config_from_environment():
     assert cfg.top16_max_cooldown == 1  # clamped to at least 1, as the reference does
     default = CodecConfig.from_env({})
     assert not default.top16 and default.top16_max_cooldown == 32 and not default.fixed5_layers
+    # codec writeback defaults to on with Top-16 (vllm_connector.py:406-412)
+    assert cfg.writeback and not default.writeback
+    assert not CodecConfig.from_env({"UNCHAIN_KV_SPLITZIP_TOP16": "1",
+                                     "UNCHAIN_KV_CODEC_WRITEBACK": "0"}).writeback
+    codec = SplitzipLayerCodec(cfg)
+    assert codec.codec_writeback and codec.codec_writeback_overwrite
+    cfg.preserve_source = True
+    assert not SplitzipLayerCodec(cfg).codec_writeback_overwrite
+
+
+def test_writeback_skips_fragmented_tables():
+    from unchainkv_amd.connector import LayerPayload
+
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace)
+    members = [LayerPayload(0, [4, 5, 6], 3 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100),
+               LayerPayload(1, [7, 9, 10], 3 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100),
+               LayerPayload(2, [11], 1 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100)]
+    assert codec._writeback_members(members, 3) == [0, 2]
+    assert trace.rows == [("codec_writeback_skip", {"layer": 3, "reason": "fragmented",
+                                                     "segments": 4})]
 
 
 torch = pytest.importorskip("torch")

@@ -318,3 +318,47 @@ def test_library_declines_bad_preconditions_without_launching():
     fx.restype = ctypes.c_longlong
     assert fx(8, 8, 1000, 1 << 20, 0, 7) == 0
     assert fx(8, 8, 1000, 100, 0, 6) == 0
+
+
+def test_writeback_declines_bad_layouts_without_launching():
+    """The writeback's host checks (vllm_connector.py:3479-3502: one contiguous run
+    per request, enough room, no aliasing) decline before any launch."""
+    from unchainkv_amd import _build
+
+    lib = ctypes.CDLL(str(_build.LIB_PATH))
+    u = ctypes.c_ulonglong
+    arr = lambda *v: (u * len(v))(*v)  # noqa: E731
+    wb = lib.kvq_splitzip_top16_writeback_paged
+    wb.argtypes = [u, ctypes.POINTER(u), ctypes.POINTER(u), u, u, u, u, u, ctypes.POINTER(u),
+                   ctypes.POINTER(u), u, u]
+    wb.restype = ctypes.c_longlong
+    kv, payloads, status = 1 << 40, 1 << 44, 1 << 46
+    plane, bw = 64 * 100, 100  # 64 blocks of 100 words per plane
+    # a payload longer than its two runs (2 x 2 x 100 bytes for one block)
+    assert wb(payloads, arr(0), arr(401), 1, kv, plane, bw, bw, arr(3), arr(1), status, 0) == 0
+    # two requests whose runs overlap (blocks 3..4 and 4..5)
+    assert wb(payloads, arr(0, 1000), arr(300, 300), 2, kv, plane, bw, bw, arr(3, 4), arr(2, 2),
+              status, 0) == 0
+    # a run of several blocks needs blocks packed back to back
+    assert wb(payloads, arr(0), arr(300), 1, kv, plane, 2 * bw, bw, arr(3), arr(2), status, 0) == 0
+    # the payload buffer lies inside a destination run
+    assert wb(kv + 2 * 3 * bw, arr(0), arr(300), 1, kv, plane, bw, bw, arr(3), arr(2), status,
+              0) == 0
+    # empty run, empty payload, null pointers
+    assert wb(payloads, arr(0), arr(300), 1, kv, plane, bw, bw, arr(3), arr(0), status, 0) == 0
+    assert wb(payloads, arr(0), arr(0), 1, kv, plane, bw, bw, arr(3), arr(2), status, 0) == 0
+    assert wb(payloads, arr(0), arr(300), 1, kv, plane, bw, bw, arr(3), arr(2), 0, 0) == 0
+    assert wb(payloads, arr(0), arr(300), 0, kv, plane, bw, bw, arr(3), arr(2), status, 0) == 0
+
+
+def test_contiguous_run_and_runs():
+    from unchainkv_amd import splitzip_cuda
+    from unchainkv_amd.connector import _contiguous_runs
+
+    assert splitzip_cuda.contiguous_run([4, 5, 6]) == (4, 3)
+    assert splitzip_cuda.contiguous_run([9]) == (9, 1)
+    assert splitzip_cuda.contiguous_run([4, 6]) is None
+    assert splitzip_cuda.contiguous_run([5, 4]) is None
+    assert splitzip_cuda.contiguous_run([]) is None
+    assert _contiguous_runs([]) == ()
+    assert _contiguous_runs([3, 4, 5, 9, 10, 2]) == ((3, 3), (9, 2), (2, 1))

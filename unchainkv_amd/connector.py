@@ -12,6 +12,11 @@ This module keeps that codec behaviour and its knobs, batched per layer:
 * save (``save_kv_layer``): every request of the layer is encoded by one batched
   launch per codec (gathering the blocks in the kernel), then copied to pinned host
   memory on the current stream;
+* codec writeback (``CodecConfig.writeback`` without ``preserve_source``,
+  :3460-3563): a Top-16 payload whose request holds one contiguous run of blocks is
+  moved into those blocks (K-plane run, then V-plane run) by one launch per layer
+  and copied to the host from there, so the codec buffer is released at once;
+  requests with fragmented block tables are skipped, as in the reference;
 * ready (``ready``): after the copy, Top-16 (and fixed5) payloads whose byte 0 is
   255 are re-encoded as fixed6, and fixed6 overflow falls back to raw mode 6
   (``[6] + raw bytes``) (:4526-4665);
@@ -24,7 +29,11 @@ Everything runs on the HIP library; there is no CPU codec path. Modes 0, 1 and 2
 Payloads below 1 MiB use fixed6, as the reference does when its codec buffer pool
 is in use. The KV blocks of a saved layer must stay unchanged until ``ready``
 returns: the fallback re-encodes read them again (the reference keeps a gathered
-copy instead).
+copy instead). The writeback therefore skips an overflowed payload on the GPU (its
+mode byte is checked there), leaving its blocks intact for the fixed6 re-encode;
+the blocks of a payload that was written back hold the payload afterwards, which
+is why the reference only overwrites when neither prefix caching nor chunked
+prefill may reuse them (``preserve_source``).
 """
 
 from __future__ import annotations
@@ -58,21 +67,39 @@ class CodecConfig:
     fixed5_layers: set = field(default_factory=set)  # UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS
     top16_max_cooldown: int = 32          # UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN
     native_decode: bool = True            # UNCHAIN_KV_SPLITZIP_NATIVE_DECODE (decode is always GPU)
+    writeback: bool = False               # UNCHAIN_KV_CODEC_WRITEBACK (default: on with Top-16)
+    # prefix caching or chunked prefill may reuse the sender's blocks: no overwrite
+    # (the reference derives this from the vLLM config, vllm_connector.py:442-444)
+    preserve_source: bool = False
 
     @classmethod
     def from_env(cls, env=None) -> "CodecConfig":
         env = os.environ if env is None else env
+        top16 = _env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16", 0) > 0
         return cls(
-            top16=_env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16", 0) > 0,
+            top16=top16,
             fixed5=_env_int(env, "UNCHAIN_KV_SPLITZIP_FIXED5", 0) > 0,
             fixed5_layers=_env_int_set(env, "UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS"),
             top16_max_cooldown=max(1, _env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN", 32)),
             native_decode=_env_int(env, "UNCHAIN_KV_SPLITZIP_NATIVE_DECODE", 1) > 0,
+            writeback=_env_int(env, "UNCHAIN_KV_CODEC_WRITEBACK", int(top16)) > 0,
         )
 
 
 # bits of a payload as the reference's _SplitzipCudaPayload records them
 BITS_TOP16, BITS_FIXED5, BITS_FIXED6, BITS_RAW = 4, 5, 6, 16
+
+
+def _contiguous_runs(values) -> tuple[tuple[int, int], ...]:
+    """(start, count) runs of consecutive ids, in order (vllm_connector.py:148-161)."""
+    runs = []
+    for value in values:
+        value = int(value)
+        if runs and value == runs[-1][0] + runs[-1][1]:
+            runs[-1][1] += 1
+        else:
+            runs.append([value, 1])
+    return tuple((start, count) for start, count in runs)
 _MODE_OF_BITS = {BITS_TOP16: codec_format.MODE_TOP16, BITS_FIXED5: codec_format.MODE_FIXED5,
                  BITS_FIXED6: codec_format.MODE_FIXED6, BITS_RAW: codec_format.MODE_RAW}
 
@@ -91,8 +118,11 @@ class LayerPayload:
     fallback: bool = False
     encoded_bytes: int = 0
     view: memoryview | None = None
+    writeback: bool = False          # moved into its own blocks before the host copy
+    writeback_segments: int = 0
     _group: int = -1
     _offset: int = 0
+    _status: int = -1                # index of its mode byte in the group's status copy
 
     def metadata(self, layer_index: int, block_words: int) -> dict:
         """Receiver metadata of a compressed-native layer payload."""
@@ -107,7 +137,8 @@ class PendingLayer:
     kv_layer: object
     block_words: int
     payloads: list
-    groups: list = field(default_factory=list)  # (host tensor, event)
+    groups: list = field(default_factory=list)  # (host tensor, event, device buffer, status)
+    started: float = 0.0
 
 
 class SplitzipLayerCodec:
@@ -133,6 +164,8 @@ class SplitzipLayerCodec:
         self._splitzip_top16_epochs: dict[int, int] = {}
         self._splitzip_top16_lock = threading.Lock()
         self._traced_bf16_exponents: set[tuple[str, int]] = set()
+        self.codec_writeback = config.writeback and config.top16
+        self.codec_writeback_overwrite = self.codec_writeback and not config.preserve_source
 
     # ------------------------------------------------------------------
     # library
@@ -302,7 +335,7 @@ class SplitzipLayerCodec:
 
     def _encode_group(self, kind: int, kv_layer, members: list, block_words: int, layer_index: int):
         """Batched encode of `members` with codec `kind`; returns (device buffer,
-        offsets, sizes) or None when the library declines."""
+        offsets, sizes, batch) or None when the library declines."""
         sz = self._lib()
         batch = sz.PagedBatch([p.block_ids for p in members], block_words, kv_layer.device)
         if kind == BITS_TOP16:
@@ -311,11 +344,11 @@ class SplitzipLayerCodec:
                 return None
             out = batch.new_payload_buffer()
             got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(), tables=tables)
-            return (out, batch.out_offsets, batch.encoded_bytes) if got else None
+            return (out, batch.out_offsets, batch.encoded_bytes, batch) if got else None
         offsets, sizes, _ = batch.palette_layout(kind)
         out = batch.new_palette_buffer(kind)
         got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind)
-        return (out, offsets, sizes) if got else None
+        return (out, offsets, sizes, batch) if got else None
 
     @staticmethod
     def _stage(pending: PendingLayer, device_buffer, torch) -> int:
@@ -324,8 +357,76 @@ class SplitzipLayerCodec:
         host.copy_(device_buffer, non_blocking=True)
         event = torch.cuda.Event()
         event.record(torch.cuda.current_stream(device_buffer.device))
-        pending.groups.append((host, event, device_buffer))
+        pending.groups.append((host, event, device_buffer, None))
         return len(pending.groups) - 1
+
+    def _writeback_members(self, members: list, layer_index: int) -> list[int]:
+        """Indices of the Top-16 members whose blocks are one contiguous run (the
+        reference skips fragmented tables, vllm_connector.py:3479-3488)."""
+        picks = []
+        for i, p in enumerate(members):
+            runs = _contiguous_runs(p.block_ids)
+            if len(runs) != 1:
+                self.trace.event("codec_writeback_skip", layer=layer_index, reason="fragmented",
+                                 segments=len(runs) * 2)
+                continue
+            if not 0 < p.encoded_bytes < p.raw_bytes:
+                continue
+            picks.append(i)
+        return picks
+
+    def _stage_writeback(self, pending: PendingLayer, members: list, result, torch) -> bool:
+        """Codec writeback of the Top-16 group (vllm_connector.py:3460-3563): moves
+        the eligible payloads into their own blocks with one launch, then copies every
+        payload of the group to pinned host memory, the moved ones from their blocks
+        (first the K-plane run, then the V-plane run) and the rest from the codec
+        buffer, together with each moved payload's mode byte. Returns False (nothing
+        staged) when no payload qualifies or the library declines."""
+        out, offsets, sizes, batch = result
+        layer = pending.layer_index
+        picks = self._writeback_members(members, layer)
+        if not picks:
+            return False
+        sz = self._lib()
+        kv_layer = pending.kv_layer
+        moved, status = sz.writeback_top16_paged(out, batch, kv_layer, picks)
+        if not moved:
+            for i in picks:
+                self.trace.event("codec_writeback_skip", layer=layer, reason="alias")
+            return False
+        host = torch.empty(out.numel(), dtype=torch.uint8, pin_memory=True)
+        status_host = torch.empty(len(picks), dtype=torch.uint8, pin_memory=True)
+        flat = kv_layer.view(-1).view(torch.uint8)
+        plane = 2 * kv_layer.stride(0)
+        picked = set(picks)
+        for i, p in enumerate(members):
+            off, size = int(offsets[i]), int(sizes[i])
+            if i not in picked:
+                host[off:off + size].copy_(out[off:off + size], non_blocking=True)
+                continue
+            start, count = _contiguous_runs(p.block_ids)[0]
+            seg = 2 * count * pending.block_words
+            k = 2 * start * kv_layer.stride(1)
+            head = min(size, seg)
+            host[off:off + head].copy_(flat[k:k + head], non_blocking=True)
+            if size > seg:
+                host[off + seg:off + size].copy_(flat[plane + k:plane + k + size - seg],
+                                                 non_blocking=True)
+        status_host.copy_(status[:len(picks)], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(kv_layer.device))
+        # the codec buffer is released now unless an unmoved payload is still read from it
+        keep = out if len(picks) < len(members) else None
+        pending.groups.append((host, event, keep, status_host))
+        group = len(pending.groups) - 1
+        for j, i in enumerate(picks):
+            p = members[i]
+            p.writeback, p.writeback_segments, p._status = True, 2, j
+            self.trace.event("codec_writeback_submitted", layer=layer, bytes=p.encoded_bytes,
+                             raw_bytes=p.raw_bytes, segments=2)
+        for p, off, size in zip(members, offsets, sizes):
+            p._group, p._offset, p.encoded_bytes = group, int(off), int(size)
+        return True
 
     def save_kv_layer(self, layer_index: int, kv_layer, block_tables) -> PendingLayer:
         """Encode every request's blocks of one layer (the save hook's codec step) and
@@ -357,7 +458,11 @@ class SplitzipLayerCodec:
                     p.bits, p.fallback = BITS_FIXED6, True
                 self.trace.event("splitzip_top16_fallback", layer=layer_index)
             else:
-                self._assign(pending, top, result, torch)
+                for p, size in zip(top, result[2]):
+                    p.encoded_bytes = int(size)
+                if not (self.codec_writeback_overwrite
+                        and self._stage_writeback(pending, top, result, torch)):
+                    self._assign(pending, top, result, torch)
         five = [p for p in payloads if p.bits == BITS_FIXED5]
         if five:
             result = self._encode_group(BITS_FIXED5, kv_layer, five, block_words, layer_index)
@@ -381,7 +486,7 @@ class SplitzipLayerCodec:
         return pending
 
     def _assign(self, pending, members, result, torch) -> None:
-        out, offsets, sizes = result
+        out, offsets, sizes, _ = result
         group = self._stage(pending, out, torch)
         for p, off, size in zip(members, offsets, sizes):
             p._group, p._offset, p.encoded_bytes = group, int(off), int(size)
@@ -392,12 +497,22 @@ class SplitzipLayerCodec:
     def ready(self, pending: PendingLayer) -> list:
         import torch
 
-        for host, event, _ in pending.groups:
+        for host, event, _, _ in pending.groups:
             event.synchronize()
         layer = pending.layer_index
         for p in pending.payloads:
             if p._group >= 0:
-                host = pending.groups[p._group][0]
+                host, _, _, status = pending.groups[p._group]
+                if p.writeback:
+                    # a payload the GPU did not move (an overflow) left its blocks
+                    # intact and the host bytes are not the payload: mark it 255
+                    mode = int(status[p._status])
+                    overflow = mode != codec_format.MODE_TOP16
+                    if overflow:
+                        host[p._offset] = codec_format.MODE_OVERFLOW
+                    self.trace.event("codec_writeback_done", layer=layer, bytes=p.encoded_bytes,
+                                     raw_bytes=p.raw_bytes, segments=p.writeback_segments,
+                                     overflow=overflow)
                 p.view = memoryview(host.numpy())[p._offset:p._offset + p.encoded_bytes]
         for p in pending.payloads:
             if p.bits == BITS_TOP16:
@@ -413,7 +528,7 @@ class SplitzipLayerCodec:
             result = self._encode_group(BITS_FIXED6, pending.kv_layer, overflowed,
                                         pending.block_words, layer)
             if result is not None:
-                out, offsets, sizes = result
+                out, offsets, sizes, _ = result
                 host = out.cpu()
                 for p, off, size in zip(overflowed, offsets, sizes):
                     p.view = memoryview(host.numpy())[off:off + size]

@@ -68,6 +68,12 @@ _SIGNATURES = (
     ("kvq_splitzip_exponent_histogram_workspace_bytes", [_U64] * 2, _U64, False),
     ("kvq_splitzip_exponent_histogram_paged", [_U64] * 10, ctypes.c_longlong, False),
     (
+        "kvq_splitzip_top16_writeback_paged",
+        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64P, _U64P, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
         "kvq_splitzip_top16_decode_attention",
         [_U64, _U64, _U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64, _U64,
          ctypes.c_float, _U64],
@@ -671,6 +677,66 @@ def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_head
     if got < 0:
         _raise_last(lib, "splitzip top16 decode attention failed")
     return out if got else None
+
+
+# ---------------------------------------------------------------------------
+# codec writeback (payloads moved into the sender's own blocks)
+
+def contiguous_run(block_ids) -> tuple[int, int] | None:
+    """(start, count) when ``block_ids`` is one ascending run start, start + 1, ...
+    (the only layout the reference writes back into, vllm_connector.py:3479-3488),
+    else ``None``."""
+    ids = [int(b) for b in block_ids]
+    if not ids or any(b != ids[0] + i for i, b in enumerate(ids)):
+        return None
+    return ids[0], len(ids)
+
+
+def writeback_top16_paged(payloads, batch: PagedBatch, kv_layer, members, *, status=None):
+    """Codec writeback (src/unchain_kv/vllm_connector.py:3460-3563): for each r in
+    ``members``, moves Top-16 payload r of ``batch`` (``batch.out_offsets[r]`` of
+    ``payloads``) into request r's own blocks of ``kv_layer``: its first bytes into
+    the K-plane run of the request's blocks, the rest into the V-plane run (the
+    reference's two segment copies). Every member's block table must be one
+    ascending contiguous run (``contiguous_run``). A payload whose mode byte is not
+    5 (an overflow) is not written, so its blocks stay intact for the fallback
+    encode. Returns ``(bytes, status)``: the bytes of the members' payloads (0 when
+    the library declines: runs that overlap each other or the payload buffer) and a
+    device uint8 tensor with each member's mode byte."""
+    lib = _load()
+    move = getattr(lib, "kvq_splitzip_top16_writeback_paged", None) if lib else None
+    if move is None:
+        raise RuntimeError(f"HIP codec library not loaded: {load_error()}")
+    import torch
+
+    members = [int(r) for r in members]
+    if not members:
+        raise ValueError("no payloads to write back")
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        raise ValueError("kv_layer is not a contiguous bf16 (2, num_blocks, ...) layer of this batch")
+    if payloads.dtype != torch.uint8 or not payloads.is_contiguous() or \
+            payloads.device != kv_layer.device or payloads.numel() < batch.out_bytes:
+        raise ValueError("payloads must be the batch's contiguous uint8 payload buffer")
+    runs = [contiguous_run(batch.block_tables[r]) for r in members]
+    if any(run is None for run in runs):
+        raise ValueError("writeback needs each request's blocks as one contiguous run")
+    if status is None:
+        status = torch.empty(len(members), dtype=torch.uint8, device=kv_layer.device)
+    elif status.dtype != torch.uint8 or status.numel() < len(members) or \
+            status.device != kv_layer.device:
+        raise ValueError("status must be a device uint8 tensor with one byte per member")
+    k = len(members)
+    offs = (ctypes.c_ulonglong * k)(*(batch.out_offsets[r] for r in members))
+    sizes = (ctypes.c_ulonglong * k)(*(batch.encoded_bytes[r] for r in members))
+    starts = (ctypes.c_ulonglong * k)(*(run[0] for run in runs))
+    counts = (ctypes.c_ulonglong * k)(*(run[1] for run in runs))
+    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    got = move(int(payloads.data_ptr()), offs, sizes, k, int(kv_layer.data_ptr()),
+               int(kv_layer.stride(0)), int(kv_layer.stride(1)), batch.block_words, starts,
+               counts, int(status.data_ptr()), int(stream))
+    if got < 0:
+        _raise_last(lib, "splitzip top16 writeback failed")
+    return int(got), status
 
 
 # ---------------------------------------------------------------------------
