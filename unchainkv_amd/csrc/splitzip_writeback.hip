@@ -13,11 +13,11 @@
 // stay intact for the fixed6 re-encode, and the mode byte each payload had is
 // reported in status[r] for the host to check.
 //
-// One launch moves up to 64 payloads. A workgroup moves 4 KiB of one payload:
-// a lane reads the five aligned dwords around its 16 destination bytes (the
-// payload body starts 5 bytes past a 256-byte boundary, so source and
-// destination are misaligned by the same amount for every lane) and writes one
-// aligned 16-byte store.
+// One launch moves up to 64 payloads. A workgroup moves 16 KiB of one payload,
+// four 16-byte chunks per lane: for each, a lane reads the five aligned dwords
+// around its 16 destination bytes (the payload body starts 5 bytes past a
+// 256-byte boundary, so source and destination are misaligned by the same amount
+// for every lane) and writes one aligned 16-byte store.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -31,7 +31,9 @@ namespace unchainkv {
 namespace {
 
 constexpr int kWbMaxPayloads = 64;
-constexpr unsigned int kWbGroupBytes = kThreads * 16;  // payload bytes per workgroup
+constexpr int kWbChunks = 4;                                // 16-byte chunks per lane
+constexpr unsigned int kWbSpan = kThreads * 16;             // one chunk of every lane
+constexpr unsigned int kWbGroupBytes = kWbSpan * kWbChunks;  // payload bytes per workgroup
 constexpr unsigned int kModeTop16 = 5;
 
 struct WbDesc {
@@ -69,45 +71,60 @@ __device__ __forceinline__ unsigned char* wb_target(const WbDesc& d, unsigned lo
 // 16 bytes from a 4-byte aligned address (global loads need dword alignment only).
 typedef unsigned int u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
-// kAligned: both runs start 16-byte aligned and a run holds a multiple of 16
-// bytes, so a lane's 16 destination bytes never straddle the two runs.
+// kAligned: both runs start 16-byte aligned, a run holds a multiple of 16 bytes
+// (a lane's 16 destination bytes never straddle the two runs) and every payload
+// has at least 20 bytes. A lane
+// moves chunks base + k * 4 KiB (k < 4) of its workgroup's 16 KiB: every load of
+// the workgroup is issued before the first store, so a resident workgroup keeps
+// 16 KiB in flight.
 template <bool kAligned>
 __global__ __launch_bounds__(kThreads) void top16_writeback(WbArgs a) {
   const unsigned int g = group_index();
   const unsigned int r = find_wb_payload(a, g);
   const WbDesc d = a.p[r];
-  const unsigned long long c0 =
+  const unsigned long long base =
       (unsigned long long)(g - d.group_begin) * kWbGroupBytes + threadIdx.x * 16u;
-  // the window of five dwords from (src + c0) rounded down to 4 bytes ends at
-  // src + c0 + 19: inside the payload when c0 + 20 <= bytes. Its first dword
-  // may begin up to 3 bytes before the payload, within the dword of src[0].
-  const bool fast = kAligned && c0 + 20 <= d.bytes;
   // the mode byte is read per lane (through an index the compiler cannot prove
   // uniform) so that testing it does not wait for it before the data loads issue
   unsigned int zero;
   __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero));
   const unsigned int mode = d.src[zero];
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (fast) {
-    const unsigned int sh = (unsigned int)(reinterpret_cast<uintptr_t>(d.src) & 3);
-    const unsigned char* w = d.src + c0 - sh;
-    const u32x4_a4 lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(w));
-    const uint32_t hi = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + 16));
-    v.x = funnel(lo.x, lo.y, sh);
-    v.y = funnel(lo.y, lo.z, sh);
-    v.z = funnel(lo.z, lo.w, sh);
-    v.w = funnel(lo.w, hi, sh);
-    // keep the data loads ahead of the mode test (one round trip for both)
-    __asm__ volatile("" ::"v"(mode), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w));
+  // chunk c's window of five dwords from (src + c) rounded down to 4 bytes ends at
+  // src + c + 19: inside the payload when c + 20 <= bytes. Its first dword may
+  // begin up to 3 bytes before the payload, within the dword of src[0]. Chunks
+  // without a whole window (the payload's last bytes, or past its end) load the
+  // first window instead, which every payload of an aligned launch holds (at
+  // least 20 bytes): the loads need no branch and all issue together.
+  const unsigned int sh = (unsigned int)(reinterpret_cast<uintptr_t>(d.src) & 3);
+  u32x4_a4 lo[kWbChunks];
+  uint32_t hi[kWbChunks];
+  if (kAligned) {
+#pragma unroll
+    for (int k = 0; k < kWbChunks; ++k) {
+      const unsigned long long c = base + (unsigned long long)k * kWbSpan;
+      const unsigned char* w = d.src + (c + 20 <= d.bytes ? c : 0) - sh;
+      lo[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(w));
+      hi[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + 16));
+    }
   }
   if (g == d.group_begin && threadIdx.x == 0) a.status[r] = (unsigned char)mode;
-  if (mode != kModeTop16 || c0 >= d.bytes) return;
-  if (fast) {
-    store_stream16(wb_target(d, c0), v);
-    return;
+  if (mode != kModeTop16) return;
+#pragma unroll
+  for (int k = 0; k < kWbChunks; ++k) {
+    const unsigned long long c = base + (unsigned long long)k * kWbSpan;
+    if (c >= d.bytes) return;
+    if (kAligned && c + 20 <= d.bytes) {
+      u32x4 v;
+      v.x = funnel(lo[k].x, lo[k].y, sh);
+      v.y = funnel(lo[k].y, lo[k].z, sh);
+      v.z = funnel(lo[k].z, lo[k].w, sh);
+      v.w = funnel(lo[k].w, hi[k], sh);
+      store_stream16(wb_target(d, c), v);
+    } else {
+      const unsigned long long stop = c + 16 < d.bytes ? c + 16 : d.bytes;
+      for (unsigned long long j = c; j < stop; ++j) *wb_target(d, j) = d.src[j];
+    }
   }
-  const unsigned long long stop = c0 + 16 < d.bytes ? c0 + 16 : d.bytes;
-  for (unsigned long long j = c0; j < stop; ++j) *wb_target(d, j) = d.src[j];
 }
 
 struct Interval {
@@ -191,7 +208,8 @@ extern "C" long long kvq_splitzip_top16_writeback_paged(
       if (i == 0) first_groups = own;
       uniform = uniform && own == first_groups;
       groups += own;
-      aligned = aligned && k % 16 == 0 && (k + 2 * plane_stride) % 16 == 0 && d.seg % 16 == 0;
+      aligned = aligned && k % 16 == 0 && (k + 2 * plane_stride) % 16 == 0 &&
+                d.seg % 16 == 0 && d.bytes >= 20;
     }
     a.uniform_groups = uniform ? (unsigned int)first_groups : 0u;
     if (aligned)

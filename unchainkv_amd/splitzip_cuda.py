@@ -390,6 +390,31 @@ class PagedBatch:
         self.max_block = max(flat)
         self.unique_blocks = len(set(flat)) == len(flat)
         self._palette = {}
+        self._runs = None
+        self._writeback = {}
+
+    @property
+    def runs(self) -> list:
+        """Per request: (start, count) when its blocks are one ascending contiguous
+        run, else ``None`` (computed once)."""
+        if self._runs is None:
+            self._runs = [contiguous_run(t) for t in self.block_tables]
+        return self._runs
+
+    def writeback_arrays(self, members: tuple):
+        """ctypes (offsets, sizes, run starts, run blocks) of ``members`` (cached)."""
+        cached = self._writeback.get(members)
+        if cached is None:
+            runs = [self.runs[r] for r in members]
+            if any(run is None for run in runs):
+                raise ValueError("writeback needs each request's blocks as one contiguous run")
+            k = len(members)
+            cached = ((ctypes.c_ulonglong * k)(*(self.out_offsets[r] for r in members)),
+                      (ctypes.c_ulonglong * k)(*(self.encoded_bytes[r] for r in members)),
+                      (ctypes.c_ulonglong * k)(*(run[0] for run in runs)),
+                      (ctypes.c_ulonglong * k)(*(run[1] for run in runs)))
+            self._writeback[members] = cached
+        return cached
 
     def _c_array(self, values, own, own_array):
         """ctypes u64 array of `values` (the batch's own array when it is the same list)."""
@@ -709,7 +734,7 @@ def writeback_top16_paged(payloads, batch: PagedBatch, kv_layer, members, *, sta
         raise RuntimeError(f"HIP codec library not loaded: {load_error()}")
     import torch
 
-    members = [int(r) for r in members]
+    members = tuple(int(r) for r in members)
     if not members:
         raise ValueError("no payloads to write back")
     if not _paged_layout_ok(kv_layer, batch, torch):
@@ -717,19 +742,12 @@ def writeback_top16_paged(payloads, batch: PagedBatch, kv_layer, members, *, sta
     if payloads.dtype != torch.uint8 or not payloads.is_contiguous() or \
             payloads.device != kv_layer.device or payloads.numel() < batch.out_bytes:
         raise ValueError("payloads must be the batch's contiguous uint8 payload buffer")
-    runs = [contiguous_run(batch.block_tables[r]) for r in members]
-    if any(run is None for run in runs):
-        raise ValueError("writeback needs each request's blocks as one contiguous run")
-    if status is None:
-        status = torch.empty(len(members), dtype=torch.uint8, device=kv_layer.device)
-    elif status.dtype != torch.uint8 or status.numel() < len(members) or \
-            status.device != kv_layer.device:
-        raise ValueError("status must be a device uint8 tensor with one byte per member")
+    offs, sizes, starts, counts = batch.writeback_arrays(members)
     k = len(members)
-    offs = (ctypes.c_ulonglong * k)(*(batch.out_offsets[r] for r in members))
-    sizes = (ctypes.c_ulonglong * k)(*(batch.encoded_bytes[r] for r in members))
-    starts = (ctypes.c_ulonglong * k)(*(run[0] for run in runs))
-    counts = (ctypes.c_ulonglong * k)(*(run[1] for run in runs))
+    if status is None:
+        status = torch.empty(k, dtype=torch.uint8, device=kv_layer.device)
+    elif status.dtype != torch.uint8 or status.numel() < k or status.device != kv_layer.device:
+        raise ValueError("status must be a device uint8 tensor with one byte per member")
     stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
     got = move(int(payloads.data_ptr()), offs, sizes, k, int(kv_layer.data_ptr()),
                int(kv_layer.stride(0)), int(kv_layer.stride(1)), batch.block_words, starts,
