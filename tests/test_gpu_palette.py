@@ -145,6 +145,8 @@ def test_dropin_decode_accepts_any_palette_order_and_skips_other_modes(sz):
     (2048, 300, [8, 40, 17, 64], 0),  # 70B TP8 share: tile kernels
     (48, 400, [50, 7, 99], 0),        # small blocks: generic kernels
     (2048, 100, [10, 20], 1),         # KV view at a 2-byte offset: generic kernels
+    (2048, 400, [3] * 70, 0),         # 70 payloads: two launches of 64 and 6
+    (48, 600, [8] * 66, 0),           # 66 payloads on the generic kernels
 ])
 def test_paged_encode_decode_matches_oracle(sz, bits, bw, pool, requests, offset):
     say("paged palette", bits, bw, requests, offset)

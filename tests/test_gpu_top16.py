@@ -247,6 +247,8 @@ def test_tile_with_many_escapes_and_overflow(sz, codebooks):
     (48, 400, [50, 7, 99], 0.003, 0),       # small block, several blocks per tile
     (40, 300, [60, 5], 0.003, 0),           # block words not a multiple of 16: generic path
     (2048, 100, [10, 20], 0.001, 1),        # KV view at a 2-byte offset: generic path
+    (2048, 400, [3] * 70 + [5], 0.002, 0),  # 71 payloads: two launches of 64 and 7
+    (48, 600, [8] * 66, 0.001, 0),          # 66 payloads on the generic kernels
 ])
 def test_paged_encode_decode_matches_oracle(sz, codebooks, bw, pool, requests, rate, offset):
     say("paged", bw, pool, requests, rate, offset)
