@@ -61,6 +61,7 @@ struct LaunchArgs {
   unsigned int tiles_per_plane_mode;  // 1: tiles never cross a plane (fast path); 0: one range [0, n)
   unsigned int tile_shift;            // log2 of the tile size in words
   unsigned int uniform_tiles;         // tiles of every payload when all are equal, else 0
+  unsigned int uniform_slot_groups;   // escape-patch workgroups of every payload, likewise
   PayloadDesc p[kMaxPayloads];
 };
 
@@ -127,6 +128,7 @@ __device__ __forceinline__ unsigned int find_payload(const LaunchArgs& a, unsign
 
 // Same search over the escape-patch workgroups of each payload.
 __device__ __forceinline__ unsigned int find_slot_payload(const LaunchArgs& a, unsigned int group) {
+  if (a.uniform_slot_groups) return group / a.uniform_slot_groups;
   if (a.payload_count <= 1) return 0;
   const unsigned int lane = __lane_id();
   const unsigned int begin =

@@ -1036,13 +1036,19 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     }
   }
   if (long long rc = check_launch("top16_decode")) return rc;
-  unsigned long long groups = 0;
+  unsigned long long groups = 0, first_groups = 0;
+  bool uniform = true;
   for (unsigned int r = 0; r < a.payload_count; ++r) {
     const unsigned long long n =
         a.linear_words ? a.linear_words : 2ull * a.p[r].block_count * a.block_words;
+    const unsigned long long own = (escape_capacity(n) + kThreads - 1) / kThreads;
+    if (r == 0) first_groups = own;
+    uniform = uniform && own == first_groups;
     a.p[r].slot_group_begin = (unsigned int)groups;
-    groups += (escape_capacity(n) + kThreads - 1) / kThreads;
+    groups += own;
   }
+  // equal payloads: a workgroup finds its payload by one division
+  a.uniform_slot_groups = uniform ? (unsigned int)first_groups : 0u;
   hipLaunchKernelGGL(top16_patch_escapes, dim3((unsigned int)groups), block, 0, stream, a);
   return check_launch("top16_patch_escapes");
 }
