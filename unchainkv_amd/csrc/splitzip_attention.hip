@@ -397,6 +397,18 @@ top16_attention_split(AttnArgs a) {
   w.ok = payload[0] == 5;
   __syncthreads();  // decode tables
 
+  // The four waves meet at a barrier after every second step, so that the two
+  // heads' waves of a token range read each 128-byte code line they share within
+  // two steps of each other and the second read hits L2 (unsynchronised waves
+  // drifted apart and fetched ~12 % of the payload bytes twice). Every wave runs
+  // the step count of the longer of the workgroup's two ranges.
+  auto range_steps = [&](unsigned int r) -> unsigned int {
+    const unsigned int s0 = (split * 2 + r) * a.tokens_per_wave;
+    const unsigned int e0 = min(ctx, s0 + a.tokens_per_wave);
+    return e0 > s0 ? (e0 - s0 + kStep - 1) / kStep : 0u;
+  };
+  const unsigned int steps_max = max(range_steps(0), range_steps(1));
+  const unsigned int steps = wb < c.we ? (c.we - wb + kStep - 1) / kStep : 0u;
   if (wb < c.we) {
     const unsigned int we = c.we;
     w.ptr_k = lower_bound_escapes(entries, c.count, wb * row_words);
@@ -412,17 +424,22 @@ top16_attention_split(AttnArgs a) {
                         (unsigned long long)min(t0 + 8, we - 1) * row_words + share, c.half);
     };
     RawShare r0 = load_step(wb);
-    for (unsigned int ts = wb;;) {
-      const unsigned int t1 = ts + kStep;
-      const RawShare r1 = load_step(t1);
-      attend_step(r0, ts, c, qb, w);
-      ts = t1;
-      if (ts >= we) break;
-      r0 = load_step(ts + kStep);
-      attend_step(r1, ts, c, qb, w);
-      ts += kStep;
-      if (ts >= we) break;
+    RawShare r1;
+    unsigned int ts = wb;
+    for (unsigned int i = 0; i < steps_max; i += 2) {
+      if (i < steps) {
+        r1 = load_step(ts + kStep);
+        attend_step(r0, ts, c, qb, w);
+      }
+      if (i + 1 < steps) {
+        r0 = load_step(ts + 2 * kStep);
+        attend_step(r1, ts + kStep, c, qb, w);
+      }
+      __builtin_amdgcn_s_barrier();
+      ts += 2 * kStep;
     }
+  } else {
+    for (unsigned int i = 0; i < steps_max; i += 2) __builtin_amdgcn_s_barrier();
   }
 
   // ---- merge each head's 2 waves (m, l, acc), then write the split's partials ----
