@@ -224,7 +224,7 @@ def test_tile_with_many_escapes_and_overflow(sz, codebooks):
     n = 2 * 8 * 4096  # 16 tiles, cap 328
     words = random_words(rng, n, books, 0.0)
     outside = sorted(set(range(256)) - set(books))
-    # 200 escapes packed into tile 3 (more than the 64 staged per tile), 50 elsewhere
+    # 200 escapes packed into tile 3 (more than the 128 staged per tile), 50 elsewhere
     for pos in list(range(3 * 4096 + 100, 3 * 4096 + 300)) + rng.choice(n, 50, replace=False).tolist():
         words[pos] = (words[pos] & 0x807F) | (outside[pos % len(outside)] << 7)
     for label, w in (("dense tile", words), ("overflow", random_words(rng, n, books, 0.01))):
@@ -313,9 +313,9 @@ def test_paged_escape_heavy_tiles(sz, codebooks, label):
                     [44, 2], [7, 8, 63, 12, 40, 41, 42, 43]]
     if label == "dense tile":
         outside = sorted(set(range(256)) - set(books))
-        # 300 escapes inside one tile of payload 0's V plane (cap 410) and 60 in one
-        # tile of payload 2's K plane (cap 164)
-        for blk, lo, count in ((1, 2048 + 100, 300), (12, 0, 60)):
+        # 300 escapes inside one tile of payload 0's V plane (cap 410: re-scanned)
+        # and 100 in one tile of payload 2's K plane (cap 164: all staged)
+        for blk, lo, count in ((1, 2048 + 100, 300), (12, 0, 100)):
             for w in range(lo % bw, lo % bw + count):
                 plane = 1 if blk == 1 else 0
                 kv_host[plane, blk, w] = (kv_host[plane, blk, w] & 0x807F) | (

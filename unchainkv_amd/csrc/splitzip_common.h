@@ -24,9 +24,11 @@ static_assert((1 << kTileShift) == kTileWords, "tile size");
 // vector memory instruction of a wave covers 64 consecutive chunks.
 constexpr int kChunkWords = 8;
 
-// Escapes staged per tile by the encode kernel (1.6% of a 4096-word tile); tiles
-// with more are re-scanned by the finalize kernel.
-constexpr int kStageSlots = 64;
+// Escapes staged per tile by the encode kernel (3.1% of a 4096-word tile, three
+// times the 0.5% escape capacity of a payload, so that a payload with 1% outliers
+// rarely has a tile to re-scan); tiles with more are re-scanned by the finalize
+// kernel.
+constexpr int kStageSlots = 128;
 // Payload descriptors passed by value in the kernel arguments.
 constexpr int kMaxPayloads = 64;
 
