@@ -1,8 +1,8 @@
 #!/usr/bin/env python3
 """Write the golden fixtures for the splitzip Top-16 codec tests.
 
-Run in a container that has the reference checkout at /root/reference; the GPU
-box never runs this. It reads reference files as text only (nothing from the
+Run where the reference checkout is at /root/reference (the tests only read the
+files it writes). It reads reference files as text only (nothing from the
 reference is imported or executed) and writes small data files next to itself:
 
 * top16_codebooks.bin   -- the 1024-byte embedded codebook table, parsed from the
