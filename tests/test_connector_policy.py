@@ -223,3 +223,27 @@ def test_exponent_trace_once_per_transfer_layer_and_retry_after_error():
     assert fields["v"]["unique_exponents"] == 1
     assert np.isclose(fields["k"]["top16_coverage"], 1.0)
     assert calls[-1] == ([[3, 4]], 2048)
+
+
+def test_writeback_skips_a_layer_that_is_not_contiguous():
+    from types import SimpleNamespace
+
+    from unchainkv_amd.connector import LayerPayload, PendingLayer
+
+    class FakeLib:
+        @staticmethod
+        def available():
+            return True
+
+        @staticmethod
+        def writeback_top16_paged(*args, **kwargs):
+            raise AssertionError("not called for a non-contiguous layer")
+
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace,
+                               lib=FakeLib())
+    layer = SimpleNamespace(is_contiguous=lambda: False)
+    members = [LayerPayload(0, [4, 5], 2 * MIB, BITS_TOP16, BITS_TOP16, encoded_bytes=100)]
+    pending = PendingLayer(7, layer, 16384, members)
+    assert not codec._stage_writeback(pending, members, (None, [0], [100], None), None)
+    assert trace.rows == [("codec_writeback_skip", {"layer": 7, "reason": "layout"})]

@@ -389,6 +389,11 @@ class SplitzipLayerCodec:
             return False
         sz = self._lib()
         kv_layer = pending.kv_layer
+        if not kv_layer.is_contiguous():
+            # a run of blocks is not one contiguous segment (vllm_connector.py:3489-3492)
+            for i in picks:
+                self.trace.event("codec_writeback_skip", layer=layer, reason="layout")
+            return False
         moved, status = sz.writeback_top16_paged(out, batch, kv_layer, picks)
         if not moved:
             for i in picks:
