@@ -100,6 +100,22 @@ __device__ __forceinline__ void store_stream(void* p, T v) {
 __device__ __forceinline__ u32x4 load_stream16(const void* p) { return load_stream<u32x4>(p); }
 __device__ __forceinline__ u32x2 load_stream8(const void* p) { return load_stream<u32x2>(p); }
 __device__ __forceinline__ uint32_t load_stream4(const void* p) { return load_stream<uint32_t>(p); }
+// Streaming stores that also write through to the device's coherence point
+// (cache policy nt sc1): a tile kernel that writes its whole output this way
+// leaves little dirty data in L2 for the write-back at its end, so the kernel
+// that follows it starts sooner (Llama-3-8B encode call 49.5 -> 48.7 us). No
+// builtin sets sc1 on a vector store, hence the inline assembly; the compiler's
+// memory-counter waits do not see these stores, so a kernel issues them only
+// after its last global load.
+__device__ __forceinline__ void store_through16(void* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_through8(void* p, u32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_through4(void* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
 __device__ __forceinline__ void store_stream16(void* p, u32x4 v) { store_stream<u32x4>(p, v); }
 __device__ __forceinline__ void store_stream8(void* p, u32x2 v) { store_stream<u32x2>(p, v); }
 __device__ __forceinline__ void store_stream4(void* p, uint32_t v) { store_stream<uint32_t>(p, v); }

@@ -564,10 +564,10 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
   if (active) {
     unsigned char* pbody = t.payload + 5 + wstart;
     unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
-    store_stream8(pbody + 8 * lane, u32x2{body_a[0], body_a[1]});
-    store_stream8(pbody + 512 + 8 * lane, u32x2{body_b[0], body_b[1]});
-    store_stream4(pcode + 4 * lane, code_a);
-    store_stream4(pcode + 256 + 4 * lane, code_b);
+    store_through8(pbody + 8 * lane, u32x2{body_a[0], body_a[1]});
+    store_through8(pbody + 512 + 8 * lane, u32x2{body_b[0], body_b[1]});
+    store_through4(pcode + 4 * lane, code_a);
+    store_through4(pcode + 256 + 4 * lane, code_b);
   } else {
     mask_a = mask_b = 0;
   }
@@ -687,8 +687,8 @@ __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, Enco
   asm volatile("" ::"v"(out_a), "v"(out_b));
   // the reference decoder leaves a payload whose byte 0 is not 5 untouched
   if (mode != 5) return;
-  store_stream16(dst + 8 * lane, out_a);
-  store_stream16(dst + 512 + 8 * lane, out_b);
+  store_through16(dst + 8 * lane, out_a);
+  store_through16(dst + 512 + 8 * lane, out_b);
 }
 
 // Scans the escapes of one tile from the source words (tiles with more escapes
