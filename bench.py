@@ -56,6 +56,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=30)
     p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--settle-seconds", type=float, default=0.5,
+                   help="after the warmup steps, keep stepping (untimed) until this much "
+                        "wall time has passed since the first warmup step")
     p.add_argument("--workload", default="llama3-8b-paged", choices=WORKLOADS)
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--cpu-baseline-seconds", type=float, default=10.0,
@@ -100,6 +103,22 @@ def hold_queue(torch, ms: float = 3.0) -> None:
         torch.cuda.synchronize()
         _SLEEP_CYCLES_PER_MS.append(probe / max(e0.elapsed_time(e1), 1e-3))
     torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS[0] * ms))
+
+
+def warm_up(torch, step, warmup: int, settle_s: float) -> int:
+    """`warmup` untimed steps, then more untimed steps until `settle_s` seconds have
+    passed since the first. A few warmup steps on a GPU that was idle are not enough:
+    20 timed Llama-3-8B steps after 3 warmup steps read 4.4-4.9 ms per step, and
+    3.18 ms after half a second of untimed steps. Returns the steps run."""
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t0 < settle_s:
+        step()
+        done += 1
+        if done >= warmup:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return done
 
 
 def calibration_copy(torch, device):
@@ -663,9 +682,7 @@ def run_attention(args, torch, sz, workloads) -> int:
                           "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(torch, step, args.warmup, args.settle_seconds)
     worst = max(verify_attention(torch, sz, w, layer) for layer in (0, layers - 1))
 
     t0 = time.perf_counter()
@@ -815,9 +832,7 @@ def main() -> int:
                           "calibration_copy_bytes": CALIBRATION_BYTES}))
         return 0
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
+    warm_up(torch, step, args.warmup, args.settle_seconds)
     verify(torch, w)
 
     # timed region: exactly `steps` steps between two synchronisations
