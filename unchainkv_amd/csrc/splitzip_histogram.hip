@@ -8,14 +8,15 @@
 // straight from the cache (no gather copy).
 //
 // Two kernels, no global atomics, deterministic output:
-//   exponent_hist_partial: each wave streams batches of twelve 1024-word chunks
-//     (block ids fetched a batch ahead) and adds every word's exponent into the
-//     workgroup's LDS histogram. Lane l of every wave counts into copy l of the
+//   exponent_hist_partial: each wave streams batches of twelve 1024-word chunks,
+//     two batches in flight (block ids fetched a batch ahead), and adds every
+//     word's exponent into the workgroup's LDS histogram. Lane l of every wave counts into copy l of the
 //     histogram, two 16-bit bins per dword, laid out so that copy l sits in bank
 //     l: an LDS atomic instruction never has two lanes on one bank (a bf16 plane
 //     concentrates on ~16 exponents, and colliding LDS atomics serialise). The
 //     workgroup then writes one 512-bin partial (K bins, then V bins).
-//   exponent_hist_reduce: sums the partials into 64-bit counts.
+//   exponent_hist_reduce: sums the partials into 64-bit counts, every bin's
+//     groups split over sixteen threads.
 // Layouts that the chunk kernel cannot take (block words not a multiple of 1024,
 // misaligned cache) go through a one-word-per-thread kernel with the same output.
 #include <hip/hip_runtime.h>
@@ -34,10 +35,10 @@ constexpr int kCopies = 64;                    // one per lane
 constexpr int kChunk = 1024;                   // words per wave step (one block)
 constexpr unsigned int kMaxPartials = 2048;    // workgroups of the partial kernel
 
-// Chunks per wave step: 24 KiB of loads per wave, two steps in flight. The kernel
-// runs two waves per SIMD (64 KiB of LDS histogram per workgroup), so the loads in
-// flight per wave set its rate: 4 chunks per step ran at 145 us per Llama-3-8B
-// layer, 8 at 99 us, 12 at 90 us (16 needs more than 256 VGPRs).
+// Chunks per wave step: 24 KiB of loads per wave, two steps (48 KiB) in flight.
+// The kernel runs two waves per SIMD (64 KiB of LDS histogram per workgroup), so
+// the loads in flight per wave set its rate (16 chunks per step would need more
+// than the 256 VGPRs a wave has at that occupancy).
 constexpr int kBatch = 12;
 
 struct HistArgs {
@@ -104,37 +105,54 @@ struct Batch {
   u32x4 d[2 * kBatch];
 };
 
-// Issues the loads of batch b (chunks kBatch*b ..): block ids from `idv`, lane k's
-// value for chunk k.
+// Issues the loads of batch b (chunks kBatch*b ..), lane k of `idv` holding chunk
+// k's block id. Chunks past the end re-read the last chunk, so that every load is
+// issued unconditionally (a load under a branch makes the compiler wait for all
+// outstanding loads where the paths join); count_batch skips them.
 __device__ __forceinline__ Batch load_batch(const HistArgs& a, unsigned int b, long long idv,
                                             unsigned int total, unsigned int lane) {
   Batch r;
 #pragma unroll
   for (int k = 0; k < kBatch; ++k) {
-    const unsigned int c = b * kBatch + k;
+    const unsigned int c = min(b * kBatch + k, total - 1);
     const long long id = __builtin_amdgcn_readlane((int)idv, k) |
                          ((long long)__builtin_amdgcn_readlane((int)(idv >> 32), k) << 32);
-    if (c < total) {
-      const uint16_t* src = a.kv + chunk_offset(a, c, (unsigned long long)id);
-      r.d[2 * k] = load_stream16(src + 8 * lane);
-      r.d[2 * k + 1] = load_stream16(src + 512 + 8 * lane);
-    } else {
-      r.d[2 * k] = r.d[2 * k + 1] = u32x4{0, 0, 0, 0};
-    }
+    const uint16_t* src = a.kv + chunk_offset(a, c, (unsigned long long)id);
+    r.d[2 * k] = load_stream16(src + 8 * lane);
+    r.d[2 * k + 1] = load_stream16(src + 512 + 8 * lane);
   }
   return r;
 }
 
+// Block ids of batch b: lane k < kBatch loads chunk k's (clamped like the data).
 __device__ __forceinline__ long long load_ids(const HistArgs& a, unsigned int b,
                                               unsigned int total, unsigned int lane) {
-  const unsigned int c = b * kBatch + lane;
-  return lane < (unsigned int)kBatch && c < total ? chunk_block_id(a, c) : 0;
+  return chunk_block_id(a, min(b * kBatch + (lane < (unsigned int)kBatch ? lane : 0u), total - 1));
+}
+
+// Adds the words of batch b (held in r) to the LDS histogram.
+__device__ __forceinline__ void count_batch(unsigned int* h, const Batch& r, unsigned int b,
+                                            unsigned int total, unsigned int chunks_per_plane,
+                                            unsigned int copy) {
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) {
+    const unsigned int c = b * kBatch + k;
+    if (c >= total) break;
+    const unsigned int plane = c >= chunks_per_plane ? 1u : 0u;
+    const u32x4 x0 = r.d[2 * k], x1 = r.d[2 * k + 1];
+    const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      add_word(h, plane, x[q], copy);
+      add_word(h, plane, x[q] >> 16, copy);
+    }
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void exponent_hist_partial(HistArgs a) {
   __shared__ unsigned int h[kHistWords];
   const unsigned int lane = threadIdx.x & (kWave - 1);
-  const unsigned int wave = threadIdx.x / kWave;
+  const unsigned int wave = uniform(threadIdx.x / kWave);
   zero_hist(h);
   const unsigned int copy = lane;
   const unsigned int total = 2 * a.chunks_per_plane;
@@ -142,34 +160,29 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_partial(HistArgs a) {
   const unsigned int stride = gridDim.x * (kThreads / kWave);
   unsigned int b0 = blockIdx.x * (kThreads / kWave) + wave;
   if (b0 < batches) {
-    // batch b0 in flight, block ids of the next batch loaded one step ahead
-    Batch cur = load_batch(a, b0, load_ids(a, b0, total, lane), total, lane);
-    unsigned int b1 = b0 + stride;
-    long long id1 = b1 < batches ? load_ids(a, b1, total, lane) : 0;
+    // Two batches in flight, in two buffers used in turn (a copy from one to the
+    // other would wait for its loads). The block ids of a batch are loaded one
+    // step ahead and issued before the batch that precedes it, so waiting for them
+    // (outstanding loads complete in issue order) does not wait for that batch.
+    const long long id0 = load_ids(a, b0, total, lane);
+    unsigned int bb = b0 + stride;
+    long long id_b = load_ids(a, min(bb, batches - 1), total, lane);
+    Batch ba = load_batch(a, b0, id0, total, lane);
+    Batch bbuf;
     for (;;) {
-      const bool more = b1 < batches;
-      Batch nxt;
-      if (more) nxt = load_batch(a, b1, id1, total, lane);
-      const unsigned int b2 = b1 + stride;
-      const long long id2 = more && b2 < batches ? load_ids(a, b2, total, lane) : 0;
-#pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        const unsigned int c = b0 * kBatch + k;
-        if (c >= total) break;
-        const unsigned int plane = c >= a.chunks_per_plane ? 1u : 0u;
-        const u32x4 x0 = cur.d[2 * k], x1 = cur.d[2 * k + 1];
-        const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          add_word(h, plane, x[q], copy);
-          add_word(h, plane, x[q] >> 16, copy);
-        }
-      }
-      if (!more) break;
-      cur = nxt;
-      b0 = b1;
-      b1 = b2;
-      id1 = id2;
+      // past the last batch the loads repeat it and nothing is counted
+      const unsigned int b2 = bb + stride;
+      const long long id_a = load_ids(a, min(b2, batches - 1), total, lane);
+      bbuf = load_batch(a, min(bb, batches - 1), id_b, total, lane);
+      count_batch(h, ba, b0, total, a.chunks_per_plane, copy);
+      if (bb >= batches) break;
+      const unsigned int b3 = b2 + stride;
+      id_b = load_ids(a, min(b3, batches - 1), total, lane);
+      ba = load_batch(a, min(b2, batches - 1), id_a, total, lane);
+      count_batch(h, bbuf, bb, total, a.chunks_per_plane, copy);
+      if (b2 >= batches) break;
+      b0 = b2;
+      bb = b3;
     }
   }
   write_partial(h, a.partial);
@@ -195,13 +208,35 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_generic(HistArgs a) {
   write_partial(h, a.partial);
 }
 
+// Sums the partials into 64-bit counts. Workgroup w owns bins [16w, 16w + 16); its
+// threads split the groups into 16 slices (each row of 16 bins is one 64-byte
+// segment) and keep eight loads in flight, then add the slices in LDS.
+constexpr unsigned int kReduceBins = 16;
+constexpr unsigned int kReduceSlices = kThreads / kReduceBins;
+
 __global__ __launch_bounds__(kThreads) void exponent_hist_reduce(const unsigned int* partial,
                                                                  unsigned int groups,
                                                                  unsigned long long* counts) {
-  const unsigned int b = blockIdx.x * kThreads + threadIdx.x;  // grid covers 2 * kBins
+  __shared__ unsigned long long s_sum[kThreads];
+  const unsigned int bin = blockIdx.x * kReduceBins + threadIdx.x % kReduceBins;
+  const unsigned int slice = threadIdx.x / kReduceBins;
   unsigned long long s = 0;
-  for (unsigned int g = 0; g < groups; ++g) s += partial[(unsigned long long)g * 2 * kBins + b];
-  counts[b] = s;
+  unsigned int g = slice;
+  for (; g + 7 * kReduceSlices < groups; g += 8 * kReduceSlices) {
+    unsigned int v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      v[k] = partial[(unsigned long long)(g + k * kReduceSlices) * 2 * kBins + bin];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += v[k];
+  }
+  for (; g < groups; g += kReduceSlices) s += partial[(unsigned long long)g * 2 * kBins + bin];
+  s_sum[threadIdx.x] = s;
+  __syncthreads();
+  if (slice == 0) {
+    for (unsigned int j = 1; j < kReduceSlices; ++j) s += s_sum[j * kReduceBins + threadIdx.x];
+    counts[bin] = s;
+  }
 }
 
 unsigned int partial_groups(unsigned long long block_count, unsigned long long block_words,
@@ -209,12 +244,13 @@ unsigned int partial_groups(unsigned long long block_count, unsigned long long b
   const unsigned long long words = 2 * block_count * block_words;
   unsigned long long g;
   if (chunked) {
-    // about eight batches per wave (measured best on Llama-3-8B and 70B-TP8 layers:
-    // 2, 5, 12 and 16 were slower), but a small layer still spreads over up to 64
-    // workgroups, one batch per wave
+    // about four batches per wave (per-layer call, Llama-3-8B: 2 -> 42.7 us,
+    // 4 -> 41.2, 8 -> 47.4; Llama-3-70B TP8: 1 -> 68.9, 2 -> 56.2, 4 -> 48.7,
+    // 8 -> 51.9), but a small layer still spreads over up to 64 workgroups, one
+    // batch per wave
     const unsigned long long batches = (words / kChunk + kBatch - 1) / kBatch;
     const unsigned long long waves = kThreads / kWave;
-    g = (batches + 8 * waves - 1) / (8 * waves);
+    g = (batches + 4 * waves - 1) / (4 * waves);
     const unsigned long long spread = (batches + waves - 1) / waves;
     const unsigned long long floor_g = spread < 64 ? spread : 64;
     if (g < floor_g) g = floor_g;
@@ -296,7 +332,7 @@ extern "C" long long kvq_splitzip_exponent_histogram_paged(
     hipLaunchKernelGGL(exponent_hist_generic, dim3(groups), dim3(kThreads), 0, stream, a);
   hipError_t st = hipGetLastError();
   if (st != hipSuccess) return fail("exponent_hist_partial", st);
-  hipLaunchKernelGGL(exponent_hist_reduce, dim3(2 * kBins / kThreads), dim3(kThreads), 0, stream,
+  hipLaunchKernelGGL(exponent_hist_reduce, dim3(2 * kBins / kReduceBins), dim3(kThreads), 0, stream,
                      a.partial, groups, reinterpret_cast<unsigned long long*>(counts_ptr));
   st = hipGetLastError();
   if (st != hipSuccess) return fail("exponent_hist_reduce", st);
