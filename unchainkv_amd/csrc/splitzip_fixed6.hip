@@ -154,10 +154,18 @@ __global__ __launch_bounds__(kThreads) void palette_reduce(LaunchArgs a, unsigne
       hi |= b[k];
     }
   }
-  const unsigned int part[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  // OR over the wave by shuffles, then one LDS atomic per wave and dword (an
+  // atomic from every lane compiles to a loop over the active lanes)
+  unsigned int part[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
   for (int k = 0; k < 8; ++k)
-    if (part[k]) atomicOr(&s_mask[k], part[k]);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) part[k] |= __shfl_xor(part[k], off, kWave);
+  if ((tid & (kWave - 1)) == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (part[k]) atomicOr(&s_mask[k], part[k]);
+  }
   __syncthreads();
   PaletteInfo& out = info[r];
   unsigned int distinct = 0;
