@@ -65,13 +65,14 @@ __host__ __device__ inline unsigned long long encoded_size(unsigned long long n)
   return 5 + n + (n + 1) / 2 + 5 * escape_capacity(n);
 }
 
+// A 4-byte type at any address: global memory takes unaligned dword accesses, so
+// an entry is one dword store and one byte store instead of five byte stores.
+typedef unsigned int u32_unaligned __attribute__((aligned(1)));
+
 __device__ __forceinline__ void put_entry(unsigned char* entries, unsigned long long slot,
                                           unsigned int pos, unsigned int exponent) {
   unsigned char* e = entries + slot * 5;
-  e[0] = (unsigned char)pos;
-  e[1] = (unsigned char)(pos >> 8);
-  e[2] = (unsigned char)(pos >> 16);
-  e[3] = (unsigned char)(pos >> 24);
+  *reinterpret_cast<u32_unaligned*>(e) = pos;  // little-endian, as the format
   e[4] = (unsigned char)exponent;
 }
 
