@@ -74,28 +74,13 @@ struct LaunchArgs {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-#ifndef UKV_NT_LOADS
-#define UKV_NT_LOADS 1
-#endif
-#ifndef UKV_NT_STORES
-#define UKV_NT_STORES 1
-#endif
-
 template <typename T>
 __device__ __forceinline__ T load_stream(const void* p) {
-#if UKV_NT_LOADS
   return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
-#else
-  return *reinterpret_cast<const T*>(p);
-#endif
 }
 template <typename T>
 __device__ __forceinline__ void store_stream(void* p, T v) {
-#if UKV_NT_STORES
   __builtin_nontemporal_store(v, reinterpret_cast<T*>(p));
-#else
-  *reinterpret_cast<T*>(p) = v;
-#endif
 }
 __device__ __forceinline__ u32x4 load_stream16(const void* p) { return load_stream<u32x4>(p); }
 __device__ __forceinline__ u32x2 load_stream8(const void* p) { return load_stream<u32x2>(p); }
