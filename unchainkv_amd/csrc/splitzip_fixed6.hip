@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void palette_encode_tile(LaunchArgs a, En
   using P = Palette<kBits>;
   constexpr unsigned int kWaveCodeBytes = 128 * kBits;  // 1024 words
   __shared__ uint32_t s_rank[64];
-  __shared__ uint32_t s_code[(kThreads / kWave) * kWaveCodeBytes / 4];
+  __shared__ __align__(16) uint32_t s_code[(kThreads / kWave) * kWaveCodeBytes / 4];
   const unsigned int tid = threadIdx.x;
   const unsigned int lane = tid & (kWave - 1);
   const unsigned int wave = uniform(tid >> 6);
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, En
   constexpr unsigned int kWaveCodeBytes = 128 * kBits;
   constexpr unsigned int kMask = (1u << kBits) - 1u;
   __shared__ unsigned char s_pal[64];
-  __shared__ uint32_t s_code[(kThreads / kWave) * kWaveCodeBytes / 4];
+  __shared__ __align__(16) uint32_t s_code[(kThreads / kWave) * kWaveCodeBytes / 4];
   const unsigned int tid = threadIdx.x;
   const unsigned int lane = tid & (kWave - 1);
   const unsigned int wave = uniform(tid >> 6);
@@ -355,8 +355,10 @@ __global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, En
   const unsigned long long tile_word = t.plane * (t.n >> 1) + t.in_plane0;
   const uint32_t* codes = reinterpret_cast<const uint32_t*>(t.payload + P::kHeader + t.n +
                                                             tile_word * kBits / 8);
-  const unsigned int dwords = t.words * kBits / 32;
-  for (unsigned int k = tid; k < dwords; k += kThreads) s_code[k] = load_stream4(codes + k);
+  // the tile's code bytes, 16 at a time (a tile's share is a multiple of 16 bytes)
+  const unsigned int quads = t.words * kBits / 128;
+  for (unsigned int k = tid; k < quads; k += kThreads)
+    reinterpret_cast<u32x4*>(s_code)[k] = load_stream16(codes + 4 * k);
   if (tid < (unsigned int)P::kLimit) s_pal[tid] = t.payload[1 + tid];
   u32x2 low_a = {0, 0}, low_b = {0, 0};
   uint16_t* dst = nullptr;
@@ -382,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, En
       const uint32_t h1 = s_pal[(bits >> (kBits * (2 * k + 1))) & kMask];
       out[k] = (lo & 0xFF) | (h0 << 8) | ((lo >> 8) << 16) | (h1 << 24);
     }
-    store_stream16(dst + run * 512 + 8 * lane, u32x4{out[0], out[1], out[2], out[3]});
+    store_through16(dst + run * 512 + 8 * lane, u32x4{out[0], out[1], out[2], out[3]});
   }
 }
 
