@@ -155,6 +155,17 @@ def _is_cuda(tensor) -> bool:
     return getattr(getattr(tensor, "device", None), "type", "") == "cuda"
 
 
+def _stream_handle(device, torch) -> int:
+    """hipStream_t of the current stream of `device`. torch's raw-stream query
+    costs ~0.1 us against ~1.9 us for current_stream(device).cuda_stream (measured
+    on the MI355X host), a sixth of a small layer's host time per call."""
+    raw = getattr(getattr(torch, "_C", None), "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return int(raw(index))
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
 # ---------------------------------------------------------------------------
 # fixed6 / fixed5 (Top-16 fallback)
 
@@ -166,7 +177,7 @@ def encode_bf16(source, out, bits: int = 6) -> int | None:
         raise ValueError("splitzip bf16 bits must be 5 or 6")
     import torch
 
-    stream = torch.cuda.current_stream(source.device).cuda_stream
+    stream = _stream_handle(source.device, torch)
     encode_mode = getattr(lib, "kvq_splitzip_bf16_encode_mode", None)
     if encode_mode is not None:
         encoded = encode_mode(int(source.data_ptr()), int(out.data_ptr()), int(source.numel()),
@@ -298,7 +309,7 @@ def encode_top16(source, out, layer_index: int, *, codebooks: bytes | None = Non
     tables = _resolve_tables(layer_index, codebooks, source.device, torch)
     if tables is None:
         return None
-    stream = torch.cuda.current_stream(source.device).cuda_stream
+    stream = _stream_handle(source.device, torch)
     encoded = encode(int(source.data_ptr()), int(out.data_ptr()), int(source.numel()),
                      int(out.numel()), int(tables.data_ptr()), int(stream))
     if encoded < 0:
@@ -526,7 +537,7 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
     if tables is None:
         return None
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), batch._out_offsets,
@@ -561,7 +572,7 @@ def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Page
         return None
     offs = batch._c_array(src_offsets, batch.out_offsets, batch._out_offsets)
     encs = batch._c_array(encoded_bytes, batch.encoded_bytes, batch._encoded)
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
                     int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
@@ -592,7 +603,7 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
         return None
     batch.palette_layout(bits)
     offs = batch._palette[bits][3]
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), offs, int(out.numel()),
@@ -627,7 +638,7 @@ def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Paged
     else:
         offs = batch._c_array(src_offsets, None, None)
         encs = batch._c_array(encoded_bytes, None, None)
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
                     int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
@@ -695,7 +706,7 @@ def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_head
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
     offs = (ctypes.c_ulonglong * batch)(*map(int, payload_offsets))
     ctxs = (ctypes.c_ulonglong * batch)(*map(int, context_tokens))
-    stream = torch.cuda.current_stream(q.device).cuda_stream
+    stream = _stream_handle(q.device, torch)
     got = attend(int(q.data_ptr()), int(out.data_ptr()), int(payloads.data_ptr()), offs, ctxs,
                  int(block_tokens), batch, q_heads, kv_heads, head_dim, int(tables.data_ptr()),
                  int(workspace.data_ptr()), int(workspace.numel()), float(scale), int(stream))
@@ -748,7 +759,7 @@ def writeback_top16_paged(payloads, batch: PagedBatch, kv_layer, members, *, sta
         status = torch.empty(k, dtype=torch.uint8, device=kv_layer.device)
     elif status.dtype != torch.uint8 or status.numel() < k or status.device != kv_layer.device:
         raise ValueError("status must be a device uint8 tensor with one byte per member")
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     got = move(int(payloads.data_ptr()), offs, sizes, k, int(kv_layer.data_ptr()),
                int(kv_layer.stride(0)), int(kv_layer.stride(1)), batch.block_words, starts,
                counts, int(status.data_ptr()), int(stream))
@@ -786,7 +797,7 @@ def exponent_histogram_paged(kv_layer, batch: PagedBatch, *, workspace=None, cou
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=kv_layer.device)
     if counts is None:
         counts = torch.empty((2, 256), dtype=torch.int64, device=kv_layer.device)
-    stream = torch.cuda.current_stream(kv_layer.device).cuda_stream
+    stream = _stream_handle(kv_layer.device, torch)
     got = hist(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                batch.block_words, int(batch.ids.data_ptr()), count, int(counts.data_ptr()),
                int(workspace.data_ptr()), int(workspace.numel()), int(stream))
