@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
+from attention_ref import attention_f64
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -60,18 +61,6 @@ def kv_words(rng, books, tokens, kv_heads, escape_rate):
 
 def bf16_to_f64(words):
     return (words.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-
-
-def attention_f64(q, k, v):
-    """q (q_heads, 128); k, v (tokens, kv_heads, 128) -> (q_heads, 128)."""
-    group = q.shape[0] // k.shape[1]
-    out = np.empty_like(q)
-    for qh in range(q.shape[0]):
-        kh = k[:, qh // group]
-        s = kh @ q[qh] / np.sqrt(HEAD_DIM)
-        p = np.exp(s - s.max())
-        out[qh] = (p / p.sum()) @ v[:, qh // group]
-    return out
 
 
 def encode_sequences(sz, words_per_seq, kv_heads, books):
