@@ -139,6 +139,24 @@ def test_dropin_encode_matches_oracle(sz, codebooks, n, shift, roomy):
     assert bytes(backing[:shift].cpu().numpy()) == b"\xa5" * shift
 
 
+def test_dropin_encode_more_tiles_than_one_finalize_pass(sz, codebooks):
+    """A payload of 4100 tiles: the finalize scans the tile counts in two passes
+    (4096 tiles per pass when a payload has 16 finalize workgroups), and the
+    escape slots carry over from one pass to the next."""
+    n = 4100 * 4096
+    say("dropin encode, two finalize passes", n)
+    rng = np.random.default_rng(41)
+    books = codebooks[3 * 32:4 * 32]
+    words = random_words(rng, n, books, 0.004)
+    ref = oracle.top16_encode(words, oracle.top16_tables(books))
+    size = codec_format.top16_encoded_size(n)
+    out = torch.empty((size + 64,), dtype=torch.uint8, device="cuda")
+    got = sz.encode_top16(bf16(words), out, 3)
+    torch.cuda.synchronize()
+    assert got == size
+    assert bytes(out[:size].cpu().numpy()) == bytes(ref)
+
+
 def test_dropin_encode_unaligned_source(sz, codebooks):
     say("dropin encode unaligned source")
     rng = np.random.default_rng(5)
