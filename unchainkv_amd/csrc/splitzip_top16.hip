@@ -22,8 +22,9 @@
 //   top16_encode_lanes<fast, sequential>  any section alignment or geometry:
 //       16 consecutive words per lane (misaligned stores realigned through
 //       neighbour-lane shuffles); or one workgroup walking every tile in order.
-//   top16_encode_finalize    per payload: scan tile counts, place escapes in
-//       ascending order, zero unused slots, write the header.
+//   top16_encode_finalize    per payload (8 or 16 workgroups): scan tile counts,
+//       place escapes in ascending order, write the header (the tile kernel
+//       zeroes the escape slots of its span).
 //   top16_decode_tile / top16_decode_lanes / top16_decode_generic
 //       decode + scatter for aligned sections, any alignment, any geometry.
 //   top16_patch_escapes      apply escapes (any order) after decode.
