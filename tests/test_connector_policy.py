@@ -25,25 +25,25 @@ def test_backoff_single_flight_and_recovery():
     attempt = c._should_try_splitzip_top16(7, MIB)
     assert attempt == (True, 0, False)
     c._finish_splitzip_top16_attempt(7, *attempt[1:], True)
-    assert c._splitzip_top16_windows == {7: 1}
+    assert c.top16_gate.window(7) == 1
     for expected_window in (2, 4, 8, 16, 32, 32):
-        while c._splitzip_top16_cooldowns[7] > 0:
+        while c.top16_gate.skips_left(7) > 0:
             assert not c._should_try_splitzip_top16(7, MIB)[0]
         with ThreadPoolExecutor(max_workers=8) as pool:
             attempts = list(pool.map(lambda _: c._should_try_splitzip_top16(7, MIB), range(16)))
         probes = [a for a in attempts if a[0]]
         assert len(probes) == 1  # one probe in flight
         c._finish_splitzip_top16_attempt(7, probes[0][1], probes[0][2], True)
-        assert c._splitzip_top16_windows[7] == expected_window
-    while c._splitzip_top16_cooldowns[7] > 0:
+        assert c.top16_gate.window(7) == expected_window
+    while c.top16_gate.skips_left(7) > 0:
         c._should_try_splitzip_top16(7, MIB)
     probe = c._should_try_splitzip_top16(7, MIB)
     c._finish_splitzip_top16_attempt(7, *probe[1:], False)
-    assert 7 not in c._splitzip_top16_cooldowns and 7 not in c._splitzip_top16_windows
+    assert c.top16_gate.skips_left(7) is None and c.top16_gate.window(7) == 0
     assert "splitzip_top16_probe_success" in trace.names()
-    before = dict(c._splitzip_top16_cooldowns)
+    before = (c.top16_gate.epoch(7), c.top16_gate.skips_left(7))
     assert not c._should_try_splitzip_top16(7, MIB - 1)[0]
-    assert c._splitzip_top16_cooldowns == before
+    assert (c.top16_gate.epoch(7), c.top16_gate.skips_left(7)) == before
 
 
 def test_stale_ready_result_cannot_reset_backoff():
@@ -52,8 +52,8 @@ def test_stale_ready_result_cannot_reset_backoff():
     late = c._should_try_splitzip_top16(7, MIB)
     c._finish_splitzip_top16_attempt(7, *first[1:], True)
     c._finish_splitzip_top16_attempt(7, *late[1:], False)
-    assert c._splitzip_top16_cooldowns == {7: 1}
-    assert c._splitzip_top16_windows == {7: 1}
+    assert c.top16_gate.skips_left(7) == 1
+    assert c.top16_gate.window(7) == 1
     assert trace.names()[-1] == "splitzip_top16_stale_result"
 
 
@@ -61,9 +61,9 @@ def test_disable_is_sticky_and_epoch_guarded():
     c, trace = codec(top16=True)
     ok, epoch, _ = c._should_try_splitzip_top16(3, MIB)
     c._disable_splitzip_top16(3, epoch + 5)  # stale epoch: ignored
-    assert 3 not in c._splitzip_top16_unavailable_layers
+    assert not c.top16_gate.closed(3)
     c._disable_splitzip_top16(3, epoch)
-    assert 3 in c._splitzip_top16_unavailable_layers
+    assert c.top16_gate.closed(3)
     assert not c._should_try_splitzip_top16(3, MIB)[0]
     assert trace.names()[-2:] == ["splitzip_top16_stale_result", "splitzip_top16_unavailable"]
 
@@ -94,7 +94,7 @@ def test_codec_choice_top16_large_fixed6_small_and_fixed5_rules():
     both, _ = codec(top16=True, fixed5=True)
     assert both._choose_bits(0, MIB)[0] == BITS_TOP16
     assert both._choose_bits(0, 4096)[0] == BITS_FIXED5
-    both._splitzip_top16_unavailable_layers.add(0)
+    both.top16_gate.close(0)
     # Top-16 requested but unavailable for the layer: fixed6, not fixed5
     assert both._choose_bits(0, MIB)[0] == BITS_FIXED6
 

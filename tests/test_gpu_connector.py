@@ -126,7 +126,7 @@ def test_top16_overflow_falls_back_to_fixed6_and_backs_off(sz, codebooks):
     assert [p.bits for p in payloads] == [BITS_TOP16, BITS_FIXED6, BITS_TOP16]
     assert payloads[1].fallback and payloads[1].view[0] == codec_format.MODE_FIXED6
     assert bytes(payloads[1].view) == bytes(oracle.fixed6_encode(kv_host[:, tables[1]].reshape(-1)))
-    assert codec._splitzip_top16_windows == {2: 1}
+    assert codec.top16_gate.window(2) == 1
     assert "splitzip_top16_overflow" in trace.names()
     # the next payload of the layer waits out the window, then probes
     assert codec._choose_bits(2, 1 << 20)[0] == BITS_FIXED6
@@ -159,7 +159,7 @@ def test_layer_without_codebook_is_unavailable_and_sticks_to_fixed6(sz, codebook
     codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
     first = roundtrip(codec, 40, kv, tables, pool)
     assert first[0].bits == BITS_FIXED6 and first[0].fallback
-    assert 40 in codec._splitzip_top16_unavailable_layers
+    assert codec.top16_gate.closed(40)
     second = roundtrip(codec, 40, kv, tables, pool)
     assert second[0].bits == BITS_FIXED6 and not second[0].fallback
     # with an explicit codebook the layer uses Top-16

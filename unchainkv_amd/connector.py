@@ -39,10 +39,10 @@ prefill may reuse them (``preserve_source``).
 from __future__ import annotations
 
 import os
-import threading
 from dataclasses import dataclass, field
 
 from . import codec_format, frames
+from .backoff import Top16Backoff
 from .codebooks import summarize_symbol_counts
 from .trace import TraceWriter
 
@@ -157,12 +157,7 @@ class SplitzipLayerCodec:
         self.splitzip_fixed5_layers = set(config.fixed5_layers)
         self.splitzip_top16_max_cooldown_payloads = max(1, int(config.top16_max_cooldown))
         self._splitzip_fixed6_layers: set[int] = set()
-        self._splitzip_top16_unavailable_layers: set[int] = set()
-        self._splitzip_top16_cooldowns: dict[int, int] = {}
-        self._splitzip_top16_windows: dict[int, int] = {}
-        self._splitzip_top16_probe_layers: set[int] = set()
-        self._splitzip_top16_epochs: dict[int, int] = {}
-        self._splitzip_top16_lock = threading.Lock()
+        self.top16_gate = Top16Backoff(self.splitzip_top16_max_cooldown_payloads, self.trace.event)
         self._traced_bf16_exponents: set[tuple[str, int]] = set()
         self.codec_writeback = config.writeback and config.top16
         self.codec_writeback_overwrite = self.codec_writeback and not config.preserve_source
@@ -224,90 +219,23 @@ class SplitzipLayerCodec:
                              layer=layer_index, error=str(exc)[:160])
 
     # ------------------------------------------------------------------
-    # Top-16 backoff (vllm_connector.py:2906-3021)
+    # Top-16 backoff (behaviour of vllm_connector.py:2906-3021; state machine in
+    # backoff.Top16Backoff). The reference's method names are kept as the hooks.
 
     def _should_try_splitzip_top16(self, layer_index: int, raw_bytes: int):
         if not self.splitzip_top16 or raw_bytes < TOP16_MIN_BYTES:
             return False, -1, False
-        event, fields = None, {}
-        with self._splitzip_top16_lock:
-            epoch = self._splitzip_top16_epochs.get(layer_index, 0)
-            if layer_index in self._splitzip_top16_unavailable_layers:
-                return False, epoch, False
-            remaining = self._splitzip_top16_cooldowns.get(layer_index)
-            if remaining is None:
-                return True, epoch, False
-            if remaining > 0:
-                remaining -= 1
-                self._splitzip_top16_cooldowns[layer_index] = remaining
-                event = "splitzip_top16_cooldown_skip"
-                fields = {"layer": layer_index, "remaining": remaining,
-                          "window": self._splitzip_top16_windows[layer_index]}
-            elif layer_index in self._splitzip_top16_probe_layers:
-                event = "splitzip_top16_probe_wait_skip"
-                fields = {"layer": layer_index}
-            else:
-                epoch += 1
-                self._splitzip_top16_epochs[layer_index] = epoch
-                self._splitzip_top16_probe_layers.add(layer_index)
-                event = "splitzip_top16_probe"
-                fields = {"layer": layer_index,
-                          "window": self._splitzip_top16_windows[layer_index]}
-        self.trace.event(event, **fields)
-        if event == "splitzip_top16_probe":
-            return True, epoch, True
-        return False, epoch, False
+        return self.top16_gate.admit(layer_index)
 
     def _finish_splitzip_top16_attempt(self, layer_index: int, epoch: int, probe: bool,
                                        overflow: bool) -> None:
-        if layer_index < 0 or epoch < 0:
-            return
-        event, fields = None, {"layer": layer_index}
-        with self._splitzip_top16_lock:
-            if self._splitzip_top16_epochs.get(layer_index, 0) != epoch:
-                event = "splitzip_top16_stale_result"
-            elif overflow:
-                previous = self._splitzip_top16_windows.get(layer_index, 0)
-                window = (min(max(1, previous * 2), self.splitzip_top16_max_cooldown_payloads)
-                          if probe else 1)
-                self._splitzip_top16_windows[layer_index] = window
-                self._splitzip_top16_cooldowns[layer_index] = window
-                self._splitzip_top16_probe_layers.discard(layer_index)
-                self._splitzip_top16_epochs[layer_index] = epoch + 1
-                event = "splitzip_top16_overflow"
-                fields.update(window=window, probe=probe)
-            elif probe:
-                self._splitzip_top16_windows.pop(layer_index, None)
-                self._splitzip_top16_cooldowns.pop(layer_index, None)
-                self._splitzip_top16_probe_layers.discard(layer_index)
-                self._splitzip_top16_epochs[layer_index] = epoch + 1
-                event = "splitzip_top16_probe_success"
-        if event is not None:
-            self.trace.event(event, **fields)
+        self.top16_gate.settle(layer_index, epoch, probe, overflow)
 
     def _disable_splitzip_top16(self, layer_index: int, epoch: int) -> None:
-        if layer_index < 0 or epoch < 0:
-            return
-        disabled = False
-        with self._splitzip_top16_lock:
-            if self._splitzip_top16_epochs.get(layer_index, 0) == epoch:
-                self._splitzip_top16_unavailable_layers.add(layer_index)
-                self._splitzip_top16_cooldowns.pop(layer_index, None)
-                self._splitzip_top16_windows.pop(layer_index, None)
-                self._splitzip_top16_probe_layers.discard(layer_index)
-                self._splitzip_top16_epochs[layer_index] = epoch + 1
-                disabled = True
-        self.trace.event("splitzip_top16_unavailable" if disabled else "splitzip_top16_stale_result",
-                         layer=layer_index)
+        self.top16_gate.disable(layer_index, epoch)
 
     def _cancel_splitzip_top16_probe(self, layer_index: int, epoch: int, probe: bool) -> None:
-        if not probe:
-            return
-        with self._splitzip_top16_lock:
-            if self._splitzip_top16_epochs.get(layer_index, 0) != epoch:
-                return
-            self._splitzip_top16_probe_layers.discard(layer_index)
-        self.trace.event("splitzip_top16_probe_error", layer=layer_index)
+        self.top16_gate.cancel(layer_index, epoch, probe)
 
     def _choose_bits(self, layer_index: int, raw_bytes: int):
         """Codec choice of _splitzip_bf16_native_blocks (vllm_connector.py:3078-3094)."""

@@ -12,7 +12,7 @@ Every draw comes from torch generators seeded with seed * 1000 + layer.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 from . import codebooks as cb
 
@@ -103,16 +103,3 @@ def fit_codebook(torch, kv_layer, block_tables) -> bytes:
     hist = exponent_histograms(torch, kv_layer, block_tables).cpu().tolist()
     return cb.fit_layer_codebook(hist[0], hist[1])
 
-
-@dataclass
-class PagedWorkload:
-    """Several layers of one batch of requests over a block pool."""
-    shape: Shape
-    pool_blocks: int
-    tokens: list[int]
-    seed: int
-    block_tables: list[list[int]] = field(default_factory=list)
-
-    @property
-    def blocks_per_request(self) -> list[int]:
-        return [t // self.shape.block_size for t in self.tokens]
