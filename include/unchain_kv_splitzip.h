@@ -134,6 +134,28 @@ long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
     unsigned long long stream_ptr);
 
+/* No counterpart in the reference: kvq_splitzip_bf16_encode_top16_paged for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments, results and preconditions,
+ * without the workspace: the escape staging lives in a fixed array of
+ * kvq_splitzip_top16_noalloc_scratch_bytes() bytes (16 MiB) per GPU, owned by the
+ * library for the life of the process; the call allocates nothing. A batch that
+ * needs more than that (kvq_splitzip_top16_paged_workspace_bytes) returns -1 with
+ * the reason in kvq_splitzip_last_error(). Every call on one GPU shares the array:
+ * calls that overlap on one GPU (different streams, or different host threads)
+ * race and must be serialised by the caller. */
+long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long stream_ptr);
+
+/* Size of the fixed per-GPU scratch of kvq_splitzip_bf16_encode_top16_paged_noalloc
+ * (no counterpart in the reference). */
+unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes(void);
+
 /* Top-16 decode + scatter of a batch (no counterpart in the reference; it replaces one
  * kvq_splitzip_bf16_decode_top16_blocks call per request). Payload r is read from
  * src + src_offsets[r] and must be encoded_bytes[r] = E(n_r) long; it is written into

@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -1250,11 +1251,14 @@ unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
 
 }  // namespace
 
+namespace {
+
 // Gathers and encodes payload r = blocks ids[block_offsets[r] .. block_offsets[r+1])
 // of one paged layer into out + out_offsets[r], for every r, in one launch per 64
-// payloads. Returns the total encoded bytes, 0 on a failed precondition (see
-// the header), or -1 with kvq_splitzip_last_error() set.
-extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
+// payloads, with the workspace at workspace_ptr. Returns the total encoded bytes, 0
+// on a failed precondition (a workspace smaller than the batch needs included), or
+// -1 with the error recorded.
+long long encode_top16_paged_impl(
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long payload_count,
@@ -1313,6 +1317,92 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
     ws += workspace_words(tiles);
   }
   return (long long)total;
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned scratch for the entry point that allocates nothing: the encode's
+// per-tile escape counts and staged escapes live in this array instead of a
+// caller workspace. Each GPU holds its own copy for the life of the process; its
+// device address is looked up once per device (the array's host-side name is not
+// a device address) and every call on that GPU shares it.
+constexpr unsigned long long kStaticScratchBytes = 16ull << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mutex;
+unsigned long long g_scratch_ptr[kMaxDevices];  // 0: not looked up yet
+
+// Device address of `scratch` on the device that runs `stream` (0 on failure, with
+// the error recorded).
+unsigned long long scratch_address(hipStream_t stream) {
+  int device = 0;
+  hipError_t st = stream ? hipStreamGetDevice(stream, &device) : hipGetDevice(&device);
+  if (st != hipSuccess) {
+    fail("encode_top16_paged_noalloc: device of the stream", st);
+    return 0;
+  }
+  if (device < 0 || device >= kMaxDevices) {
+    fail_msg("encode_top16_paged_noalloc: device index out of range");
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == 0) {
+    int current = 0;
+    st = hipGetDevice(&current);
+    if (st == hipSuccess && current != device) st = hipSetDevice(device);
+    void* ptr = nullptr;
+    if (st == hipSuccess) st = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (current != device) (void)hipSetDevice(current);
+    if (st != hipSuccess || ptr == nullptr) {
+      fail("encode_top16_paged_noalloc: scratch address", st);
+      return 0;
+    }
+    g_scratch_ptr[device] = reinterpret_cast<unsigned long long>(ptr);
+  }
+  return g_scratch_ptr[device];
+}
+
+}  // namespace
+
+extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long stream_ptr) {
+  return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                 block_offsets, payload_count, out_ptr, out_offsets,
+                                 out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
+                                 stream_ptr);
+}
+
+extern "C" unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes() {
+  return kStaticScratchBytes;
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long stream_ptr) {
+  if (block_offsets != nullptr && payload_count != 0) {
+    const unsigned long long need =
+        kvq_splitzip_top16_paged_workspace_bytes(block_words, block_offsets, payload_count);
+    if (need > kStaticScratchBytes)
+      return fail_msg("encode_top16_paged_noalloc: the batch needs " + std::to_string(need) +
+                      " bytes of scratch, above the library's fixed " +
+                      std::to_string(kStaticScratchBytes) + " bytes; split the batch");
+  }
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  const unsigned long long ws = scratch_address(stream);
+  if (ws == 0) return -1;
+  return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                 block_offsets, payload_count, out_ptr, out_offsets,
+                                 out_capacity, tables_ptr, ws, kStaticScratchBytes, stream_ptr);
 }
 
 // Decodes payload r (src + src_offsets[r], encoded_bytes[r] long) and scatters it

@@ -63,6 +63,13 @@ _SIGNATURES = (
         ctypes.c_longlong,
         False,
     ),
+    (
+        "kvq_splitzip_bf16_encode_top16_paged_noalloc",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    ("kvq_splitzip_top16_noalloc_scratch_bytes", [], _U64, False),
     ("kvq_splitzip_palette_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
     ("kvq_splitzip_top16_decode_attention_workspace_bytes", [_U64] * 3, _U64, False),
     ("kvq_splitzip_exponent_histogram_workspace_bytes", [_U64] * 2, _U64, False),
@@ -546,6 +553,46 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
     if encoded < 0:
         _raise_last(lib, "splitzip top16 paged encode failed")
     return int(encoded) or None
+
+
+def encode_top16_paged_noalloc(kv_layer, batch: PagedBatch, out, layer_index: int = -1, *,
+                               codebooks: bytes | None = None, tables=None) -> int | None:
+    """``encode_top16_paged`` without a workspace argument and without any
+    allocation by the library: its scratch is a fixed array of
+    ``noalloc_scratch_bytes()`` bytes per GPU, shared by every call on that GPU
+    (calls that overlap on one GPU race). Raises ``RuntimeError`` for a batch
+    that needs more scratch than that."""
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_top16_paged_noalloc", None) if lib else None
+    if encode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    if tables is None:
+        tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
+    if tables is None:
+        return None
+    stream = _stream_handle(kv_layer.device, torch)
+    encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                     batch.payload_count, int(out.data_ptr()), batch._out_offsets,
+                     int(out.numel()), int(tables.data_ptr()), int(stream))
+    if encoded < 0:
+        _raise_last(lib, "splitzip top16 paged encode (no allocation) failed")
+    return int(encoded) or None
+
+
+def noalloc_scratch_bytes() -> int:
+    """Bytes of the library's fixed per-GPU scratch for encode_top16_paged_noalloc."""
+    lib = _load()
+    query = getattr(lib, "kvq_splitzip_top16_noalloc_scratch_bytes", None) if lib else None
+    if query is None:
+        raise RuntimeError(f"splitzip HIP library unavailable: {load_error()}")
+    return int(query())
 
 
 def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: PagedBatch,
