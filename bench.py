@@ -81,7 +81,7 @@ PROFILES = ROOT / "profiles"
 # kernels of one call of each direction (the roofline's unit of work)
 CALL_KERNELS = {
     "encode": ("top16_encode_tile", "top16_encode_finalize"),
-    "decode": ("top16_decode_tile", "top16_patch_escapes"),
+    "decode": ("top16_decode_tile_dir",),
     "attention": ("top16_attention_split", "top16_attention_combine"),
 }
 
@@ -233,6 +233,7 @@ def build_workload(torch, sz, workloads, name: str, seed: int):
          "send": send, "recv": recv, "device": device, "outliers": outliers,
          "kv": [], "tables": [], "books": [], "payloads": [], "plan": []}
     w["workspace"] = send.new_workspace()
+    w["dirs"] = []
     for layer in range(layers):
         cache = workloads.make_kv_layer(torch, shape, pool, seed=seed, layer=layer, device=device,
                                         outlier_rate=outliers)
@@ -241,6 +242,8 @@ def build_workload(torch, sz, workloads, name: str, seed: int):
         w["books"].append(book)
         w["tables"].append(sz.top16_tables_for(book, device, torch))
         w["payloads"].append(send.new_payload_buffer())
+        # the escape directory the encoder writes next to each layer's payloads
+        w["dirs"].append(send.new_directory())
     w["receiver"] = [torch.zeros_like(w["kv"][0]) for _ in range(layers)]
     plan_fallbacks(torch, sz, w)
     return w
@@ -280,7 +283,7 @@ def plan_fallbacks(torch, sz, w):
 
 def encode_top16(sz, w, layer):
     got = sz.encode_top16_paged(w["kv"][layer], w["send"], w["payloads"][layer], w["workspace"],
-                                tables=w["tables"][layer])
+                                tables=w["tables"][layer], directory=w["dirs"][layer])
     if got != w["send"].total_encoded_bytes:
         raise RuntimeError(f"layer {layer}: paged encode declined ({got})")
 
@@ -300,7 +303,8 @@ def decode_layer(sz, w, layer):
     send, plan = w["send"], w["plan"][layer]
     if not plan["over"]:
         got = sz.decode_top16_paged(w["payloads"][layer], send.out_offsets, send.encoded_bytes,
-                                    w["receiver"][layer], w["recv"], tables=w["tables"][layer])
+                                    w["receiver"][layer], w["recv"], tables=w["tables"][layer],
+                                    directory=w["dirs"][layer])
         if got != send.total_raw_bytes:
             raise RuntimeError(f"layer {layer}: paged decode declined ({got})")
         return
@@ -922,7 +926,7 @@ def main() -> int:
     dominant = (("encode", enc_call, enc_hbm, b_enc) if enc_call >= dec_call
                 else ("decode", dec_call, dec_hbm, b_dec))
     kernels = {"encode": "top16_encode_tile+top16_encode_finalize",
-               "decode": "top16_decode_tile+top16_patch_escapes"}
+               "decode": "top16_decode_tile_dir (escape directory)"}
     if overflowed:
         kernels = {"encode": "top16 encode + palette_presence/reduce/encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}

@@ -120,10 +120,25 @@ unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
     unsigned long long block_words, const unsigned long long* block_offsets,
     unsigned long long payload_count);
 
+/* Escape directory bytes of a batch (no counterpart in the reference): 68 bytes per
+ * 4096-word tile of each plane of each payload, 0 when block_words is not a
+ * multiple of 1024. The directory lists, per 1024-word chunk, where the chunk's
+ * escapes sit in the payload's ascending escape list and the first three of them,
+ * so that the decode applies escapes in its tile kernel instead of a second pass.
+ * It is written by the encode below or built on the host by
+ * kvq_splitzip_top16_build_directory; it is not part of the wire format. */
+unsigned long long kvq_splitzip_top16_paged_directory_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count);
+
 /* Gather + Top-16 encode (no counterpart in the reference; it replaces the
  * index_select + kvq_splitzip_bf16_encode_top16 pair per request). Payload r goes to
  * out + out_offsets[r]; payloads must not overlap and must fit in out_capacity.
- * workspace must hold kvq_splitzip_top16_paged_workspace_bytes() bytes. Returns the
+ * workspace must hold kvq_splitzip_top16_paged_workspace_bytes() bytes.
+ * directory_ptr: 0, or a 16-byte aligned device buffer of
+ * kvq_splitzip_top16_paged_directory_bytes() bytes that receives the escape
+ * directory (declined unless block_words is a multiple of 1024 and every body
+ * section is 16-byte aligned: (out + out_offsets[r] + 5) % 16 == 0). Returns the
  * sum of the encoded sizes, or 0 when a precondition fails. */
 long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
@@ -132,7 +147,7 @@ long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
-    unsigned long long stream_ptr);
+    unsigned long long directory_ptr, unsigned long long stream_ptr);
 
 /* No counterpart in the reference: kvq_splitzip_bf16_encode_top16_paged for callers
  * that cannot allocate (code under HIP graph capture, tight serving loops,
@@ -150,7 +165,7 @@ long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
     const unsigned long long* block_offsets, unsigned long long payload_count,
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
-    unsigned long long stream_ptr);
+    unsigned long long directory_ptr, unsigned long long stream_ptr);
 
 /* Size of the fixed per-GPU scratch of kvq_splitzip_bf16_encode_top16_paged_noalloc
  * (no counterpart in the reference). */
@@ -159,14 +174,32 @@ unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes(void);
 /* Top-16 decode + scatter of a batch (no counterpart in the reference; it replaces one
  * kvq_splitzip_bf16_decode_top16_blocks call per request). Payload r is read from
  * src + src_offsets[r] and must be encoded_bytes[r] = E(n_r) long; it is written into
- * the blocks of block table r. Returns the total raw bytes (sum of 2*n_r). */
+ * the blocks of block table r. directory_ptr: 0 (escapes applied by a second
+ * kernel, in any order), or the escape directory of these payloads (from their
+ * encode with the same block counts, or kvq_splitzip_top16_build_directory), with
+ * the conditions of the encode; the decode is then one kernel. Returns the total
+ * raw bytes (sum of 2*n_r). */
 long long kvq_splitzip_bf16_decode_top16_paged(
     unsigned long long src_ptr, const unsigned long long* src_offsets,
     const unsigned long long* encoded_bytes, unsigned long long payload_count,
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long tables_ptr,
-    unsigned long long stream_ptr);
+    unsigned long long directory_ptr, unsigned long long stream_ptr);
+
+/* Host-side escape directory of Top-16 payloads held in HOST memory (no counterpart
+ * in the reference): payload r at host_buf + offsets[r] (encoded_bytes[r] long, of
+ * the batch's block counts). Sorts each mode-5 payload's escape list by position in
+ * place (the decode's result does not depend on that order) and writes the
+ * directory (kvq_splitzip_top16_paged_directory_bytes() bytes) to host_directory,
+ * to be copied to the device with the payloads. Returns the directory bytes, or 0
+ * when block_words is not a multiple of 1024, directory_bytes is too small or a
+ * size is not E(n_r). */
+long long kvq_splitzip_top16_build_directory(
+    unsigned char* host_buf, const unsigned long long* offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned char* host_directory, unsigned long long directory_bytes);
 
 /* Workspace bytes that kvq_splitzip_bf16_encode_mode_paged needs for this batch (no
  * counterpart in the reference). */

@@ -41,7 +41,7 @@ def test_noalloc_refuses_batches_beyond_its_scratch():
     need = int(lib.kvq_splitzip_top16_paged_workspace_bytes(block_words, offsets, 256))
     assert need > cap
     rc = lib.kvq_splitzip_bf16_encode_top16_paged_noalloc(
-        16, 1 << 30, 1 << 14, block_words, 16, offsets, 256, 16, _u64s([0] * 256), 1 << 40, 16, 0)
+        16, 1 << 30, 1 << 14, block_words, 16, offsets, 256, 16, _u64s([0] * 256), 1 << 40, 16, 0, 0)
     assert rc == -1
     message = lib.kvq_splitzip_last_error().decode()
     assert "scratch" in message and str(need) in message and str(cap) in message
@@ -57,10 +57,10 @@ def _encode_both(lib, kv, batch, tables):
               int(batch.ids.data_ptr()), batch._block_offsets, batch.payload_count)
     a = lib.kvq_splitzip_bf16_encode_top16_paged(
         *common, int(ref.data_ptr()), batch._out_offsets, int(ref.numel()),
-        int(tables.data_ptr()), int(ws.data_ptr()), int(ws.numel()), stream)
+        int(tables.data_ptr()), int(ws.data_ptr()), int(ws.numel()), 0, stream)
     b = lib.kvq_splitzip_bf16_encode_top16_paged_noalloc(
         *common, int(got.data_ptr()), batch._out_offsets, int(got.numel()),
-        int(tables.data_ptr()), stream)
+        int(tables.data_ptr()), 0, stream)
     torch.cuda.synchronize(kv.device)
     return a, b, ref.cpu().numpy(), got.cpu().numpy()
 

@@ -64,8 +64,20 @@ struct LaunchArgs {
   unsigned int tile_shift;            // log2 of the tile size in words
   unsigned int uniform_tiles;         // tiles of every payload when all are equal, else 0
   unsigned int uniform_slot_groups;   // escape-patch workgroups of every payload, likewise
+  // Escape directory of the launch's tiles (Top-16 tile kernels only; null when
+  // absent): per 1024-word wave chunk of tile t a record dir_rec[4 * (4t + wave)
+  // .. + 4) = {tile-relative slot of the chunk's first escape | chunk escapes << 16,
+  // up to kDirInline of them as (tile-local position << 8 | exponent)}, and per
+  // tile dir_base[t] = payload slot of the tile's first escape.
+  uint32_t* dir_rec;
+  uint32_t* dir_base;
   PayloadDesc p[kMaxPayloads];
 };
+
+// Escapes of a wave chunk held in its directory record.
+constexpr int kDirInline = 3;
+// Directory bytes per tile: four 16-byte chunk records and the tile's base slot.
+constexpr unsigned long long kDirBytesPerTile = 4 * 16 + 4;
 
 // ---------------------------------------------------------------------------
 // streaming (nontemporal) vector memory access: the codec reads its source once

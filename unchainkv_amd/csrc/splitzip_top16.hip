@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstring>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -604,6 +605,11 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
     total += v;
   }
   if (tid == 0) a.workspace[tile] = total;
+  // directory record of this wave's chunk: its first escape's slot within the tile,
+  // its escape count, and its first kDirInline escapes (written by the lanes that
+  // hold them, below)
+  uint32_t* rec = a.dir_rec ? a.dir_rec + 4 * (4 * (unsigned long long)tile + wave) : nullptr;
+  if (rec && lane == 0) rec[0] = before | ((wave_a + (wave_tot >> 16)) << 16);
   if (mask_a | mask_b) {
     const unsigned int excl = incl - cnt;
     unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
@@ -612,16 +618,19 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (!((mask_a >> j) & 1)) continue;
-      if (idx < kStageSlots)
-        staged[idx] = ((local + j) << 8) | ((x[j >> 1] >> (7 + 16 * (j & 1))) & 0xFF);
+      const uint32_t e = ((local + j) << 8) | ((x[j >> 1] >> (7 + 16 * (j & 1))) & 0xFF);
+      if (idx < kStageSlots) staged[idx] = e;
+      if (rec && idx - before < kDirInline) rec[1 + idx - before] = e;
       ++idx;
     }
     idx = before + wave_a + (excl >> 16);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (!((mask_b >> j) & 1)) continue;
-      if (idx < kStageSlots)
-        staged[idx] = ((local + 512 + j) << 8) | ((x[4 + (j >> 1)] >> (7 + 16 * (j & 1))) & 0xFF);
+      const uint32_t e =
+          ((local + 512 + j) << 8) | ((x[4 + (j >> 1)] >> (7 + 16 * (j & 1))) & 0xFF);
+      if (idx < kStageSlots) staged[idx] = e;
+      if (rec && idx - before < kDirInline) rec[1 + idx - before] = e;
       ++idx;
     }
   }
@@ -692,6 +701,92 @@ __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, Enco
   // compiler sinks them under the test and the mode byte's round trip comes first.
   asm volatile("" ::"v"(out_a), "v"(out_b));
   // the reference decoder leaves a payload whose byte 0 is not 5 untouched
+  if (mode != 5) return;
+  store_through16(dst + 8 * lane, out_a);
+  store_through16(dst + 512 + 8 * lane, out_b);
+}
+
+// Replaces the exponent of word w (0..1023) of this wave's chunk, held in run A
+// (w < 512) or run B of lane (w & 511) / 8, by `exponent` (kvq_splitzip_cuda.cu:
+// 276-281: sign and mantissa stay, bits 7-14 take the escape's exponent). w and
+// exponent are wave-uniform; only the owning lane's dword changes. Branch-free
+// selects over the eight dwords (no register indexing).
+__device__ __forceinline__ void patch_word(u32x4& run_a, u32x4& run_b, unsigned int lane,
+                                           unsigned int w, unsigned int exponent) {
+  const unsigned int half = 16 * (w & 1);
+  const uint32_t clear = lane == ((w & 511) >> 3) ? (0x7F80u << half) : 0u;
+  const uint32_t bits = (exponent << (7 + half)) & clear;
+  const unsigned int d = ((w >> 9) << 2) | ((w >> 1) & 3);  // dword of the two runs
+#define UKV_PATCH(v, k) v = (d == (k)) ? ((v & ~clear) | bits) : v
+  UKV_PATCH(run_a.x, 0); UKV_PATCH(run_a.y, 1); UKV_PATCH(run_a.z, 2); UKV_PATCH(run_a.w, 3);
+  UKV_PATCH(run_b.x, 4); UKV_PATCH(run_b.y, 5); UKV_PATCH(run_b.z, 6); UKV_PATCH(run_b.w, 7);
+#undef UKV_PATCH
+}
+
+// Decode + scatter with the escape directory the encoder wrote (one kernel, no
+// patch pass): each wave reads its chunk's record and its tile's base slot along
+// with the payload, and puts the chunk's escapes into its registers before the
+// stores. A chunk with more than kDirInline escapes reads them from the payload's
+// (ascending) escape list at slots base + first .. + count.
+template <bool kIds>
+__global__ __launch_bounds__(kThreads) void top16_decode_tile_dir(LaunchArgs a, EncodeGeom geo) {
+  const unsigned int lane = threadIdx.x & (kWave - 1);
+  const unsigned int wave = uniform(threadIdx.x >> 6);
+  const unsigned int tile = group_index();
+  const PlaneTile t = plane_tile<kTileShift>(a, tile);
+  const unsigned int in_plane = t.in_plane0 + wave * 1024;
+  const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
+  if (wave * 1024 >= t.words) return;  // whole waves; no barrier in this kernel
+  const u32x4 rec =
+      *reinterpret_cast<const u32x4*>(a.dir_rec + 4 * (4 * (unsigned long long)tile + wave));
+  const unsigned int tile_base = a.dir_base[tile];
+  const unsigned int mode = t.payload[0];
+  const uint32_t* cbw = reinterpret_cast<const uint32_t*>(a.tables + 512 + t.plane * 16);
+  const uint32_t cb[4] = {cbw[0], cbw[1], cbw[2], cbw[3]};
+  const unsigned char* pbody = t.payload + 5 + wstart;
+  const unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
+  const u32x2 body_a = load_stream8(pbody + 8 * lane);
+  const u32x2 body_b = load_stream8(pbody + 512 + 8 * lane);
+  const uint32_t code_a = load_stream4(pcode + 4 * lane);
+  const uint32_t code_b = load_stream4(pcode + 256 + 4 * lane);
+  __builtin_amdgcn_sched_barrier(0);
+  uint16_t* dst = a.kv + wave_source<kIds>(a, t, geo, in_plane);
+  u32x4 out_a = decode_run8(body_a, code_a, cb);
+  u32x4 out_b = decode_run8(body_b, code_b, cb);
+  const unsigned int first = uniform(rec.x & 0xFFFFu);
+  const unsigned int count = uniform(rec.x >> 16);
+  const unsigned int chunk0 = wave * 1024;  // tile-local position of the chunk's first word
+  if (count != 0) {
+    if (count <= (unsigned int)kDirInline) {
+      const uint32_t inl[kDirInline] = {uniform(rec.y), uniform(rec.z), uniform(rec.w)};
+#pragma unroll
+      for (int i = 0; i < kDirInline; ++i)
+        if ((unsigned int)i < count)
+          patch_word(out_a, out_b, lane, ((inl[i] >> 8) - chunk0) & 1023u, inl[i] & 0xFF);
+    } else if (mode == 5 && (unsigned long long)tile_base + first + count <=
+                                escape_capacity(t.n)) {
+      // escape-dense chunk: entries from the payload, 64 per round (an overflowed
+      // payload, whose slots stop at the capacity, is not stored at all)
+      const unsigned char* entries = t.payload + 5 + t.n + (t.n >> 1);
+      const unsigned long long slot0 = (unsigned long long)tile_base + first;
+      for (unsigned int r0 = 0; r0 < count; r0 += kWave) {
+        unsigned int pos = 0xFFFFFFFFu, ex = 0;
+        if (r0 + lane < count) {
+          const unsigned char* e = entries + 5 * (slot0 + r0 + lane);
+          pos = *reinterpret_cast<const u32_unaligned*>(e);
+          ex = e[4];
+        }
+        const unsigned int m = min(count - r0, (unsigned int)kWave);
+        for (unsigned int i = 0; i < m; ++i) {
+          const unsigned long long p = (unsigned int)__builtin_amdgcn_readlane((int)pos, i);
+          const unsigned int xe = (unsigned int)__builtin_amdgcn_readlane((int)ex, i);
+          if (p >= wstart && p < wstart + 1024)
+            patch_word(out_a, out_b, lane, (unsigned int)(p - wstart), xe);
+        }
+      }
+    }
+  }
+  asm volatile("" ::"v"(out_a), "v"(out_b));
   if (mode != 5) return;
   store_through16(dst + 8 * lane, out_a);
   store_through16(dst + 512 + 8 * lane, out_b);
@@ -789,6 +884,8 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       if ((unsigned int)k == grp) c = mine[k];
     }
     const unsigned long long base = running + prefix;
+    if (a.dir_base && own < m)
+      a.dir_base[d.tile_begin + chunk0 + own] = (unsigned int)min(base, 0xFFFFFFFFull);
     if (c != 0 && base < cap) {
       if (c > (unsigned int)kStageSlots) {
         const unsigned int q = atomicAdd(&s_over_count, 1u);
@@ -1035,6 +1132,13 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
 
 long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream) {
   const dim3 block(kThreads);
+  if (a.dir_rec) {  // the host only passes a directory with the tile plan
+    if (a.ids)
+      hipLaunchKernelGGL(top16_decode_tile_dir<true>, dim3(a.total_tiles), block, 0, stream, a, g);
+    else
+      hipLaunchKernelGGL(top16_decode_tile_dir<false>, dim3(a.total_tiles), block, 0, stream, a, g);
+    return check_launch("top16_decode_tile_dir");
+  }
   switch (p.kernel) {
     case Kernel::kTile:
       if (a.ids)
@@ -1203,7 +1307,33 @@ extern "C" unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
   return workspace_words(tiles) * 4;
 }
 
+// Escape directory bytes of a batch (0 when block_words is not a multiple of 1024,
+// the geometry of the tile kernels, which alone read and write a directory).
+extern "C" unsigned long long kvq_splitzip_top16_paged_directory_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count) {
+  if (block_offsets == nullptr || block_words == 0 || block_words % 1024 != 0) return 0;
+  unsigned long long tiles = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+    tiles += host_payload_tiles(2 * (block_offsets[r + 1] - block_offsets[r]) * block_words, true,
+                                kTileShift);
+  }
+  return tiles * kDirBytesPerTile;
+}
+
 namespace {
+
+// Points launch `a` (whose first tile is call tile `tile_offset`) at its part of a
+// call's directory of `call_tiles` tiles: the chunk records of every tile, then
+// the tile base slots.
+void set_directory(LaunchArgs& a, unsigned long long directory_ptr, unsigned long long call_tiles,
+                   unsigned long long tile_offset) {
+  if (directory_ptr == 0) return;
+  uint32_t* dir = reinterpret_cast<uint32_t*>(directory_ptr);
+  a.dir_rec = dir + 16 * tile_offset;
+  a.dir_base = dir + 16 * call_tiles + tile_offset;
+}
 
 struct PagedGeometry {
   unsigned long long kv_ptr, plane_stride, block_stride, block_words, ids_ptr;
@@ -1265,7 +1395,7 @@ long long encode_top16_paged_impl(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
-    unsigned long long stream_ptr) {
+    unsigned long long directory_ptr, unsigned long long stream_ptr) {
   if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || tables_ptr == 0 || workspace_ptr == 0 ||
       block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 || block_words == 0 ||
       block_words > 0xFFFFFFFFULL)
@@ -1295,9 +1425,17 @@ long long encode_top16_paged_impl(
       paged_aligned(out_ptr, block_offsets, out_offsets, payload_count, block_words) &&
           tables_ptr % 4 == 0 && block_words % 1024 == 0,
       false);
+  const unsigned long long dir_tiles =
+      kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count) /
+      kDirBytesPerTile;
+  // a directory is written by the tile kernels only
+  if (directory_ptr != 0 && (plan.kernel != Kernel::kTile || directory_ptr % 16 != 0 ||
+                             dir_tiles == 0))
+    return 0;
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned int* ws = reinterpret_cast<unsigned int*>(workspace_ptr);
+  unsigned long long tile_offset = 0;
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
     LaunchArgs a{};
     a.kv = reinterpret_cast<uint16_t*>(kv_ptr);
@@ -1312,9 +1450,11 @@ long long encode_top16_paged_impl(
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
     const unsigned int tiles = fill_descs(a, pg, block_offsets, out_offsets, first, count, plan);
     a.workspace = ws;
+    set_directory(a, directory_ptr, dir_tiles, tile_offset);
     long long rc = launch_encode(a, g, plan, stream);
     if (rc < 0) return rc;
     ws += workspace_words(tiles);
+    tile_offset += tiles;
   }
   return (long long)total;
 }
@@ -1371,11 +1511,11 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
-    unsigned long long stream_ptr) {
+    unsigned long long directory_ptr, unsigned long long stream_ptr) {
   return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
                                  block_offsets, payload_count, out_ptr, out_offsets,
                                  out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
-                                 stream_ptr);
+                                 directory_ptr, stream_ptr);
 }
 
 extern "C" unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes() {
@@ -1388,7 +1528,7 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
     const unsigned long long* block_offsets, unsigned long long payload_count,
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
-    unsigned long long stream_ptr) {
+    unsigned long long directory_ptr, unsigned long long stream_ptr) {
   if (block_offsets != nullptr && payload_count != 0) {
     const unsigned long long need =
         kvq_splitzip_top16_paged_workspace_bytes(block_words, block_offsets, payload_count);
@@ -1402,7 +1542,8 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
   if (ws == 0) return -1;
   return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
                                  block_offsets, payload_count, out_ptr, out_offsets,
-                                 out_capacity, tables_ptr, ws, kStaticScratchBytes, stream_ptr);
+                                 out_capacity, tables_ptr, ws, kStaticScratchBytes,
+                                 directory_ptr, stream_ptr);
 }
 
 // Decodes payload r (src + src_offsets[r], encoded_bytes[r] long) and scatters it
@@ -1414,7 +1555,7 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long tables_ptr,
-    unsigned long long stream_ptr) {
+    unsigned long long directory_ptr, unsigned long long stream_ptr) {
   if (src_ptr == 0 || kv_ptr == 0 || block_ids_ptr == 0 || tables_ptr == 0 ||
       src_offsets == nullptr || encoded_bytes == nullptr || block_offsets == nullptr ||
       payload_count == 0 || block_words == 0 || block_words > 0xFFFFFFFFULL)
@@ -1432,8 +1573,15 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
       paged_fast(pg),
       paged_aligned(src_ptr, block_offsets, src_offsets, payload_count, block_words) &&
           tables_ptr % 4 == 0 && block_words % 1024 == 0 && max_plane < kTilePlaneLimit);
+  const unsigned long long dir_tiles =
+      kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count) /
+      kDirBytesPerTile;
+  if (directory_ptr != 0 && (plan.kernel != Kernel::kTile || directory_ptr % 16 != 0 ||
+                             dir_tiles == 0))
+    return 0;
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  unsigned long long tile_offset = 0;
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
     LaunchArgs a{};
     a.kv = reinterpret_cast<uint16_t*>(kv_ptr);
@@ -1446,9 +1594,87 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
     apply_plan(a, plan);
     const unsigned int count =
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
-    fill_descs(a, pg, block_offsets, src_offsets, first, count, plan);
+    const unsigned int tiles = fill_descs(a, pg, block_offsets, src_offsets, first, count, plan);
+    set_directory(a, directory_ptr, dir_tiles, tile_offset);
     long long rc = launch_decode(a, g, plan, stream);
     if (rc < 0) return rc;
+    tile_offset += tiles;
   }
   return (long long)total;
+}
+
+// ---------------------------------------------------------------------------
+// host-built escape directory (payloads that arrive in host memory)
+
+extern "C" long long kvq_splitzip_top16_build_directory(
+    unsigned char* host_buf, const unsigned long long* offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned char* host_directory, unsigned long long directory_bytes) {
+  if (host_buf == nullptr || offsets == nullptr || encoded_bytes == nullptr ||
+      host_directory == nullptr || payload_count == 0)
+    return 0;
+  const unsigned long long need =
+      kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count);
+  if (need == 0 || need > directory_bytes) return 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    if (encoded_bytes[r] != encoded_size(n)) return 0;
+  }
+  const unsigned long long call_tiles = need / kDirBytesPerTile;
+  uint32_t* rec = reinterpret_cast<uint32_t*>(host_directory);
+  uint32_t* tile_base = rec + 16 * call_tiles;
+  std::fill(rec, rec + 17 * call_tiles, 0u);
+
+  std::vector<std::pair<uint32_t, uint8_t>> list;
+  unsigned long long tile0 = 0;  // call tile of the payload's first tile
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    const unsigned long long half = n / 2;
+    const unsigned long long tpp = (half + kTileWords - 1) / kTileWords;
+    unsigned char* payload = host_buf + offsets[r];
+    const unsigned long long cap = escape_capacity(n);
+    unsigned long long count = (unsigned long long)payload[1] | (payload[2] << 8) |
+                               ((unsigned long long)payload[3] << 16) |
+                               ((unsigned long long)payload[4] << 24);
+    count = std::min(count, cap);
+    if (payload[0] == 5 && count != 0) {
+      // the list in position order (stable: a repeated position keeps its order, so
+      // the last entry still wins as it would in slot order)
+      unsigned char* entries = payload + 5 + n + (n + 1) / 2;
+      list.resize(count);
+      for (unsigned long long s = 0; s < count; ++s) {
+        uint32_t pos;
+        std::memcpy(&pos, entries + 5 * s, 4);
+        list[s] = {pos, entries[5 * s + 4]};
+      }
+      std::stable_sort(list.begin(), list.end(),
+                       [](const std::pair<uint32_t, uint8_t>& x,
+                          const std::pair<uint32_t, uint8_t>& y) { return x.first < y.first; });
+      for (unsigned long long s = 0; s < count; ++s) {
+        std::memcpy(entries + 5 * s, &list[s].first, 4);
+        entries[5 * s + 4] = list[s].second;
+      }
+      // entries at or beyond n are not applied and sort last
+      unsigned long long slot = 0;
+      for (unsigned long long j = 0; j < 2 * tpp; ++j) {
+        tile_base[tile0 + j] = (uint32_t)slot;
+        const unsigned long long plane = j >= tpp ? 1 : 0;
+        const unsigned long long lo = plane * half + (j - plane * tpp) * kTileWords;
+        const unsigned long long hi = std::min(lo + kTileWords, (plane + 1) * half);
+        const unsigned long long first_slot = slot;
+        while (slot < count && list[slot].first < hi) {
+          const unsigned long long local = list[slot].first - lo;  // tile-local position
+          uint32_t* c = rec + 16 * (tile0 + j) + 4 * (local >> 10);
+          const uint32_t k = c[0] >> 16;
+          if (k == 0) c[0] = (uint32_t)(slot - first_slot);
+          if (k < (uint32_t)kDirInline) c[1 + k] = (uint32_t)(local << 8) | list[slot].second;
+          c[0] = (c[0] & 0xFFFFu) | ((k + 1) << 16);
+          ++slot;
+        }
+      }
+    }
+    tile0 += 2 * tpp;
+  }
+  return (long long)need;
 }

@@ -51,21 +51,29 @@ _SIGNATURES = (
     ("kvq_splitzip_bf16_decode_top16_blocks", [_U64] * 12, ctypes.c_longlong, False),
     ("kvq_splitzip_last_error", [], ctypes.c_char_p, True),
     ("kvq_splitzip_top16_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
+    ("kvq_splitzip_top16_paged_directory_bytes", [_U64, _U64P, _U64], _U64, False),
+    (
+        "kvq_splitzip_top16_build_directory",
+        [ctypes.c_void_p, _U64P, _U64P, _U64, _U64, _U64P, ctypes.c_void_p, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
     (
         "kvq_splitzip_bf16_encode_top16_paged",
-        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64],
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64,
+         _U64],
         ctypes.c_longlong,
         False,
     ),
     (
         "kvq_splitzip_bf16_decode_top16_paged",
-        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64],
+        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64],
         ctypes.c_longlong,
         False,
     ),
     (
         "kvq_splitzip_bf16_encode_top16_paged_noalloc",
-        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64],
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64],
         ctypes.c_longlong,
         False,
     ),
@@ -466,6 +474,22 @@ class PagedBatch:
         return torch.empty(max(self.workspace_bytes(), 16), dtype=torch.uint8,
                            device=self.device)
 
+    def directory_bytes(self) -> int:
+        """Bytes of the batch's escape directory (0 when its block geometry has none:
+        block words not a multiple of 1024)."""
+        lib = _load()
+        query = getattr(lib, "kvq_splitzip_top16_paged_directory_bytes", None) if lib else None
+        if query is None:
+            raise RuntimeError(f"splitzip HIP library unavailable: {load_error()}")
+        return int(query(self.block_words, self._block_offsets, self.payload_count))
+
+    def new_directory(self, torch=None):
+        """Device buffer for the escape directory, or None when the batch has none."""
+        if torch is None:
+            import torch
+        size = self.directory_bytes()
+        return torch.empty(size, dtype=torch.uint8, device=self.device) if size else None
+
     def payload(self, out, r: int):
         return out[self.out_offsets[r]:self.out_offsets[r] + self.encoded_bytes[r]]
 
@@ -521,15 +545,29 @@ def _paged_layout_ok(kv_layer, batch: PagedBatch, torch) -> bool:
 def _payloads_fit(source, src_offsets, encoded_bytes, batch: PagedBatch) -> bool:
     if len(src_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
         return False
-    size = source.numel()
+    size = source.numel() if hasattr(source, "numel") and callable(source.numel) else source.size
     return all(o + e <= size for o, e in zip(src_offsets, encoded_bytes))
 
 
+def _directory_ptr(directory, batch: PagedBatch, torch) -> int | None:
+    """Device address of an escape directory (0 for none); None when unusable."""
+    if directory is None:
+        return 0
+    if directory.dtype != torch.uint8 or not directory.is_contiguous() or \
+            directory.device != batch.ids.device or directory.numel() < batch.directory_bytes():
+        return None
+    return int(directory.data_ptr())
+
+
 def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index: int = -1, *,
-                       codebooks: bytes | None = None, tables=None) -> int | None:
+                       codebooks: bytes | None = None, tables=None,
+                       directory=None) -> int | None:
     """Gather + Top-16 encode every request of ``batch`` from one paged layer
     ``(2, num_blocks, ...)`` into ``out`` (a ``batch.out_bytes`` uint8 buffer).
-    Returns the total encoded bytes or ``None`` when the codec declines."""
+    With ``directory`` (``batch.new_directory()``) the encoder also writes the
+    escape directory that lets ``decode_top16_paged`` apply escapes without a
+    second pass. Returns the total encoded bytes or ``None`` when the codec
+    declines."""
     lib = _load()
     encode = getattr(lib, "kvq_splitzip_bf16_encode_top16_paged", None) if lib else None
     if encode is None:
@@ -542,21 +580,23 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
         return None
     if tables is None:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
-    if tables is None:
+    dir_ptr = _directory_ptr(directory, batch, torch)
+    if tables is None or dir_ptr is None:
         return None
     stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), batch._out_offsets,
                      int(out.numel()), int(tables.data_ptr()), int(workspace.data_ptr()),
-                     int(workspace.numel()), int(stream))
+                     int(workspace.numel()), dir_ptr, int(stream))
     if encoded < 0:
         _raise_last(lib, "splitzip top16 paged encode failed")
     return int(encoded) or None
 
 
 def encode_top16_paged_noalloc(kv_layer, batch: PagedBatch, out, layer_index: int = -1, *,
-                               codebooks: bytes | None = None, tables=None) -> int | None:
+                               codebooks: bytes | None = None, tables=None,
+                               directory=None) -> int | None:
     """``encode_top16_paged`` without a workspace argument and without any
     allocation by the library: its scratch is a fixed array of
     ``noalloc_scratch_bytes()`` bytes per GPU, shared by every call on that GPU
@@ -574,13 +614,14 @@ def encode_top16_paged_noalloc(kv_layer, batch: PagedBatch, out, layer_index: in
         return None
     if tables is None:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
-    if tables is None:
+    dir_ptr = _directory_ptr(directory, batch, torch)
+    if tables is None or dir_ptr is None:
         return None
     stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), batch._out_offsets,
-                     int(out.numel()), int(tables.data_ptr()), int(stream))
+                     int(out.numel()), int(tables.data_ptr()), dir_ptr, int(stream))
     if encoded < 0:
         _raise_last(lib, "splitzip top16 paged encode (no allocation) failed")
     return int(encoded) or None
@@ -597,10 +638,13 @@ def noalloc_scratch_bytes() -> int:
 
 def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: PagedBatch,
                        layer_index: int = -1, *, codebooks: bytes | None = None,
-                       tables=None) -> int | None:
+                       tables=None, directory=None) -> int | None:
     """Decode payload r (``source[src_offsets[r]:][:encoded_bytes[r]]``) and scatter
     it into ``batch.block_tables[r]`` of the paged layer ``kv_layer``; one launch
-    for every request. Returns the total raw bytes written or ``None``."""
+    for every request. ``directory``: the escape directory written by the encode of
+    these payloads (for a batch with the same block counts), or built on the host
+    by ``build_directory``; the decode is then one kernel. Returns the total raw
+    bytes written or ``None``."""
     lib = _load()
     decode = getattr(lib, "kvq_splitzip_bf16_decode_top16_paged", None) if lib else None
     if decode is None:
@@ -615,7 +659,8 @@ def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Page
         return None
     if tables is None:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
-    if tables is None:
+    dir_ptr = _directory_ptr(directory, batch, torch)
+    if tables is None or dir_ptr is None:
         return None
     offs = batch._c_array(src_offsets, batch.out_offsets, batch._out_offsets)
     encs = batch._c_array(encoded_bytes, batch.encoded_bytes, batch._encoded)
@@ -623,10 +668,39 @@ def decode_top16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Page
     copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
                     int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
-                    int(tables.data_ptr()), int(stream))
+                    int(tables.data_ptr()), dir_ptr, int(stream))
     if copied < 0:
         _raise_last(lib, "splitzip top16 paged decode failed")
     return int(copied) or None
+
+
+def build_directory(host_payloads, src_offsets, encoded_bytes, batch: PagedBatch):
+    """Escape directory of Top-16 payloads held in host memory (a writable uint8
+    numpy array or CPU tensor; payload r at ``src_offsets[r]``, ``encoded_bytes[r]``
+    long, of ``batch``'s block counts), as a uint8 numpy array to copy to the
+    device with the payloads. Each mode-5 payload's escape list is sorted by
+    position in place (the decode does not depend on its order). ``None`` when the
+    batch's geometry has no directory or a size does not match."""
+    import numpy as np
+
+    lib = _load()
+    build = getattr(lib, "kvq_splitzip_top16_build_directory", None) if lib else None
+    if build is None:
+        return None
+    buf = host_payloads.numpy() if hasattr(host_payloads, "numpy") else host_payloads
+    if buf.dtype != np.uint8 or not buf.flags["C_CONTIGUOUS"] or not buf.flags["WRITEABLE"]:
+        raise ValueError("host payloads must be a writable contiguous uint8 array")
+    if not _payloads_fit(buf.reshape(-1), src_offsets, encoded_bytes, batch):
+        return None
+    size = batch.directory_bytes()
+    if not size:
+        return None
+    out = np.empty(size, dtype=np.uint8)
+    offs = batch._c_array(src_offsets, batch.out_offsets, batch._out_offsets)
+    encs = batch._c_array(encoded_bytes, batch.encoded_bytes, batch._encoded)
+    got = build(buf.ctypes.data, offs, encs, batch.payload_count, batch.block_words,
+                batch._block_offsets, out.ctypes.data, size)
+    return out if got == size else None
 
 
 # ---------------------------------------------------------------------------
