@@ -64,6 +64,7 @@ struct LaunchArgs {
   unsigned int tile_shift;            // log2 of the tile size in words
   unsigned int uniform_tiles;         // tiles of every payload when all are equal, else 0
   unsigned int uniform_slot_groups;   // escape-patch workgroups of every payload, likewise
+  unsigned int uniform_blocks;        // blocks per plane of every payload when uniform_tiles
   // Escape directory of the launch's tiles (Top-16 tile kernels only; null when
   // absent): per 1024-word wave chunk of tile t a record dir_rec[4 * (4t + wave)
   // .. + 4) = {tile-relative slot of the chunk's first escape | chunk escapes << 16,
@@ -268,21 +269,40 @@ struct PlaneTile {
   unsigned int payload_index;  // index of the payload within the launch
 };
 
+// With equal payloads whose block tables lie back to back, the payload's tile and
+// block-table offsets follow from its index, so the block-id load that gates a
+// wave's source address does not wait for the payload descriptor.
 template <int kShift>
 __device__ __forceinline__ PlaneTile plane_tile(const LaunchArgs& a, unsigned int tile) {
   constexpr unsigned int kWords = 1u << kShift;
+  const unsigned int ut = a.uniform_tiles, ub = a.uniform_blocks;
+  const unsigned int bw = (unsigned int)a.block_words;
+  const long long* const ids = a.ids;
+  unsigned char* const buf = a.buf;
   PlaneTile t;
-  t.payload_index = find_payload(a, tile);
-  const PayloadDesc d = a.p[t.payload_index];
-  const unsigned int plane_words = d.block_count * (unsigned int)a.block_words;
+  unsigned int block_count, tile_begin;
+  unsigned long long ids_offset;
+  if (ut != 0 && ub != 0) {
+    t.payload_index = tile / ut;
+    block_count = ub;
+    tile_begin = t.payload_index * ut;
+    ids_offset = (unsigned long long)t.payload_index * ub;
+  } else {
+    t.payload_index = find_payload(a, tile);
+    const PayloadDesc d = a.p[t.payload_index];
+    block_count = d.block_count;
+    tile_begin = d.tile_begin;
+    ids_offset = d.ids_offset;
+  }
+  const unsigned int plane_words = block_count * bw;
   const unsigned int tpp = (plane_words + kWords - 1) >> kShift;
-  t.local_tile = tile - d.tile_begin;
+  t.local_tile = tile - tile_begin;
   t.plane = t.local_tile >= tpp ? 1u : 0u;
   t.in_plane0 = (t.local_tile - t.plane * tpp) << kShift;
   t.words = min(kWords, plane_words - t.in_plane0);
   t.n = 2ull * plane_words;
-  t.payload = a.buf + d.buf_offset;
-  t.ids = a.ids + d.ids_offset;
+  t.payload = buf + a.p[t.payload_index].buf_offset;
+  t.ids = ids + ids_offset;
   t.payload_tiles = 2 * tpp;
   return t;
 }

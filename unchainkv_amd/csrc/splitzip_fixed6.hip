@@ -526,6 +526,13 @@ unsigned int fill_batch(LaunchArgs& a, const unsigned long long* block_offsets,
   a.tiles_per_plane_mode = 1;
   a.tile_shift = kTileShift;
   a.uniform_tiles = uniform_size ? tiles / count : 0;
+  // equal payloads whose block tables lie back to back from the start: block-table
+  // offsets follow from the payload index (see plane_tile)
+  const unsigned long long nblk0 = block_offsets[first + 1] - block_offsets[first];
+  bool packed = uniform_size && block_offsets[first] == 0;
+  for (unsigned int k = 0; k < count && packed; ++k)
+    packed = block_offsets[first + k] == k * nblk0;
+  a.uniform_blocks = packed ? (unsigned int)nblk0 : 0;
   return tiles;
 }
 

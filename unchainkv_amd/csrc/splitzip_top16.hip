@@ -841,15 +841,34 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   const unsigned int tid = threadIdx.x;
   const unsigned int r = blockIdx.x / kFinGroups;
   const unsigned int grp = blockIdx.x % kFinGroups;
+  // Every kernel argument of the common path is read here, before any branch on
+  // one of them: the scalar loads then go out together instead of as a chain of
+  // dependent round trips (a cold constant cache makes each one an L2 access).
   const PayloadDesc d = a.p[r];
-  const unsigned long long n = payload_words(a, d);
+  const unsigned long long linear = a.linear_words;
+  const unsigned long long bw = a.block_words;
+  const unsigned int per_plane = a.tiles_per_plane_mode;
+  const unsigned int shift = a.tile_shift;
+  const unsigned int total_tiles = a.total_tiles;
+  unsigned char* const buf = a.buf;
+  unsigned int* const ws = a.workspace;
+  uint32_t* const dir_base = a.dir_base;
+  // (the compiler would otherwise sink each load to its first use, behind branches)
+  asm volatile("" ::"s"(d.buf_offset), "s"(d.block_count), "s"(d.tile_begin), "s"(linear),
+               "s"(bw), "s"(per_plane), "s"(shift), "s"(total_tiles), "s"(buf), "s"(ws),
+               "s"(dir_base));
+  asm volatile("" ::"s"(a.kv), "s"(a.ids), "s"(a.tables), "s"(a.plane_stride),
+               "s"(a.block_stride), "s"(a.block_start), "s"(d.ids_offset));
+  const unsigned long long n = linear ? linear : 2ull * d.block_count * bw;
   const unsigned long long cap = escape_capacity(n);
-  const unsigned int tiles = payload_tiles(a, n);
-  unsigned char* payload = a.buf + d.buf_offset;
+  const unsigned long long tile_words = 1ull << shift;
+  const unsigned int tiles =
+      per_plane ? 2u * (unsigned int)(((n >> 1) + tile_words - 1) >> shift)
+                : (unsigned int)((n + tile_words - 1) >> shift);
+  unsigned char* payload = buf + d.buf_offset;
   unsigned char* entries = payload + 5 + n + (n + 1) / 2;
-  const unsigned int* counts = a.workspace + d.tile_begin;
-  const unsigned int* staged =
-      a.workspace + a.total_tiles + (unsigned long long)d.tile_begin * kStageSlots;
+  const unsigned int* counts = ws + d.tile_begin;
+  const unsigned int* staged = ws + total_tiles + (unsigned long long)d.tile_begin * kStageSlots;
   if (tid == 0) s_over_count = 0;  // ordered by the barriers of the first scan
 
   unsigned long long running = 0;  // escapes in earlier chunks
@@ -864,15 +883,17 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
     unsigned int sum = 0;
 #pragma unroll
     for (int k = 0; k < kFinPerThread; ++k) {
+      // loads without branches: indices past the chunk read its last count
       const unsigned int t = tid * kFinPerThread + k;
-      mine[k] = t < m ? counts[chunk0 + t] : 0;
+      const unsigned int v = counts[chunk0 + min(t, m - 1)];
+      mine[k] = t < m ? v : 0;
       sum += mine[k];
     }
     const unsigned int own = tid * kFinPerThread + grp;  // this thread's tile of the group
-    const unsigned int* st = staged + (unsigned long long)(chunk0 + own) * kStageSlots;
+    const unsigned int* st = staged + (unsigned long long)(chunk0 + min(own, m - 1)) * kStageSlots;
     unsigned int pre[kFinPreload];
 #pragma unroll
-    for (int q = 0; q < kFinPreload; ++q) pre[q] = own < m ? st[q] : 0;
+    for (int q = 0; q < kFinPreload; ++q) pre[q] = st[q];
     unsigned int chunk_total;
     unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
 
@@ -884,8 +905,8 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       if ((unsigned int)k == grp) c = mine[k];
     }
     const unsigned long long base = running + prefix;
-    if (a.dir_base && own < m)
-      a.dir_base[d.tile_begin + chunk0 + own] = (unsigned int)min(base, 0xFFFFFFFFull);
+    if (dir_base && own < m)
+      dir_base[d.tile_begin + chunk0 + own] = (unsigned int)min(base, 0xFFFFFFFFull);
     if (c != 0 && base < cap) {
       if (c > (unsigned int)kStageSlots) {
         const unsigned int q = atomicAdd(&s_over_count, 1u);
@@ -1376,6 +1397,13 @@ unsigned int fill_descs(LaunchArgs& a, const PagedGeometry& pg,
   // every payload has the same tile count: the kernels find a tile's payload by
   // one division instead of a search of the descriptors
   a.uniform_tiles = uniform ? tiles / count : 0;
+  // ... and its block-table offset by one multiplication, when the block tables
+  // are laid out back to back (as the host's block_offsets are)
+  const unsigned long long nblk0 = block_offsets[first + 1] - block_offsets[first];
+  bool packed = uniform;
+  for (unsigned int k = 0; k < count && packed; ++k)
+    packed = block_offsets[first + k] == block_offsets[first] + k * nblk0;
+  a.uniform_blocks = packed && block_offsets[first] == 0 ? (unsigned int)nblk0 : 0;
   return tiles;
 }
 
