@@ -49,6 +49,12 @@ METRIC = "codec encode/decode GB/s of raw bf16 KV (% HBM peak) + compression rat
 WORKLOADS = ["llama3-8b-paged", "llama32-1b-contiguous", "llama3-8b-outliers",
              "llama3-70b-tp8-mixed", "llama3-8b-decode-attention"]
 ATTN_BATCH, ATTN_CONTEXT, ATTN_OUTLIERS = 32, 8192, 0.001
+# the benchmark's configurations by index, and the timed steps of the configurations
+# that ride along with the headline one
+CONFIG_OF = {"llama32-1b-contiguous": "config0", "llama3-8b-paged": "config1",
+             "llama3-8b-outliers": "config2", "llama3-70b-tp8-mixed": "config3",
+             "llama3-8b-decode-attention": "config4"}
+SUB_STEPS = 10
 
 
 def parse_args():
@@ -60,6 +66,9 @@ def parse_args():
                    help="after the warmup steps, keep stepping (untimed) until this much "
                         "wall time has passed since the first warmup step")
     p.add_argument("--workload", default="llama3-8b-paged", choices=WORKLOADS)
+    p.add_argument("--configs", default="all", choices=["all", "none"],
+                   help="also run every other workload (shorter) and report it under "
+                        "\"configs\" of the line")
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--cpu-baseline-seconds", type=float, default=10.0,
                    help="codec time of the CPU baseline sample (repeated passes)")
@@ -257,8 +266,8 @@ def plan_fallbacks(torch, sz, w):
     cache = {}
     for layer in range(w["layers"]):
         encode_top16(sz, w, layer)
-        host = w["payloads"][layer].cpu()
-        over = tuple(r for r, off in enumerate(send.out_offsets) if int(host[off]) == 255)
+        head = payload_headers(torch, w, layer)
+        over = tuple(r for r, h in enumerate(head) if h[0] == 255)
         keep = tuple(r for r in range(send.payload_count) if r not in over)
         entry = {"over": over, "keep": keep}
         if over:
@@ -327,16 +336,25 @@ def final_payload_bytes(w, layer) -> int:
     return sum(send.encoded_bytes[r] for r in plan["keep"]) + sum(plan.get("sizes", []))
 
 
+def payload_headers(torch, w, layer):
+    """The 5-byte headers of a layer's Top-16 payloads (read without copying the
+    payloads to the host)."""
+    send = w["send"]
+    key = "header_index"
+    if key not in w:
+        w[key] = torch.tensor([o + k for o in send.out_offsets for k in range(5)],
+                              dtype=torch.int64, device=w["device"])
+    head = w["payloads"][layer].index_select(0, w[key]).cpu().view(-1, 5).tolist()
+    return [(h[0], h[1] | (h[2] << 8) | (h[3] << 16) | (h[4] << 24)) for h in head]
+
+
 def escape_counts(torch, w):
     """Escape entries per layer (from the Top-16 payload headers) and overflowed payloads."""
-    send = w["send"]
     total, overflow = 0, 0
     for layer in range(w["layers"]):
-        host = w["payloads"][layer].cpu()
-        for off in send.out_offsets:
-            head = bytes(host[off:off + 5].tolist())
-            total += int.from_bytes(head[1:5], "little")
-            overflow += head[0] == 255
+        for mode, count in payload_headers(torch, w, layer):
+            total += count
+            overflow += mode == 255
     return total, overflow
 
 
@@ -550,6 +568,266 @@ def cpu_baseline(torch, w, layers: int, seconds: float = 10.0):
     }
 
 
+def cpu_baseline_torch(torch, w, seconds: float = 10.0):
+    """``ref-cpu-torch``: the oracle's torch-CPU restatement in the reference's
+    op-by-op style (index_select gather, bitwise split, table indexing, strided
+    nibble packing, nonzero for escapes; decode by strided unpacking, table
+    indexing and index_copy_) on this host's torch threads, over the requests of
+    layer 0 in turn until about `seconds` have passed; its payloads are compared
+    with the GPU's."""
+    import oracle
+    from oracle import torch_codec
+
+    send, recv = w["send"], w["recv"]
+    kv = w["kv"][0].view(torch.int16).cpu()
+    tables = torch.from_numpy(oracle.top16_tables(w["books"][0]).copy())
+    target = torch.zeros_like(kv)
+    gpu = w["payloads"][0].cpu().numpy()
+    raw = 0
+    t_enc = t_dec = 0.0
+    done = 0
+    while done == 0 or t_enc + t_dec < seconds:
+        r = done % send.payload_count
+        t0 = time.perf_counter()
+        payload = torch_codec.encode_paged(kv, [send.block_tables[r]], tables, torch)
+        t1 = time.perf_counter()
+        torch_codec.decode_paged(payload, target, [recv.block_tables[r]], tables, torch)
+        t2 = time.perf_counter()
+        t_enc += t1 - t0
+        t_dec += t2 - t1
+        raw += send.raw_bytes[r]
+        if done < send.payload_count:
+            off, size = send.out_offsets[r], send.encoded_bytes[r]
+            if r in w["plan"][0]["keep"] and bytes(payload[0].numpy()) != bytes(gpu[off:off + size]):
+                raise RuntimeError(f"request {r}: torch-CPU payload differs from the GPU's")
+        done += 1
+    return {
+        "value": round(2 * raw / (t_enc + t_dec) / 1e9, 3),
+        "unit": "GB/s raw bf16 (encode+decode round trip)",
+        "threads": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{done} requests of layer 0 ({raw / 2**30:.2f} GiB raw bf16), "
+                  f"{t_enc + t_dec:.1f} s",
+        "encode_GBps": round(raw / t_enc / 1e9, 3),
+        "decode_GBps": round(raw / t_dec / 1e9, 3),
+    }
+
+
+def python_decoder_rate(w, words: int = 1 << 20):
+    """The reference's per-element Python Top-16 decoder (restated in the oracle) on
+    a 1 M-word payload: the first blocks of request 0 of layer 0. Reported per
+    word, not extrapolated."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    send, shape = w["send"], w["shape"]
+    blocks = max(1, words // (2 * shape.block_words))
+    ids = send.block_tables[0][:blocks]
+    kv = w["kv"][0].view(torch.int16).cpu().numpy().view(np.uint16).reshape(2, w["pool"], -1)
+    sample = kv[:, ids].reshape(-1)
+    tab = oracle.top16_tables(w["books"][0])
+    payload = oracle.top16_encode(sample, tab)
+    if payload[0] != 5:
+        return {"skipped": "the sample overflowed its escape capacity"}
+    t0 = time.perf_counter()
+    raw = oracle.decode_top16_payload_py(bytes(payload), 2 * sample.size, w["books"][0])
+    elapsed = time.perf_counter() - t0
+    if raw != sample.tobytes():
+        raise RuntimeError("Python decoder result differs")
+    return {"words": int(sample.size), "seconds": round(elapsed, 3),
+            "ns_per_word": round(elapsed / sample.size * 1e9, 1),
+            "raw_GBps": round(2 * sample.size / elapsed / 1e9, 6), "threads": 1}
+
+
+def time_dropin(torch, sz, w, reps: int = 3):
+    """The reference-ABI per-request path an unchanged reference connector takes:
+    index_select gather of a request's blocks into a packed copy, encode_top16 into
+    a raw-sized byte buffer (payload at its start, so the body section is 5 bytes
+    off 16-byte alignment), and decode_top16 of each payload into the receiver's
+    blocks; for the 8 requests of layer 0, checked against the batched payloads.
+    Also the encode at the ABI's minimum capacity (align4(E) + 8 bytes)."""
+    send, recv = w["send"], w["recv"]
+    kv, books = w["kv"][0], w["books"][0]
+    if w["plan"][0]["over"]:
+        return {"skipped": "layer 0 has overflowed payloads"}
+    stream = torch.cuda.current_stream(w["device"])
+    ids = [torch.tensor(t, dtype=torch.int64, device=w["device"]) for t in send.block_tables]
+    outs = [torch.empty(n, dtype=torch.uint8, device=w["device"]) for n in send.raw_bytes]
+    target = torch.zeros_like(kv)
+
+    def encode_all(gather: bool, sources=None):
+        for r in range(send.payload_count):
+            src = kv.index_select(1, ids[r]) if gather else sources[r]
+            if sz.encode_top16(src, outs[r], -1, codebooks=books) != send.encoded_bytes[r]:
+                raise RuntimeError("drop-in encode declined")
+
+    def decode_all():
+        for r in range(send.payload_count):
+            got = sz.decode_top16(outs[r][:send.encoded_bytes[r]], target, recv.block_tables[r],
+                                  send.raw_bytes[r], -1, codebooks=books)
+            if got != send.raw_bytes[r]:
+                raise RuntimeError("drop-in decode declined")
+
+    sources = [kv.index_select(1, i) for i in ids]
+
+    def timed(fn, *a):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        best = []
+        for _ in range(reps):
+            hold_queue(torch)
+            e0.record(stream)
+            fn(*a)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            best.append(e0.elapsed_time(e1))
+        return statistics.median(best)
+
+    encode_all(False, sources)
+    decode_all()
+    torch.cuda.synchronize()
+    for r in range(send.payload_count):
+        batched = w["payloads"][0][send.out_offsets[r]:send.out_offsets[r] + send.encoded_bytes[r]]
+        if not torch.equal(outs[r][:send.encoded_bytes[r]], batched):
+            raise RuntimeError("drop-in payload differs from the batched one")
+    src_ids = torch.cat(ids)
+    dst_ids = torch.tensor([b for t in recv.block_tables for b in t], device=w["device"])
+    if not torch.equal(kv.view(torch.int16).index_select(1, src_ids),
+                       target.view(torch.int16).index_select(1, dst_ids)):
+        raise RuntimeError("drop-in round trip differs")
+    raw = send.total_raw_bytes
+    ms_gather_enc = timed(encode_all, True)
+    ms_enc = timed(encode_all, False, sources)
+    ms_dec = timed(decode_all)
+    # minimum capacity: no room for the parallel tiles' workspace past the payload
+    r0 = 0
+    e = send.encoded_bytes[r0]
+    tight = torch.empty(((e + 3) & ~3) + 8, dtype=torch.uint8, device=w["device"])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    sz.encode_top16(sources[r0], tight, -1, codebooks=books)
+    hold_queue(torch)
+    e0.record(stream)
+    sz.encode_top16(sources[r0], tight, -1, codebooks=books)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_tight = e0.elapsed_time(e1)
+    if not torch.equal(tight[:e], outs[r0][:e]):
+        raise RuntimeError("minimum-capacity payload differs")
+
+    def rate(ms, nbytes):
+        return round(nbytes / (ms * 1e-3) / 1e9, 2)
+
+    return {
+        "requests": send.payload_count,
+        "gather_encode_ms_per_request": round(ms_gather_enc / send.payload_count, 5),
+        "gather_encode_raw_GBps": rate(ms_gather_enc, raw),
+        "encode_ms_per_request": round(ms_enc / send.payload_count, 5),
+        "encode_raw_GBps": rate(ms_enc, raw),
+        "decode_ms_per_request": round(ms_dec / send.payload_count, 5),
+        "decode_raw_GBps": rate(ms_dec, raw),
+        "min_capacity_encode_ms": round(ms_tight, 5),
+        "min_capacity_encode_raw_GBps": rate(ms_tight, send.raw_bytes[r0]),
+        "layout": "payload at the start of a raw-sized uint8 buffer (body 5 bytes past "
+                  "16-byte alignment); gather by index_select as the reference connector",
+    }
+
+
+def time_overlap(torch, sz, w, repeats: int = 7):
+    """Encode + device-to-host copy of a layer's payloads against the model's
+    attention, in the modes of the reference's scripts/bench_codec_attention.py:
+    attention alone, encode alone, copy alone, fully serial (the copy on the
+    forward stream: attention waits for it), serial pipeline (encode on the forward
+    stream, copy on a copy stream beside the attention: what the connector does)
+    and concurrent pipeline (encode and copy on side streams). The attention is
+    causal prefill over the layer's 8 x 4096 tokens (32 query heads, 8 KV heads,
+    flash kernel); all streams at the default priority."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    send, shape = w["send"], w["shape"]
+    device = w["device"]
+    g = torch.Generator(device=device)
+    g.manual_seed(5)
+    reqs, tokens = send.payload_count, len(send.block_tables[0]) * shape.block_size
+    q = torch.randn((reqs, 4 * shape.kv_heads, tokens, shape.head_dim), generator=g,
+                    device=device).to(torch.bfloat16)
+    k = torch.randn((reqs, shape.kv_heads, tokens, shape.head_dim), generator=g,
+                    device=device).to(torch.bfloat16)
+    v = torch.randn_like(k)
+
+    def attention():
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True,
+                                                                    enable_gqa=True)
+    try:
+        attention()
+        torch.cuda.synchronize()
+    except Exception as exc:  # noqa: BLE001 - no flash kernel for this build: report it
+        return {"skipped": f"flash attention unavailable: {exc}"[:200]}
+    main = torch.cuda.current_stream(device)
+    codec = torch.cuda.Stream(device=device)
+    copy = torch.cuda.Stream(device=device)
+    payloads = w["payloads"][0]
+    host = torch.empty(payloads.numel(), dtype=torch.uint8, pin_memory=True)
+
+    def encode():
+        encode_top16(sz, w, 0)
+
+    def run(mode):
+        ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+        start = ev()
+        start.record(main)
+        ends = {}
+        enc_end = None
+        if mode in ("encode_only", "fully_serial", "serial_pipeline"):
+            encode()
+            enc_end = ev()
+            enc_end.record(main)
+            ends["encode"] = enc_end
+        elif mode == "concurrent_pipeline":
+            codec.wait_event(start)
+            with torch.cuda.stream(codec):
+                encode()
+                enc_end = ev()
+                enc_end.record(codec)
+            ends["encode"] = enc_end
+        if mode in ("d2h_only", "fully_serial", "serial_pipeline", "concurrent_pipeline"):
+            stream = main if mode == "fully_serial" else copy
+            stream.wait_event(enc_end if enc_end is not None else start)
+            with torch.cuda.stream(stream):
+                host.copy_(payloads, non_blocking=True)
+                end = ev()
+                end.record(stream)
+            ends["d2h"] = end
+        if mode in ("attention_only", "fully_serial", "serial_pipeline", "concurrent_pipeline"):
+            attention()
+            end = ev()
+            end.record(main)
+            ends["attention"] = end
+        for e in ends.values():
+            e.synchronize()
+        return max(start.elapsed_time(e) for e in ends.values())
+
+    modes = ("attention_only", "encode_only", "d2h_only", "fully_serial", "serial_pipeline",
+             "concurrent_pipeline")
+    for m in modes:
+        run(m)
+    samples = {m: [] for m in modes}
+    for rep in range(repeats):
+        for m in modes[rep % len(modes):] + modes[:rep % len(modes)]:
+            samples[m].append(run(m))
+    torch.cuda.synchronize()
+    if not torch.equal(host, payloads.cpu()):
+        raise RuntimeError("staged payload bytes differ")
+    out = {m: round(statistics.median(v), 4) for m, v in samples.items()}
+    hidden = out["fully_serial"] - out["serial_pipeline"]
+    return {"wall_ms_p50": out, "payload_bytes": int(send.total_encoded_bytes),
+            "copy_hidden_ms": round(hidden, 4),
+            "attention": f"causal flash SDPA, {reqs} x {tokens} tokens, "
+                         f"{4 * shape.kv_heads} q heads / {shape.kv_heads} kv heads x "
+                         f"{shape.head_dim}, bf16"}
+
+
 # ---------------------------------------------------------------------------
 # fused decode attention workload
 
@@ -697,7 +975,8 @@ def cpu_attention_baseline(torch, w, ref_layer_out):
     }
 
 
-def run_attention(args, torch, sz, workloads) -> int:
+def run_attention(args, torch, sz, workloads, headline: bool = True):
+    """Fused decode-attention workload; the JSON object of its run."""
     w = build_attention(torch, sz, workloads, args.seed)
     layers, batch, shape = w["layers"], w["batch"], w["shape"]
     stream = torch.cuda.current_stream(w["device"])
@@ -712,23 +991,23 @@ def run_attention(args, torch, sz, workloads) -> int:
         torch.cuda.synchronize()
         verify_attention(torch, sz, w, 0)
         calibration_copy(torch, w["device"])
-        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload,
-                          "calibration_copy_bytes": CALIBRATION_BYTES}))
-        return 0
+        return {"profile_steps": args.profile_steps, "workload": "llama3-8b-decode-attention",
+                "calibration_copy_bytes": CALIBRATION_BYTES}
 
-    warm_up(torch, step, args.warmup, args.settle_seconds)
+    steps = args.steps if headline else SUB_STEPS
+    warm_up(torch, step, args.warmup if headline else 2, args.settle_seconds)
     worst = max(verify_attention(torch, sz, w, layer) for layer in (0, layers - 1))
 
     t0 = time.perf_counter()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = start.elapsed_time(end) / args.steps
+    ms_per_step = start.elapsed_time(end) / steps
     call_ms = ms_per_step / layers
 
     # the decode half of decode-then-attend, for comparison: the codec's decoder
@@ -764,13 +1043,13 @@ def run_attention(args, torch, sz, workloads) -> int:
     achieved = b_call / (call_ms * 1e-3) / 1e9
     raw_layer = batch.total_raw_bytes
     flops = 2 * 2 * ATTN_BATCH * q_heads * ATTN_CONTEXT * shape.head_dim
-    traffic, traffic_source = measured_traffic(args.workload, "attention")
+    traffic, traffic_source = measured_traffic("llama3-8b-decode-attention", "attention")
     result = {
         "metric": METRIC,
         "value": round(raw_layer * layers / (ms_per_step * 1e-3) / 1e9, 2),
         "unit": "GB/s raw bf16 KV attended (fused Top-16 decode + decode attention)",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -780,7 +1059,7 @@ def run_attention(args, torch, sz, workloads) -> int:
         "data": (f"synthetic seeded (seed {args.seed}); K=N(0,1)*logU[0.1,10] per channel, "
                  f"V=N(0,0.5), {ATTN_OUTLIERS:.1%} outliers +-logU[1e2,1e4]; Q=N(0,1) bf16"),
         "config": {
-            "workload": args.workload,
+            "workload": "llama3-8b-decode-attention",
             "layers": layers,
             "batch": ATTN_BATCH,
             "context": ATTN_CONTEXT,
@@ -810,36 +1089,23 @@ def run_attention(args, torch, sz, workloads) -> int:
             "ms_per_call": round(call_ms, 5),
         },
         "wall_s_timed": round(wall, 3),
+        "verified": True,
     }
-    if not args.no_cpu_baseline:
+    if headline and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_attention_baseline(torch, w, w["out"][0])
-    print(json.dumps(result))
-    return 0
+    return result
 
 
 # ---------------------------------------------------------------------------
 # main
 
-def main() -> int:
-    args = parse_args()
-    if args.pmc_summary:
-        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
-        return 0
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(per-request and per-layer payloads shard with no exchange)"}))
-        return 2
-    import torch
-
+def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
+    """One codec workload (encode + decode of every layer per step); the JSON object
+    of its run. The headline run adds the histogram, writeback, graph replay,
+    drop-in, overlap and CPU-baseline legs."""
     from unchainkv_amd import codec_format
-    from unchainkv_amd import splitzip_cuda as sz
-    from unchainkv_amd import workloads
 
-    if not sz.available():
-        raise RuntimeError(f"HIP codec library not loaded: {sz.load_error()}")
-    if args.workload == "llama3-8b-decode-attention":
-        return run_attention(args, torch, sz, workloads)
-    w = build_workload(torch, sz, workloads, args.workload, args.seed)
+    w = build_workload(torch, sz, workloads, name, args.seed)
     layers = w["layers"]
     stream = torch.cuda.current_stream(w["device"])
 
@@ -862,11 +1128,11 @@ def main() -> int:
         verify(torch, w)
         time_writeback(torch, sz, w, reps=1)
         calibration_copy(torch, w["device"])
-        print(json.dumps({"profile_steps": args.profile_steps, "workload": args.workload,
-                          "calibration_copy_bytes": CALIBRATION_BYTES}))
-        return 0
+        return {"profile_steps": args.profile_steps, "workload": name,
+                "calibration_copy_bytes": CALIBRATION_BYTES}
 
-    warm_up(torch, step, args.warmup, args.settle_seconds)
+    steps = args.steps if headline else SUB_STEPS
+    warm_up(torch, step, args.warmup if headline else 2, args.settle_seconds)
     verify(torch, w)
 
     # timed region: exactly `steps` steps between two synchronisations
@@ -874,12 +1140,12 @@ def main() -> int:
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = start.elapsed_time(end) / args.steps
+    ms_per_step = start.elapsed_time(end) / steps
 
     # per-call durations of encode and decode on the codec stream: HIP events
     # around each direction's back-to-back layer calls, divided by the layer count;
@@ -887,7 +1153,7 @@ def main() -> int:
     # lands in one repetition only)
     events = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     enc_ms, dec_ms = [], []
-    for _ in range(max(5, min(args.steps, 11))):
+    for _ in range(max(5, min(steps, 11))):
         hold_queue(torch)
         step(events)
         torch.cuda.synchronize()
@@ -896,10 +1162,6 @@ def main() -> int:
     verify(torch, w)
     enc_call = statistics.median(enc_ms)
     dec_call = statistics.median(dec_ms)
-    hist = time_histogram(torch, sz, w)
-    writeback = time_writeback(torch, sz, w)
-    graph = time_graph_replay(torch, step, w, args.steps, raw_bytes=w["send"].total_raw_bytes
-                              * layers)
 
     send = w["send"]
     raw_layer = send.total_raw_bytes
@@ -931,14 +1193,14 @@ def main() -> int:
         kernels = {"encode": "top16 encode + palette_presence/reduce/encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
-    traffic, traffic_source = (None, None) if overflowed else measured_traffic(args.workload,
+    traffic, traffic_source = (None, None) if overflowed else measured_traffic(name,
                                                                                  dominant[0])
     result = {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s raw bf16 through encode+decode",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -949,7 +1211,7 @@ def main() -> int:
                  f"V=N(0,0.5)" + (f", {w['outliers']:.0%} outliers +-logU[1e2,1e4]"
                                   if w["outliers"] else "")),
         "config": {
-            "workload": args.workload,
+            "workload": name,
             "layers": layers,
             "kv_heads": w["shape"].kv_heads,
             "head_dim": w["shape"].head_dim,
@@ -971,9 +1233,6 @@ def main() -> int:
             "hbm_frac": round(dec_hbm / HBM_PEAK_GBPS, 4),
             "ms_per_layer_call": round(dec_call, 5),
         },
-        "graph_replay": graph,
-        "exponent_histogram": hist,
-        "codec_writeback": writeback,
         "compression_ratio": round(raw_layer / final, 5),
         "escapes_per_layer": round(escapes / layers, 1),
         "overflowed_payloads": overflowed,
@@ -990,10 +1249,82 @@ def main() -> int:
             "ms_per_call": round(dominant[1], 5),
         },
         "wall_s_timed": round(wall, 3),
+        "verified": True,
     }
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch, w, args.cpu_baseline_layers,
-                                              args.cpu_baseline_seconds)
+    if headline:
+        result["graph_replay"] = time_graph_replay(torch, step, w, steps,
+                                                   raw_bytes=raw_layer * layers)
+        result["exponent_histogram"] = time_histogram(torch, sz, w)
+        result["codec_writeback"] = time_writeback(torch, sz, w)
+        result["dropin_per_request"] = time_dropin(torch, sz, w)
+        result["staging_overlap"] = time_overlap(torch, sz, w)
+        if not args.no_cpu_baseline:
+            base = cpu_baseline(torch, w, args.cpu_baseline_layers, args.cpu_baseline_seconds)
+            base["legs"] = {"ref-cpu-c": {k: base[k] for k in ("value", "cores", "sample")},
+                            "ref-cpu-torch": cpu_baseline_torch(torch, w,
+                                                                args.cpu_baseline_seconds),
+                            "python_decoder": python_decoder_rate(w)}
+            result["cpu_baseline"] = base
+    return result
+
+
+
+
+def _sub_summary(result: dict) -> dict:
+    """The fields of a non-headline configuration carried in the headline line."""
+    keep = ("metric", "value", "unit", "ms_per_step", "steps", "config", "encode", "decode",
+            "compression_ratio", "escapes_per_layer", "overflowed_payloads", "roofline",
+            "verified", "ms_per_layer_call", "escape_fraction",
+            "max_rel_error_vs_decode_then_attend", "decode_only_ms_per_layer", "mfma_TFLOPs",
+            "dtype", "data")
+    return {k: result[k] for k in keep if k in result}
+
+
+def _free(torch) -> None:
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def main() -> int:
+    args = parse_args()
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return 0
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(per-request and per-layer payloads shard with no exchange)"}))
+        return 2
+    import torch
+
+    from unchainkv_amd import splitzip_cuda as sz
+    from unchainkv_amd import workloads
+
+    if not sz.available():
+        raise RuntimeError(f"HIP codec library not loaded: {sz.load_error()}")
+
+    def run(name, headline):
+        if name == "llama3-8b-decode-attention":
+            return run_attention(args, torch, sz, workloads, headline)
+        return run_codec(args, torch, sz, workloads, name, headline)
+
+    result = run(args.workload, True)
+    if not args.profile_steps and args.configs == "all":
+        # every other configuration of the benchmark, shorter: its per-call rates,
+        # roofline fraction, ratio and verification
+        _free(torch)
+        subs = {}
+        for name in WORKLOADS:
+            if name == args.workload:
+                continue
+            t0 = time.perf_counter()
+            sub = _sub_summary(run(name, False))
+            sub["run_s"] = round(time.perf_counter() - t0, 1)
+            subs[CONFIG_OF[name]] = dict(workload=name, **sub)
+            _free(torch)
+        result["configs"] = subs
     print(json.dumps(result))
     return 0
 

@@ -249,3 +249,58 @@ def test_layer_travels_in_compressed_native_frames(sz, codebooks):
                     ("r2h", tables[2]), ("r1raw", tables[1])):
         assert got[name] == (len(t), 4 * BW * len(t)), name
         assert np.array_equal(dst[:, recv[name]], src[:, t]), name
+
+
+# ---------------------------------------------------------------------------
+# payload staging: copy stream and pinned pool (vllm_connector.py:3406-3458)
+
+def test_payload_copy_runs_beside_the_forward_stream(sz, codebooks):
+    """A kernel queued on the forward stream right after save_kv_layer finishes
+    while the layer's device-to-host copy is still running: the copy is on its own
+    stream. The payloads still arrive whole."""
+    say("connector staging overlap")
+    books = codebooks[3 * 32:4 * 32]
+    rng = np.random.default_rng(12)
+    pool = 1100
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.0005), pool)
+    tables = disjoint_tables(rng, pool, [256, 256, 256, 256])  # ~50 MB of payloads
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False))
+    torch.cuda.synchronize()
+    pending = codec.save_kv_layer(3, kv, tables)
+    marker = torch.cuda.Event()
+    marker.record(torch.cuda.current_stream())   # forward work after the save hook
+    marker.synchronize()
+    copies = [event for _, event, _, _ in pending.groups]
+    assert copies and not all(event.query() for event in copies)
+    payloads = codec.ready(pending)
+    tab = oracle.top16_tables(books)
+    src = u16(kv).reshape(2, pool, BW)
+    for t, p in zip(tables[:2], payloads[:2]):
+        assert bytes(p.view) == bytes(oracle.top16_encode(src[:, t].reshape(-1), tab))
+    codec.release(pending)
+
+
+def test_pinned_pool_reuse_and_cap(sz, codebooks):
+    """Released buffers are reused for the next layer (no new pinned allocation);
+    with a one-buffer cap a second layer in flight falls back to a fresh pinned
+    buffer (trace host_mirror_full); every round trip stays exact."""
+    say("connector pinned pool")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(13)
+    pool = 80
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.001), pool)
+    tables = disjoint_tables(rng, pool, [16, 20])
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, host_mirror_layers=1), trace=trace)
+    first = codec.save_kv_layer(5, kv, tables)
+    second = codec.save_kv_layer(5, kv, tables)          # the cap's one buffer is busy
+    assert codec.pinned.allocations == 1
+    assert "host_mirror_full" in trace.names()
+    a, b = codec.ready(first), codec.ready(second)
+    assert [bytes(p.view) for p in a] == [bytes(p.view) for p in b]
+    codec.release(first)
+    codec.release(second)
+    torch.cuda.synchronize()
+    payloads = roundtrip(codec, 5, kv, tables, pool)      # reuses the released buffer
+    assert codec.pinned.allocations == 1
+    assert [bytes(p.view) for p in payloads] == [bytes(p.view) for p in a]

@@ -11,7 +11,9 @@ This module keeps that codec behaviour and its knobs, batched per layer:
   enabled, downgraded to fixed6 for a layer after it declines or overflows;
 * save (``save_kv_layer``): every request of the layer is encoded by one batched
   launch per codec (gathering the blocks in the kernel), then copied to pinned host
-  memory on the current stream;
+  memory from a reusable pool on a copy stream that waits for the forward stream
+  (:3406-3458), so later forward kernels do not wait for the copy; ``release``
+  returns a layer's pinned buffers once its payloads are sent;
 * codec writeback (``CodecConfig.writeback`` without ``preserve_source``,
   :3460-3563): a Top-16 payload whose request holds one contiguous run of blocks is
   moved into those blocks (K-plane run, then V-plane run) by one launch per layer
@@ -43,6 +45,7 @@ from dataclasses import dataclass, field
 
 from . import codec_format, frames
 from .backoff import Top16Backoff
+from .staging import CopyStreams, PinnedPool
 from .codebooks import summarize_symbol_counts
 from .trace import TraceWriter
 
@@ -71,6 +74,9 @@ class CodecConfig:
     # prefix caching or chunked prefill may reuse the sender's blocks: no overwrite
     # (the reference derives this from the vLLM config, vllm_connector.py:442-444)
     preserve_source: bool = False
+    # caps of the pinned staging pool (0: none), vllm_connector.py:480-486
+    host_mirror_layers: int = 0           # UNCHAIN_KV_HOST_MIRROR_LAYERS (buffers)
+    host_mirror_bytes: int = 0            # UNCHAIN_KV_HOST_MIRROR_BYTES
 
     @classmethod
     def from_env(cls, env=None) -> "CodecConfig":
@@ -83,6 +89,8 @@ class CodecConfig:
             top16_max_cooldown=max(1, _env_int(env, "UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN", 32)),
             native_decode=_env_int(env, "UNCHAIN_KV_SPLITZIP_NATIVE_DECODE", 1) > 0,
             writeback=_env_int(env, "UNCHAIN_KV_CODEC_WRITEBACK", int(top16)) > 0,
+            host_mirror_layers=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_LAYERS", 0)),
+            host_mirror_bytes=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_BYTES", 0)),
         )
 
 
@@ -138,6 +146,7 @@ class PendingLayer:
     block_words: int
     payloads: list
     groups: list = field(default_factory=list)  # (host tensor, event, device buffer, status)
+    slots: list = field(default_factory=list)   # pinned pool buffers behind the host tensors
     started: float = 0.0
 
 
@@ -161,6 +170,8 @@ class SplitzipLayerCodec:
         self._traced_bf16_exponents: set[tuple[str, int]] = set()
         self.codec_writeback = config.writeback and config.top16
         self.codec_writeback_overwrite = self.codec_writeback and not config.preserve_source
+        self.pinned = PinnedPool(config.host_mirror_bytes, config.host_mirror_layers)
+        self.copy_streams = CopyStreams()
 
     # ------------------------------------------------------------------
     # library
@@ -278,15 +289,51 @@ class SplitzipLayerCodec:
         got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind)
         return (out, offsets, sizes, batch) if got else None
 
-    @staticmethod
-    def _stage(pending: PendingLayer, device_buffer, torch) -> int:
-        """Asynchronous copy of a payload buffer into pinned host memory."""
-        host = torch.empty(device_buffer.numel(), dtype=torch.uint8, pin_memory=True)
-        host.copy_(device_buffer, non_blocking=True)
-        event = torch.cuda.Event()
-        event.record(torch.cuda.current_stream(device_buffer.device))
+    def _host_buffer(self, nbytes: int, torch):
+        """(pinned host tensor of nbytes, its pool buffer): from the pool, or a fresh
+        pinned tensor (buffer None) when the pool's caps leave none."""
+        slot = self.pinned.acquire(nbytes, torch)
+        if slot is None:
+            self.trace.event("host_mirror_full", bytes=nbytes)
+            return torch.empty(nbytes, dtype=torch.uint8, pin_memory=True), None
+        return slot.view(nbytes), slot
+
+    def _begin_copies(self, device, torch):
+        """The copy stream, after it has waited for everything queued so far on the
+        current (forward) stream: later forward kernels do not wait for the copies
+        (vllm_connector.py:3431-3444)."""
+        copy = self.copy_streams.get(device, torch)
+        copy.wait_stream(torch.cuda.current_stream(device))
+        return copy
+
+    def _stage(self, pending: PendingLayer, device_buffer, torch) -> int:
+        """Asynchronous copy of a payload buffer into pinned host memory, on the copy
+        stream."""
+        host, slot = self._host_buffer(device_buffer.numel(), torch)
+        copy = self._begin_copies(device_buffer.device, torch)
+        with torch.cuda.stream(copy):
+            host.copy_(device_buffer, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record(copy)
+        # the caching allocator must not hand the buffer out again before the copy
+        device_buffer.record_stream(copy)
+        self._keep_slot(pending, slot, event)
         pending.groups.append((host, event, device_buffer, None))
         return len(pending.groups) - 1
+
+    @staticmethod
+    def _keep_slot(pending: PendingLayer, slot, event) -> None:
+        # the pool reuses the buffer only after release() and the copy's end
+        if slot is not None:
+            slot.event = event
+            pending.slots.append(slot)
+
+    def release(self, pending: PendingLayer) -> None:
+        """Returns the layer's pinned buffers to the pool once its payloads have been
+        consumed (sent); their memory views must not be used afterwards."""
+        for slot in pending.slots:
+            self.pinned.release(slot)
+        pending.slots.clear()
 
     def _writeback_members(self, members: list, layer_index: int) -> list[int]:
         """Indices of the Top-16 members whose blocks are one contiguous run (the
@@ -327,27 +374,32 @@ class SplitzipLayerCodec:
             for i in picks:
                 self.trace.event("codec_writeback_skip", layer=layer, reason="alias")
             return False
-        host = torch.empty(out.numel(), dtype=torch.uint8, pin_memory=True)
+        host, slot = self._host_buffer(out.numel(), torch)
         status_host = torch.empty(len(picks), dtype=torch.uint8, pin_memory=True)
         flat = kv_layer.view(-1).view(torch.uint8)
         plane = 2 * kv_layer.stride(0)
         picked = set(picks)
-        for i, p in enumerate(members):
-            off, size = int(offsets[i]), int(sizes[i])
-            if i not in picked:
-                host[off:off + size].copy_(out[off:off + size], non_blocking=True)
-                continue
-            start, count = _contiguous_runs(p.block_ids)[0]
-            seg = 2 * count * pending.block_words
-            k = 2 * start * kv_layer.stride(1)
-            head = min(size, seg)
-            host[off:off + head].copy_(flat[k:k + head], non_blocking=True)
-            if size > seg:
-                host[off + seg:off + size].copy_(flat[plane + k:plane + k + size - seg],
-                                                 non_blocking=True)
-        status_host.copy_(status[:len(picks)], non_blocking=True)
-        event = torch.cuda.Event()
-        event.record(torch.cuda.current_stream(kv_layer.device))
+        copy = self._begin_copies(kv_layer.device, torch)
+        with torch.cuda.stream(copy):
+            for i, p in enumerate(members):
+                off, size = int(offsets[i]), int(sizes[i])
+                if i not in picked:
+                    host[off:off + size].copy_(out[off:off + size], non_blocking=True)
+                    continue
+                start, count = _contiguous_runs(p.block_ids)[0]
+                seg = 2 * count * pending.block_words
+                k = 2 * start * kv_layer.stride(1)
+                head = min(size, seg)
+                host[off:off + head].copy_(flat[k:k + head], non_blocking=True)
+                if size > seg:
+                    host[off + seg:off + size].copy_(flat[plane + k:plane + k + size - seg],
+                                                     non_blocking=True)
+            status_host.copy_(status[:len(picks)], non_blocking=True)
+            event = torch.cuda.Event()
+            event.record(copy)
+        out.record_stream(copy)
+        status.record_stream(copy)
+        self._keep_slot(pending, slot, event)
         # the codec buffer is released now unless an unmoved payload is still read from it
         keep = out if len(picks) < len(members) else None
         pending.groups.append((host, event, keep, status_host))
@@ -616,11 +668,16 @@ class SplitzipLayerCodec:
                 start = -(-(end + header[mode]) // 256) * 256 - header[mode]
                 layout.append((mode, member, start))
                 end = start + len(member[3])
-        host = torch.empty(max(end, 1), dtype=torch.uint8, pin_memory=True)
+        host, slot = self._host_buffer(max(end, 1), torch)
         host_view = memoryview(host.numpy())
         for mode, member, start in layout:
             host_view[start:start + len(member[3])] = member[3]
         device = host.to(kv_layer.device, non_blocking=True)
+        if slot is not None:
+            # back to the pool at once: reused after the host-to-device copy ends
+            slot.event = torch.cuda.Event()
+            slot.event.record(torch.cuda.current_stream(kv_layer.device))
+            self.pinned.release(slot)
         for mode, members in groups.items():
             starts = [start for m, _, start in layout if m == mode]
             batch = sz.PagedBatch([m[1] for m in members], block_words, kv_layer.device)

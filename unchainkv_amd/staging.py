@@ -1,0 +1,102 @@
+"""Pinned host staging for codec payloads: a reusable pool of pinned buffers and a
+device-to-host copy stream per GPU.
+
+Behaviour of the reference connector's pinned staging (`_stage_cpu`,
+src/unchain_kv/vllm_connector.py:3406-3458, pool `_acquire_pinned_stage_buffer`
+:3970-4040): payload copies leave the forward stream, run on a dedicated copy
+stream that first waits for the work queued so far, land in pinned buffers that
+are reused once released and their copy has finished, and the pool can be capped
+in buffers or bytes (UNCHAIN_KV_HOST_MIRROR_LAYERS / _BYTES); when the cap leaves
+no buffer the caller copies synchronously instead.
+
+Here buffers are plain pinned byte tensors sized in 2 MiB steps, handed out
+smallest-fit; a released buffer returns to the pool at once and is reused only
+after its last copy's event has completed.
+"""
+
+from __future__ import annotations
+
+import threading
+from dataclasses import dataclass
+
+GRANULE = 2 << 20
+
+
+@dataclass(eq=False)
+class PinnedSlot:
+    tensor: object            # pinned uint8 CPU tensor
+    event: object = None      # last copy into or out of it (torch.cuda.Event)
+    leased: bool = False
+
+    @property
+    def capacity(self) -> int:
+        return int(self.tensor.numel())
+
+    def view(self, nbytes: int):
+        return self.tensor[:nbytes]
+
+
+class PinnedPool:
+    """Pinned host buffers reused across layers (thread-safe)."""
+
+    def __init__(self, cap_bytes: int = 0, cap_buffers: int = 0) -> None:
+        self.cap_bytes = max(0, int(cap_bytes))
+        self.cap_buffers = max(0, int(cap_buffers))
+        self._slots: list[PinnedSlot] = []
+        self._lock = threading.Lock()
+        self.allocations = 0
+
+    @staticmethod
+    def _idle(slot: PinnedSlot) -> bool:
+        return not slot.leased and (slot.event is None or slot.event.query())
+
+    @property
+    def committed_bytes(self) -> int:
+        return sum(s.capacity for s in self._slots)
+
+    def acquire(self, nbytes: int, torch) -> PinnedSlot | None:
+        """A leased buffer of at least nbytes, or None when the caps leave none."""
+        nbytes = max(1, int(nbytes))
+        with self._lock:
+            fits = [s for s in self._slots if s.capacity >= nbytes and self._idle(s)]
+            if fits:
+                slot = min(fits, key=lambda s: s.capacity)
+                slot.leased = True
+                return slot
+            size = -(-nbytes // GRANULE) * GRANULE
+
+            def over() -> bool:
+                return ((self.cap_buffers and len(self._slots) >= self.cap_buffers)
+                        or (self.cap_bytes and self.committed_bytes + size > self.cap_bytes))
+
+            while over():
+                idle = [s for s in self._slots if self._idle(s)]
+                if not idle:
+                    return None
+                self._slots.remove(max(idle, key=lambda s: s.capacity))
+            if self.cap_bytes and size > self.cap_bytes:
+                return None
+            slot = PinnedSlot(torch.empty(size, dtype=torch.uint8, pin_memory=True), leased=True)
+            self._slots.append(slot)
+            self.allocations += 1
+            return slot
+
+    def release(self, slot: PinnedSlot) -> None:
+        with self._lock:
+            slot.leased = False
+
+
+class CopyStreams:
+    """One device-to-host copy stream per GPU, at the default priority."""
+
+    def __init__(self) -> None:
+        self._streams: dict[int, object] = {}
+        self._lock = threading.Lock()
+
+    def get(self, device, torch):
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        with self._lock:
+            stream = self._streams.get(index)
+            if stream is None:
+                stream = self._streams[index] = torch.cuda.Stream(device=index)
+            return stream
