@@ -157,6 +157,42 @@ def test_dropin_encode_more_tiles_than_one_finalize_pass(sz, codebooks):
     assert bytes(out[:size].cpu().numpy()) == bytes(ref)
 
 
+@pytest.mark.parametrize("label,n,src_shift,out_shift", [
+    ("llama3-8b 64 blocks", 2 * 64 * 16384, 0, 0),
+    ("70b 5 blocks, short last tiles", 2 * 5 * 2048, 0, 3),
+    ("unaligned source: generic kernels", 2 * 9 * 2048, 1, 0),
+])
+@pytest.mark.parametrize("rate", [0.001, 0.006])
+def test_dropin_encode_at_minimum_capacity_is_parallel(sz, codebooks, label, n, src_shift,
+                                                       out_shift, rate):
+    """Capacity align4(E) + 8, the reference ABI's minimum: the tiles stage their
+    escapes in their own body bytes (escape-dense tiles re-scanned, and at 0.6 %
+    the payload overflows), byte-identical to the oracle; bytes past the scratch
+    tail untouched."""
+    say("dropin min capacity", label, rate)
+    rng = np.random.default_rng(n + src_shift + int(rate * 1e4))
+    books = codebooks[6 * 32:7 * 32]
+    words = random_words(rng, n + src_shift, books, rate)
+    if rate < 0.005:
+        # three dense tiles: 300 escapes in one (re-scanned), 100 in another
+        outside = sorted(set(range(256)) - set(books))
+        for lo, count in ((4096 + 10, 300), (n // 2 + 50, 100), (n - 70, 60)):
+            for i in range(lo, lo + count):
+                words[src_shift + i] = (words[src_shift + i] & 0x807F) | (
+                    outside[i % len(outside)] << 7)
+    ref = oracle.top16_encode(words[src_shift:], oracle.top16_tables(books))
+    size = codec_format.top16_encoded_size(n)
+    capacity = ((size + 3) & ~3) + 8
+    backing = torch.full((capacity + out_shift + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    out = backing[out_shift:out_shift + capacity]
+    source = bf16(words)[src_shift:]
+    got = sz.encode_top16(source, out, 6)
+    torch.cuda.synchronize()
+    assert got == size
+    assert bytes(out[:size].cpu().numpy()) == bytes(ref)
+    assert bytes(backing[out_shift + capacity:].cpu().numpy()) == b"\xa5" * 64
+
+
 def test_dropin_encode_unaligned_source(sz, codebooks):
     say("dropin encode unaligned source")
     rng = np.random.default_rng(5)

@@ -65,6 +65,10 @@ struct LaunchArgs {
   unsigned int uniform_tiles;         // tiles of every payload when all are equal, else 0
   unsigned int uniform_slot_groups;   // escape-patch workgroups of every payload, likewise
   unsigned int uniform_blocks;        // blocks per plane of every payload when uniform_tiles
+  // Drop-in encode without room for a workspace: 0, or the escapes staged per tile
+  // inside the tile's own body bytes (u32 count, then staged entries), which the
+  // body pass writes last (top16_body_lanes).
+  unsigned int inbody_slots;
   // Escape directory of the launch's tiles (Top-16 tile kernels only; null when
   // absent): per 1024-word wave chunk of tile t a record dir_rec[4 * (4t + wave)
   // .. + 4) = {tile-relative slot of the chunk's first escape | chunk escapes << 16,

@@ -348,6 +348,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
     stop = first + 1;
   }
   unsigned long long running = 0;  // sequential mode: escapes in earlier tiles
+  const unsigned int inbody = a.inbody_slots;  // body bytes hold the staging (see below)
 
   for (unsigned int tile = first; tile < stop; ++tile) {
     const unsigned int r = find_payload(a, tile);
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
       if (!active) emask = 0;
       const bool first_lane = active && lane == 0;
       const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= end);
-      store16_run(payload + 5 + i0, body, active, first_lane, last_lane);
+      if (!inbody) store16_run(payload + 5 + i0, body, active, first_lane, last_lane);
       store8_run(payload + 5 + n + (i0 >> 1), codes, active, first_lane, last_lane);
     } else {
       // Generic geometry: per-word addressing and plane, byte stores.
@@ -401,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
         if (i >= end) break;
         const uint32_t w = a.kv[word_offset(a, d, i)];
         const uint32_t c = s_tab[(i >= half ? 256u : 0u) + ((w >> 7) & 0xFF)];
-        payload[5 + i] = (unsigned char)((w & 0x7F) | ((w >> 8) & 0x80));
+        if (!inbody) payload[5 + i] = (unsigned char)((w & 0x7F) | ((w >> 8) & 0x80));
         emask |= (c >> 4) << k;
         x[k >> 1] = (k & 1) ? (x[k >> 1] | (w << 16)) : w;
         codes[k >> 3] |= (c & 0x0F) << (4 * (k & 7));
@@ -432,6 +433,24 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
         }
       }
       running += tile_total;
+    } else if (inbody) {
+      // the count, then up to `slots` escapes, in the tile's own body bytes (the
+      // body is written from the source after the finalize has read them)
+      unsigned char* hdr = payload + 5 + start;
+      const unsigned int slots = min(inbody, (unsigned int)((end - start) >> 2) - 1u);
+      if (emask) {
+        unsigned int idx = lane_base;
+#pragma unroll
+        for (int k = 0; k < kWordsPerLane; ++k) {
+          if (!((emask >> k) & 1)) continue;
+          if (idx < slots)
+            *reinterpret_cast<u32_unaligned*>(hdr + 4 + 4 * idx) =
+                ((unsigned int)(i0 + k - start) << 8) | ((x[k >> 1] >> (7 + 16 * (k & 1))) & 0xFF);
+          ++idx;
+        }
+      }
+      if (tid == 0) *reinterpret_cast<u32_unaligned*>(hdr) = tile_total;
+      zero_escape_share(payload, n, tile - d.tile_begin, payload_tiles(a, n));
     } else {
       unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
       if (emask) {
@@ -463,6 +482,59 @@ __global__ __launch_bounds__(kThreads) void top16_encode_lanes(LaunchArgs a, Enc
   }
 }
 
+
+// Body bytes of every tile, from the source (the last pass of the drop-in encode
+// whose escapes were staged in the body bytes).
+template <bool kFast>
+__global__ __launch_bounds__(kThreads) void top16_body_lanes(LaunchArgs a, EncodeGeom g) {
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1);
+  const unsigned int tile = xcd_remap(blockIdx.x, gridDim.x);
+  const unsigned int r = find_payload(a, tile);
+  const PayloadDesc d = a.p[r];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long half = n >> 1;
+  unsigned long long start, end;
+  tile_range(a, d, tile - d.tile_begin, n, start, end);
+  unsigned char* payload = a.buf + d.buf_offset;
+  const unsigned long long i0 = start + (unsigned long long)tid * kWordsPerLane;
+  const bool active = i0 < end;
+  if (kFast) {
+    const unsigned int plane = start >= half ? 1u : 0u;
+    uint32_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (active) {
+      const unsigned int in_plane = (unsigned int)(i0 - plane * half);
+      const unsigned int j = div_u32(in_plane, g.bw_magic, g.bw);
+      const unsigned int within = in_plane - j * g.bw;
+      const unsigned long long blk =
+          a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+      const uint4* src = reinterpret_cast<const uint4*>(
+          a.kv + plane * a.plane_stride + blk * a.block_stride + within);
+      const uint4 v0 = src[0];
+      const uint4 v1 = src[1];
+      x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w;
+      x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+    }
+    uint32_t body[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t w0 = x[2 * q], w1 = x[2 * q + 1];
+      const uint32_t t0 = (w0 & 0x007F007Fu) | ((w0 >> 8) & ~0x007F007Fu);
+      const uint32_t t1 = (w1 & 0x007F007Fu) | ((w1 >> 8) & ~0x007F007Fu);
+      body[q] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
+    }
+    const bool first_lane = active && lane == 0;
+    const bool last_lane = active && (lane == kWave - 1 || i0 + kWordsPerLane >= end);
+    store16_run(payload + 5 + i0, body, active, first_lane, last_lane);
+  } else {
+    for (int k = 0; k < kWordsPerLane; ++k) {
+      const unsigned long long i = i0 + k;
+      if (i >= end) break;
+      const uint32_t w = a.kv[word_offset(a, d, i)];
+      payload[5 + i] = (unsigned char)((w & 0x7F) | ((w >> 8) & 0x80));
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Tile kernels: the batched layout (aligned sections) with one block per wave.
@@ -829,7 +901,7 @@ __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned 
   }
 }
 
-template <int kFinGroups>
+template <int kFinGroups, bool kInBody>
 __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
   constexpr int kFinPerThread = kFinGroups;             // tile counts per thread per pass
   constexpr int kFinChunk = kThreads * kFinPerThread;   // tiles scanned per pass
@@ -869,6 +941,10 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   unsigned char* entries = payload + 5 + n + (n + 1) / 2;
   const unsigned int* counts = ws + d.tile_begin;
   const unsigned int* staged = ws + total_tiles + (unsigned long long)d.tile_begin * kStageSlots;
+  // kInBody (drop-in encode without a workspace): each tile's count and staged
+  // escapes sit in its own body bytes (u32 count, then the entries; tiles of at
+  // least 64 words)
+  const unsigned int inbody = kInBody ? a.inbody_slots : 0u;
   if (tid == 0) s_over_count = 0;  // ordered by the barriers of the first scan
 
   unsigned long long running = 0;  // escapes in earlier chunks
@@ -885,15 +961,35 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
     for (int k = 0; k < kFinPerThread; ++k) {
       // loads without branches: indices past the chunk read its last count
       const unsigned int t = tid * kFinPerThread + k;
-      const unsigned int v = counts[chunk0 + min(t, m - 1)];
+      const unsigned int tt = chunk0 + min(t, m - 1);
+      unsigned int v;
+      if (kInBody) {
+        unsigned long long ts, te;
+        tile_range(a, d, tt, n, ts, te);
+        v = *reinterpret_cast<const u32_unaligned*>(payload + 5 + ts);
+      } else {
+        v = counts[tt];
+      }
       mine[k] = t < m ? v : 0;
       sum += mine[k];
     }
     const unsigned int own = tid * kFinPerThread + grp;  // this thread's tile of the group
-    const unsigned int* st = staged + (unsigned long long)(chunk0 + min(own, m - 1)) * kStageSlots;
+    const unsigned int own_c = chunk0 + min(own, m - 1);
+    const unsigned int* st = staged + (unsigned long long)own_c * kStageSlots;
+    const unsigned char* st_body = nullptr;
+    unsigned int slots = kStageSlots;
+    if (kInBody) {
+      unsigned long long ts, te;
+      tile_range(a, d, own_c, n, ts, te);
+      st_body = payload + 5 + ts + 4;
+      slots = min(inbody, (unsigned int)((te - ts) >> 2) - 1u);
+    }
+    auto staged_at = [&](unsigned int q) -> unsigned int {
+      return kInBody ? *reinterpret_cast<const u32_unaligned*>(st_body + 4 * q) : st[q];
+    };
     unsigned int pre[kFinPreload];
 #pragma unroll
-    for (int q = 0; q < kFinPreload; ++q) pre[q] = st[q];
+    for (int q = 0; q < kFinPreload; ++q) pre[q] = staged_at(q);
     unsigned int chunk_total;
     unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
 
@@ -908,7 +1004,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
     if (dir_base && own < m)
       dir_base[d.tile_begin + chunk0 + own] = (unsigned int)min(base, 0xFFFFFFFFull);
     if (c != 0 && base < cap) {
-      if (c > (unsigned int)kStageSlots) {
+      if (c > slots) {
         const unsigned int q = atomicAdd(&s_over_count, 1u);
         s_over_tile[q] = chunk0 + own;
         s_over_base[q] = (unsigned int)base;
@@ -922,7 +1018,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
 #pragma unroll
           for (int e = 0; e < kFinPreload; ++e) {
             const unsigned int q = q0 + e;
-            v[e] = q0 == 0 ? pre[e] : (q < c ? st[q] : 0u);
+            v[e] = q0 == 0 ? pre[e] : (q < c ? staged_at(q) : 0u);
           }
 #pragma unroll
           for (int e = 0; e < kFinPreload; ++e) {
@@ -1144,11 +1240,28 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     const unsigned int end = r + 1 < a.payload_count ? a.p[r + 1].tile_begin : a.total_tiles;
     max_tiles = std::max(max_tiles, end - a.p[r].tile_begin);
   }
-  if (max_tiles >= kFinLargeTiles)
-    hipLaunchKernelGGL(top16_encode_finalize<16>, dim3(a.payload_count * 16), block, 0, stream, a);
-  else
-    hipLaunchKernelGGL(top16_encode_finalize<8>, dim3(a.payload_count * 8), block, 0, stream, a);
-  return check_launch("top16_encode_finalize");
+  const bool large = max_tiles >= kFinLargeTiles;
+  const dim3 fin_grid(a.payload_count * (large ? 16 : 8));
+  if (a.inbody_slots) {
+    if (large)
+      hipLaunchKernelGGL((top16_encode_finalize<16, true>), fin_grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((top16_encode_finalize<8, true>), fin_grid, block, 0, stream, a);
+  } else if (large) {
+    hipLaunchKernelGGL((top16_encode_finalize<16, false>), fin_grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((top16_encode_finalize<8, false>), fin_grid, block, 0, stream, a);
+  }
+  if (long long rc = check_launch("top16_encode_finalize")) return rc;
+  if (a.inbody_slots) {
+    // the staging in the body bytes has been read: write the body
+    if (p.kernel == Kernel::kGeneric)
+      hipLaunchKernelGGL(top16_body_lanes<false>, dim3(a.total_tiles), block, 0, stream, a, g);
+    else
+      hipLaunchKernelGGL(top16_body_lanes<true>, dim3(a.total_tiles), block, 0, stream, a, g);
+    return check_launch("top16_body_lanes");
+  }
+  return 0;
 }
 
 long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream) {
@@ -1243,15 +1356,30 @@ extern "C" long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr,
   // Parallel tiles need a workspace for per-tile escape counts; it lives in the
   // caller's buffer past the payload when the capacity allows, else one
   // workgroup walks the tiles in order.
+  // Without that room (the ABI only promises align4(E) + 8 bytes) the tiles are still
+  // encoded in parallel: each stages its escape count and escapes in its own body
+  // bytes, the finalize places them, and a last pass writes the body from the source
+  // (every tile needs 64 words for its staging); otherwise one workgroup walks them.
   Plan plan = make_plan(geometry_fast, aligned, false);
   unsigned int tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
   const unsigned long long ws_offset = align_up(dst_ptr + encoded, 16) - dst_ptr;
   const unsigned long long ws_bytes = workspace_words(tiles) * 4;
-  if (tiles == 1 || ws_offset + ws_bytes > capacity) {
-    plan = make_plan(geometry_fast, aligned, true);
-    tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
-  } else {
+  if (tiles > 1 && ws_offset + ws_bytes <= capacity) {
     a.workspace = reinterpret_cast<unsigned int*>(dst_ptr + ws_offset);
+  } else {
+    Plan staged = make_plan(geometry_fast, false, false);  // lanes or generic kernels
+    const unsigned long long tile_words = 1ull << staged.tile_shift;
+    const unsigned long long span = staged.per_plane ? count / 2 : count;
+    const unsigned long long last = span % tile_words ? span % tile_words : tile_words;
+    const unsigned int staged_tiles = host_payload_tiles(count, staged.per_plane, staged.tile_shift);
+    if (staged_tiles > 1 && std::min(last, span) >= 64) {
+      plan = staged;
+      tiles = staged_tiles;
+      a.inbody_slots = kStageSlots - 1;  // 512 bytes: count + 127 escapes
+    } else {
+      plan = make_plan(geometry_fast, aligned, true);
+      tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
+    }
   }
   apply_plan(a, plan);
   a.total_tiles = tiles;
