@@ -236,6 +236,21 @@ long long kvq_splitzip_bf16_decode_mode_paged(
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long stream_ptr, int bits);
 
+/* Decode + scatter of the reference connector's torch-op codec payloads, modes 0
+ * (palette of high bytes), 1 (four nibble planes) and 2 (sign/magnitude), mixed
+ * in one batch (no counterpart in the reference library: it replaces the torch
+ * decoders of _copy_splitzip_bf16_native_blocks, src/unchain_kv/vllm_connector.py:
+ * 5168-5252, followed by index_copy_). Payload r (src + src_offsets[r],
+ * encoded_bytes[r] long) goes into the blocks of block table r; a payload whose
+ * header does not give exactly its encoded size is left unapplied. Returns the
+ * total raw bytes. */
+long long kvq_splitzip_bf16_decode_torchop_paged(
+    unsigned long long src_ptr, const unsigned long long* src_offsets,
+    const unsigned long long* encoded_bytes, unsigned long long payload_count,
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long stream_ptr);
+
 /* ------------------------------------------------------------------------------
  * bf16 exponent histograms of a paged layer: the statistics Top-16 codebooks are
  * fit from (no counterpart in the reference as a native call: it runs

@@ -342,3 +342,141 @@ def default_threads() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+# ---------------------------------------------------------------------------
+# the reference connector's torch-op codecs, payload modes 0, 1, 2
+# (src/unchain_kv/vllm_connector.py:3204-3343 encode, :5168-5252 decode); numpy
+
+def pack_bits_lsb(codes, width: int) -> np.ndarray:
+    """``_pack_splitzip_bits`` (vllm_connector.py:3345-3374): code i at bits
+    [i*width, i*width + width) of a little-endian bit stream, (count*width+7)//8
+    bytes."""
+    codes = np.asarray(codes, dtype=np.uint16).reshape(-1)
+    bits = ((codes[:, None] >> np.arange(width, dtype=np.uint16)) & 1).astype(np.uint8)
+    return np.packbits(bits.reshape(-1), bitorder="little")
+
+
+def unpack_bits_lsb(packed, count: int, width: int) -> np.ndarray:
+    """``_unpack_splitzip_bits`` (vllm_connector.py:3376-3404)."""
+    bits = np.unpackbits(np.asarray(packed, dtype=np.uint8), bitorder="little")[:count * width]
+    weights = (1 << np.arange(width, dtype=np.uint16)).astype(np.uint16)
+    return (bits.reshape(count, width).astype(np.uint16) * weights).sum(axis=1).astype(np.uint16)
+
+
+def _split_words(words):
+    w = np.asarray(words, dtype=np.uint16).reshape(-1)
+    return w, (w >> 8).astype(np.uint8), (w & 0xFF).astype(np.uint8)
+
+
+def encode_signmag(words) -> np.ndarray | None:
+    """Mode 2 (vllm_connector.py:3204-3247): [2][width][mag_min][low n][sign bits]
+    [magnitude - mag_min in `width` bits]; None when the width is 7 or the payload
+    is not smaller than the raw words."""
+    w, high, low = _split_words(words)
+    n = w.size
+    sign, mag = high >> 7, high & 0x7F
+    mag_min = int(mag.min())
+    width = max(1, (int(mag.max()) - mag_min).bit_length())
+    size = 3 + n + (n + 7) // 8 + (n * width + 7) // 8
+    if width >= 7 or size >= 2 * n:
+        return None
+    return np.concatenate([np.array([2, width, mag_min], np.uint8), low, pack_bits_lsb(sign, 1),
+                           pack_bits_lsb(mag - mag_min, width)])
+
+
+def encode_palette(words) -> np.ndarray | None:
+    """Mode 0 (vllm_connector.py:3249-3276): [0][width][256-byte sorted palette of
+    high bytes, zero-filled][low n][palette index in `width` bits]."""
+    w, high, low = _split_words(words)
+    n = w.size
+    palette, codes = np.unique(high, return_inverse=True)
+    width = max(1, (palette.size - 1).bit_length())
+    size = 258 + n + (n * width + 7) // 8
+    if width >= 8 or size >= 2 * n:
+        return None
+    head = np.zeros(258, np.uint8)
+    head[1] = width
+    head[2:2 + palette.size] = palette
+    return np.concatenate([head, low, pack_bits_lsb(codes, width)])
+
+
+def encode_nibbles(words) -> np.ndarray | None:
+    """Mode 1 (vllm_connector.py:3278-3343): [1][4 widths][4 x 16-byte sorted
+    palettes of the nibble values][4 planes of indices], nibble p = bits 4p..4p+3;
+    width 1, 2 or 4 by the plane's distinct values."""
+    w = np.asarray(words, dtype=np.uint16).reshape(-1)
+    n = w.size
+    head = np.zeros(69, np.uint8)
+    head[0] = 1
+    planes = []
+    for p, shift in enumerate((0, 4, 8, 12)):
+        nibble = ((w >> shift) & 0xF).astype(np.uint8)
+        palette, codes = np.unique(nibble, return_inverse=True)
+        width = 1 if palette.size <= 2 else 2 if palette.size <= 4 else 4
+        head[1 + p] = width
+        head[5 + 16 * p:5 + 16 * p + palette.size] = palette
+        planes.append(pack_bits_lsb(codes, width))
+    payload = np.concatenate([head] + planes)
+    return payload if payload.size < 2 * n else None
+
+
+def encode_torchop(words) -> np.ndarray | None:
+    """The reference's codec choice when the native codec is not used
+    (vllm_connector.py:3204-3343): sign/magnitude, else palette, else nibble planes."""
+    for encode in (encode_signmag, encode_palette, encode_nibbles):
+        payload = encode(words)
+        if payload is not None:
+            return payload
+    return None
+
+
+def decode_torchop(payload, n: int) -> np.ndarray | None:
+    """Words of a mode 0, 1 or 2 payload of n words, or None when the restore
+    validation of vllm_connector.py:5168-5252 refuses it. The arithmetic is the
+    reference's: int32 intermediates, the word truncated to 16 bits at the end."""
+    p = np.asarray(payload, dtype=np.uint8).reshape(-1)
+    size = p.size
+    if size < 1:
+        return None
+    mode = int(p[0])
+    if mode == 0:
+        if size < 258:
+            return None
+        width = int(p[1])
+        if not 1 <= width < 8 or size != 258 + n + (n * width + 7) // 8:
+            return None
+        codes = unpack_bits_lsb(p[258 + n:], n, width)
+        high = p[2:258][codes].astype(np.int64)
+        words = (high << 8) | p[258:258 + n].astype(np.int64)
+    elif mode == 1:
+        if size < 69:
+            return None
+        widths = [int(x) for x in p[1:5]]
+        if any(x not in (1, 2, 4) for x in widths):
+            return None
+        sizes = [(n * x + 7) // 8 for x in widths]
+        if size != 69 + sum(sizes):
+            return None
+        words = np.zeros(n, np.int64)
+        at = 69
+        for plane, (width, nbytes) in enumerate(zip(widths, sizes)):
+            codes = unpack_bits_lsb(p[at:at + nbytes], n, width)
+            words |= p[5 + 16 * plane:5 + 16 * plane + 16][codes].astype(np.int64) << (4 * plane)
+            at += nbytes
+    elif mode == 2:
+        if size < 3:
+            return None
+        width, mag_min = int(p[1]), int(p[2])
+        if not 1 <= width < 7:
+            return None
+        sign_bytes, mag_bytes = (n + 7) // 8, (n * width + 7) // 8
+        if size != 3 + n + sign_bytes + mag_bytes:
+            return None
+        low = p[3:3 + n].astype(np.int64)
+        sign = unpack_bits_lsb(p[3 + n:3 + n + sign_bytes], n, 1).astype(np.int64)
+        mag = unpack_bits_lsb(p[3 + n + sign_bytes:], n, width).astype(np.int64)
+        words = (((sign << 7) | (mag + mag_min)) << 8) | low
+    else:
+        return None
+    return (words & 0xFFFF).astype(np.uint16)

@@ -154,12 +154,37 @@ def test_restore_rejects_bad_payloads_before_any_gpu_work(payload, encoded_bytes
     assert got == [(0, 0)]
 
 
-def test_restore_rejects_unsupported_torch_modes_and_bad_blocks():
+@pytest.mark.parametrize("payload", [
+    b"\x01\x00\x00",                                   # nibble planes: shorter than the header
+    b"\x01\x04\x04\x04\x03" + bytes(64) + bytes(16),   # a plane width of 3
+    b"\x02\x07\x00" + bytes(8 + 1 + 7),                # sign/magnitude width 7
+    b"\x02\x01\x00" + bytes(8 + 1 + 1 + 1),            # one byte too long
+    b"\x00\x00" + bytes(256 + 8 + 1),                   # palette width 0
+])
+def test_restore_refuses_torchop_payloads_with_bad_headers(payload):
+    """Modes 0, 1 and 2 pass the reference's header checks
+    (vllm_connector.py:5168-5252) before any GPU work (a CPU layer here)."""
+    c, trace = codec()
+    kv = torch.zeros((2, 2, 2), dtype=torch.bfloat16)
+    meta = {"raw_bytes": 16, "encoded_bytes": len(payload)}
+    assert c.load_kv_layer_batch(0, kv, [([0, 1], payload, meta)]) == [(0, 0)]
+    assert trace.names() == []
+
+
+def test_torchop_sizes_follow_the_reference_rules():
+    n = 8
+    assert codec_format.torchop_encoded_size(b"\x02\x01\x00", n) == 3 + 8 + 1 + 1
+    assert codec_format.torchop_encoded_size(b"\x02\x06\x05", n) == 3 + 8 + 1 + 6
+    head = bytes([1, 4, 2, 1, 4]) + bytes(64)
+    assert codec_format.torchop_encoded_size(head, n) == 69 + 4 + 2 + 1 + 4
+    assert codec_format.torchop_encoded_size(bytes([0, 7]) + bytes(256), n) == 258 + 8 + 7
+    assert codec_format.torchop_encoded_size(bytes([0, 8]) + bytes(256), n) is None
+    assert codec_format.torchop_encoded_size(b"\x05", n) is None
+
+
+def test_restore_rejects_bad_blocks():
     c, trace = codec()
     kv = torch.zeros((2, 4, 2), dtype=torch.bfloat16)
-    meta = {"raw_bytes": 16, "encoded_bytes": 3}
-    assert c.load_kv_layer_batch(0, kv, [([0, 1], b"\x01\x00\x00", meta)]) == [(0, 0)]
-    assert trace.names() == ["splitzip_mode_unsupported"]
     raw = {"raw_bytes": 16, "encoded_bytes": 17}
     assert c.load_kv_layer_batch(0, kv, [([0, 0], b"\x06" + bytes(16), raw)]) == [(0, 0)]
     assert c.load_kv_layer_batch(0, kv, [([0, 9], b"\x06" + bytes(16), raw)]) == [(0, 0)]

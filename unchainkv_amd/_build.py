@@ -19,7 +19,7 @@ LIB_DIR = PACKAGE / "lib"
 LIB_NAME = "libunchain_kv_splitzip_cuda.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 SOURCES = ("splitzip_top16.hip", "splitzip_fixed6.hip", "splitzip_histogram.hip",
-           "splitzip_attention.hip", "splitzip_writeback.hip")
+           "splitzip_attention.hip", "splitzip_writeback.hip", "splitzip_torchop.hip")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

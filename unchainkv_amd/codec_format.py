@@ -7,11 +7,37 @@ Sizes follow native/unchain_kv/kvq_splitzip_cuda.cu:300-303 (fixed6/fixed5) and
 
 from __future__ import annotations
 
+MODE_PALETTE = 0    # torch-op codecs of the reference connector (restore only)
+MODE_NIBBLES = 1
+MODE_SIGNMAG = 2
 MODE_FIXED6 = 3
 MODE_FIXED5 = 4
 MODE_TOP16 = 5
 MODE_RAW = 6
 MODE_OVERFLOW = 255
+
+
+def torchop_encoded_size(header, n: int) -> int | None:
+    """Size a mode 0, 1 or 2 payload of n words must have, from its first bytes, or
+    None when the header itself is refused (the restore checks of
+    src/unchain_kv/vllm_connector.py:5168-5252)."""
+    view = memoryview(header).cast("B")
+    if len(view) < 1:
+        return None
+    mode = view[0]
+    if mode == MODE_PALETTE:
+        if len(view) < 258 or not 1 <= view[1] < 8:
+            return None
+        return 258 + n + (n * view[1] + 7) // 8
+    if mode == MODE_NIBBLES:
+        if len(view) < 69 or any(w not in (1, 2, 4) for w in view[1:5]):
+            return None
+        return 69 + sum((n * w + 7) // 8 for w in view[1:5])
+    if mode == MODE_SIGNMAG:
+        if len(view) < 3 or not 1 <= view[1] < 7:
+            return None
+        return 3 + n + (n + 7) // 8 + (n * view[1] + 7) // 8
+    return None
 
 
 def top16_escape_capacity(n: int) -> int:

@@ -24,11 +24,12 @@ This module keeps that codec behaviour and its knobs, batched per layer:
   (``[6] + raw bytes``) (:4526-4665);
 * load (``load_kv_layer`` / ``load_kv_layer_batch``): the restore validation of
   ``_copy_splitzip_bf16_native_blocks`` (:5098-5313) and GPU decode + scatter of
-  modes 3, 4 and 5, raw copy of mode 6.
+  modes 0-5 (0, 1 and 2, the reference's torch-op codecs, in one launch), raw copy
+  of mode 6.
 
 Everything runs on the HIP library; there is no CPU codec path. Modes 0, 1 and 2
-(the reference's torch-op codecs) are not produced and are refused on load.
-Payloads below 1 MiB use fixed6, as the reference does when its codec buffer pool
+are restored but not produced (the reference sends them only without its native
+codec). Payloads below 1 MiB use fixed6, as the reference does when its codec buffer pool
 is in use. The KV blocks of a saved layer must stay unchanged until ``ready``
 returns: the fallback re-encodes read them again (the reference keeps a gathered
 copy instead). The writeback therefore skips an overflowed payload on the GPU (its
@@ -93,6 +94,10 @@ class CodecConfig:
             host_mirror_bytes=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_BYTES", 0)),
         )
 
+
+# payload modes of the reference's torch-op codecs, restored by one decode launch
+TORCHOP_MODES = (codec_format.MODE_PALETTE, codec_format.MODE_NIBBLES, codec_format.MODE_SIGNMAG)
+TORCHOP = "torchop"
 
 # bits of a payload as the reference's _SplitzipCudaPayload records them
 BITS_TOP16, BITS_FIXED5, BITS_FIXED6, BITS_RAW = 4, 5, 6, 16
@@ -567,6 +572,8 @@ class SplitzipLayerCodec:
             return None
         if mode == codec_format.MODE_RAW and encoded_bytes != raw_bytes + 1:
             return None
+        if mode in TORCHOP_MODES and codec_format.torchop_encoded_size(view, n) != encoded_bytes:
+            return None
         return mode, raw_bytes, view
 
     # ------------------------------------------------------------------
@@ -650,18 +657,16 @@ class SplitzipLayerCodec:
             if checked is None:
                 continue
             mode, raw_bytes, view = checked
-            if mode not in {codec_format.MODE_FIXED6, codec_format.MODE_FIXED5,
-                            codec_format.MODE_TOP16, codec_format.MODE_RAW}:
-                self.trace.event("splitzip_mode_unsupported", mode=mode)
-                continue
-            groups.setdefault(mode, []).append((k, block_ids, raw_bytes, view))
+            # modes 0, 1 and 2 (the torch-op codecs) share one decode launch
+            key = TORCHOP if mode in TORCHOP_MODES else mode
+            groups.setdefault(key, []).append((k, block_ids, raw_bytes, view))
         if not groups:
             return results
         block_words = kv_layer[0, 0].numel()
         # one pinned staging buffer, each payload placed where the decode kernels
         # find its sections aligned
         header = {codec_format.MODE_TOP16: 5, codec_format.MODE_FIXED6: 65,
-                  codec_format.MODE_FIXED5: 33, codec_format.MODE_RAW: 1}
+                  codec_format.MODE_FIXED5: 33, codec_format.MODE_RAW: 1, TORCHOP: 0}
         layout, end = [], 0
         for mode, members in groups.items():
             for member in members:
@@ -688,6 +693,8 @@ class SplitzipLayerCodec:
                     continue
                 copied = sz.decode_top16_paged(device, starts, sizes, kv_layer, batch,
                                                codebooks=books)
+            elif mode == TORCHOP:
+                copied = sz.decode_torchop_paged(device, starts, sizes, kv_layer, batch)
             elif mode == codec_format.MODE_RAW:
                 copied = 0
                 for (k, ids, raw_bytes, _), start in zip(members, starts):
@@ -702,6 +709,10 @@ class SplitzipLayerCodec:
             if copied:
                 for k, ids, raw_bytes, _ in members:
                     results[k] = (len(ids), raw_bytes)
-                self.trace.event("splitzip_native_decode", blocks=sum(len(m[1]) for m in members),
-                                 bytes=int(copied), mode=mode)
+                modes = sorted({int(m[3][0]) for m in members}) if mode == TORCHOP else [mode]
+                for m in modes:
+                    self.trace.event("splitzip_native_decode",
+                                     blocks=sum(len(x[1]) for x in members if int(x[3][0]) == m),
+                                     bytes=sum(x[2] for x in members if int(x[3][0]) == m),
+                                     mode=m)
         return results

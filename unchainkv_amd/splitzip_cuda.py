@@ -103,6 +103,12 @@ _SIGNATURES = (
         False,
     ),
     (
+        "kvq_splitzip_bf16_decode_torchop_paged",
+        [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
         "kvq_splitzip_bf16_decode_mode_paged",
         [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, ctypes.c_int],
         ctypes.c_longlong,
@@ -766,6 +772,37 @@ def decode_bf16_paged(source, src_offsets, encoded_bytes, kv_layer, batch: Paged
                     int(stream), int(bits))
     if copied < 0:
         _raise_last(lib, "splitzip palette paged decode failed")
+    return int(copied) or None
+
+
+def decode_torchop_paged(source, src_offsets, encoded_bytes, kv_layer,
+                         batch: PagedBatch) -> int | None:
+    """Decode the reference connector's torch-op payloads (modes 0, 1, 2: palette,
+    nibble planes, sign/magnitude; src/unchain_kv/vllm_connector.py:5168-5252)
+    ``source[src_offsets[r]:][:encoded_bytes[r]]`` and scatter payload r into
+    ``batch.block_tables[r]``; modes may be mixed. A payload whose header does not
+    match its size is left unapplied. Returns the total raw bytes or ``None``."""
+    lib = _load()
+    decode = getattr(lib, "kvq_splitzip_bf16_decode_torchop_paged", None) if lib else None
+    if decode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch) or not batch.unique_blocks:
+        return None
+    if source.dtype != torch.uint8 or not source.is_contiguous() or source.device != kv_layer.device:
+        return None
+    if not _payloads_fit(source, src_offsets, encoded_bytes, batch):
+        return None
+    offs = batch._c_array(src_offsets, None, None)
+    encs = batch._c_array(encoded_bytes, None, None)
+    stream = _stream_handle(kv_layer.device, torch)
+    copied = decode(int(source.data_ptr()), offs, encs, batch.payload_count,
+                    int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                    batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                    int(stream))
+    if copied < 0:
+        _raise_last(lib, "splitzip torch-op paged decode failed")
     return int(copied) or None
 
 
