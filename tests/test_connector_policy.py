@@ -134,6 +134,25 @@ def test_writeback_skips_fragmented_tables():
                                                      "segments": 4})]
 
 
+def test_writeback_skips_blocks_shared_with_another_request():
+    """A request whose run shares a block with another request of the layer (prefix
+    caching) is not written back: the other request's fallback or raw copy must
+    still read the block's KV words."""
+    from unchainkv_amd.connector import LayerPayload
+
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace)
+    a = LayerPayload(0, [4, 5, 6], 3 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100)
+    b = LayerPayload(1, [6, 7], 2 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100)
+    c = LayerPayload(2, [9, 10], 2 << 20, BITS_TOP16, BITS_TOP16, encoded_bytes=100)
+    d = LayerPayload(3, [10], 1 << 20, BITS_FIXED6, BITS_FIXED6, encoded_bytes=100)
+    assert codec._writeback_members([a, b, c], 3, [a, b, c, d]) == []
+    assert [e[1]["reason"] for e in trace.rows] == ["shared", "shared", "shared"]
+    trace.rows.clear()
+    assert codec._writeback_members([a, c], 3, [a, c]) == [0, 1]
+    assert trace.rows == []
+
+
 torch = pytest.importorskip("torch")
 
 

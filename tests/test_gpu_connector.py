@@ -304,3 +304,39 @@ def test_pinned_pool_reuse_and_cap(sz, codebooks):
     payloads = roundtrip(codec, 5, kv, tables, pool)      # reuses the released buffer
     assert codec.pinned.allocations == 1
     assert [bytes(p.view) for p in payloads] == [bytes(p.view) for p in a]
+
+
+def test_restore_of_reference_ordered_escapes_through_the_host_directory(sz, codebooks):
+    """A Top-16 payload whose escape list is in the reference encoder's atomic order
+    (shuffled) and whose unused slots hold garbage: the restore builds the escape
+    directory on the host (sorting the list in its staging copy) and decodes in one
+    kernel, exactly."""
+    say("connector restore, shuffled escapes")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(21)
+    pool = 64
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.002), pool)
+    tables = disjoint_tables(rng, pool, [16, 24])
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=RecordingTrace())
+    payloads = codec.ready(codec.save_kv_layer(5, kv, tables))
+    sent = []
+    for p in payloads:
+        data = bytearray(p.view)
+        n = p.raw_bytes // 2
+        lo, hi = codec_format.top16_sections(n)["escapes"]
+        count = int.from_bytes(data[1:5], "little")
+        assert count > 10
+        entries = [bytes(data[lo + 5 * i:lo + 5 * i + 5]) for i in range(count)]
+        order = rng.permutation(count)
+        data[lo:lo + 5 * count] = b"".join(entries[i] for i in order)
+        data[lo + 5 * count:hi] = rng.integers(0, 256, hi - lo - 5 * count, dtype=np.uint8).tobytes()
+        sent.append(bytes(data))
+    target = torch.zeros_like(kv)
+    recv = [[(b + 11) % pool for b in t] for t in tables]
+    requests = [(rt, data, p.metadata(5, BW)) for rt, data, p in zip(recv, sent, payloads)]
+    assert codec.load_kv_layer_batch(5, target, requests) == [(len(t), 4 * len(t) * BW)
+                                                              for t in tables]
+    torch.cuda.synchronize()
+    src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
+    for t, rt in zip(tables, recv):
+        assert np.array_equal(dst[:, rt], src[:, t])

@@ -340,15 +340,26 @@ class SplitzipLayerCodec:
             self.pinned.release(slot)
         pending.slots.clear()
 
-    def _writeback_members(self, members: list, layer_index: int) -> list[int]:
+    def _writeback_members(self, members: list, layer_index: int,
+                           payloads: list | None = None) -> list[int]:
         """Indices of the Top-16 members whose blocks are one contiguous run (the
-        reference skips fragmented tables, vllm_connector.py:3479-3488)."""
+        reference skips fragmented tables, vllm_connector.py:3479-3488) and are not
+        blocks of another request of the layer (``payloads``): a block shared with
+        another request, as prefix caching shares them, would reach that request's
+        fallback re-encode or raw copy holding payload bytes."""
+        owners: dict[int, int] = {}
+        for p in payloads if payloads is not None else members:
+            for b in p.block_ids:
+                owners[b] = owners.get(b, 0) + 1
         picks = []
         for i, p in enumerate(members):
             runs = _contiguous_runs(p.block_ids)
             if len(runs) != 1:
                 self.trace.event("codec_writeback_skip", layer=layer_index, reason="fragmented",
                                  segments=len(runs) * 2)
+                continue
+            if any(owners[b] > 1 for b in p.block_ids):
+                self.trace.event("codec_writeback_skip", layer=layer_index, reason="shared")
                 continue
             if not 0 < p.encoded_bytes < p.raw_bytes:
                 continue
@@ -364,7 +375,7 @@ class SplitzipLayerCodec:
         staged) when no payload qualifies or the library declines."""
         out, offsets, sizes, batch = result
         layer = pending.layer_index
-        picks = self._writeback_members(members, layer)
+        picks = self._writeback_members(members, layer, pending.payloads)
         if not picks:
             return False
         sz = self._lib()
@@ -434,6 +445,8 @@ class SplitzipLayerCodec:
             payloads.append(LayerPayload(r, ids, raw, bits, bits, epoch, probe))
         pending = PendingLayer(layer_index, kv_layer, block_words, payloads)
 
+        # every group is encoded before the Top-16 writeback overwrites any block
+        top_result = None
         top = [p for p in payloads if p.bits == BITS_TOP16]
         if top:
             try:
@@ -450,9 +463,7 @@ class SplitzipLayerCodec:
             else:
                 for p, size in zip(top, result[2]):
                     p.encoded_bytes = int(size)
-                if not (self.codec_writeback_overwrite
-                        and self._stage_writeback(pending, top, result, torch)):
-                    self._assign(pending, top, result, torch)
+                top_result = result
         five = [p for p in payloads if p.bits == BITS_FIXED5]
         if five:
             result = self._encode_group(BITS_FIXED5, kv_layer, five, block_words, layer_index)
@@ -471,6 +482,10 @@ class SplitzipLayerCodec:
                     p.bits = BITS_RAW
             else:
                 self._assign(pending, six, result, torch)
+        if top_result is not None:
+            if not (self.codec_writeback_overwrite
+                    and self._stage_writeback(pending, top, top_result, torch)):
+                self._assign(pending, top, top_result, torch)
         self.trace.event("codec_encode_submitted", layer=layer_index, requests=len(payloads),
                          raw_bytes=sum(p.raw_bytes for p in payloads))
         return pending
@@ -673,10 +688,30 @@ class SplitzipLayerCodec:
                 start = -(-(end + header[mode]) // 256) * 256 - header[mode]
                 layout.append((mode, member, start))
                 end = start + len(member[3])
+        batches = {mode: sz.PagedBatch([m[1] for m in members], block_words, kv_layer.device)
+                   for mode, members in groups.items()}
+        # the Top-16 payloads' escape directory rides along in the same copy, so
+        # their decode is one kernel
+        top = groups.get(codec_format.MODE_TOP16)
+        dir_at = dir_bytes = 0
+        if top:
+            dir_bytes = batches[codec_format.MODE_TOP16].directory_bytes()
+            if dir_bytes:
+                dir_at = -(-end // 256) * 256
+                end = dir_at + dir_bytes
         host, slot = self._host_buffer(max(end, 1), torch)
-        host_view = memoryview(host.numpy())
+        host_np = host.numpy()
+        host_view = memoryview(host_np)
         for mode, member, start in layout:
             host_view[start:start + len(member[3])] = member[3]
+        if dir_bytes:
+            tops = [start for m, _, start in layout if m == codec_format.MODE_TOP16]
+            built = sz.build_directory(host_np, tops, [len(m[3]) for m in top],
+                                       batches[codec_format.MODE_TOP16])
+            if built is None:
+                dir_bytes = 0
+            else:
+                host_np[dir_at:dir_at + dir_bytes] = built
         device = host.to(kv_layer.device, non_blocking=True)
         if slot is not None:
             # back to the pool at once: reused after the host-to-device copy ends
@@ -685,14 +720,19 @@ class SplitzipLayerCodec:
             self.pinned.release(slot)
         for mode, members in groups.items():
             starts = [start for m, _, start in layout if m == mode]
-            batch = sz.PagedBatch([m[1] for m in members], block_words, kv_layer.device)
+            batch = batches[mode]
             sizes = [len(m[3]) for m in members]
             if mode == codec_format.MODE_TOP16:
                 books = self._layer_codebooks(layer_index)
                 if books is None:
                     continue
+                directory = device[dir_at:dir_at + dir_bytes] if dir_bytes else None
                 copied = sz.decode_top16_paged(device, starts, sizes, kv_layer, batch,
-                                               codebooks=books)
+                                               codebooks=books, directory=directory)
+                if not copied and directory is not None:
+                    # a layout the one-kernel decode does not take: two kernels
+                    copied = sz.decode_top16_paged(device, starts, sizes, kv_layer, batch,
+                                                   codebooks=books)
             elif mode == TORCHOP:
                 copied = sz.decode_torchop_paged(device, starts, sizes, kv_layer, batch)
             elif mode == codec_format.MODE_RAW:
