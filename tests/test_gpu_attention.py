@@ -177,6 +177,38 @@ def test_overflowed_or_unsorted_payload_gives_nan_for_that_sequence_only(sz, cod
     assert torch.isfinite(out[1]).all()
 
 
+@pytest.mark.parametrize("disorder", ["shuffled", "one_swap_at_the_end", "one_swap_at_the_start"])
+def test_unordered_escape_list_gives_nan_for_every_head_of_that_sequence(sz, codebooks, disorder):
+    """Escape lists written in another order (the reference's encoder appends in
+    atomic order) are refused as a whole: every query head of the sequence is NaN,
+    even heads whose own escapes were walked in order, and even when the one
+    misplaced pair sits where no wave's walk meets it."""
+    say("fused attention escape order", disorder)
+    rng = np.random.default_rng(7)
+    books = codebooks[:32]
+    kv_heads = 4
+    words = [kv_words(rng, books, 512, kv_heads, 0.004) for _ in range(3)]
+    payloads, batch = encode_sequences(sz, words, kv_heads, books)
+    n = words[1].size
+    a = batch.out_offsets[1]
+    count = int.from_bytes(bytes(payloads[a + 1:a + 5].cpu().numpy()), "little")
+    assert count > 100
+    lo = a + 5 + n + n // 2
+    entries = payloads[lo:lo + 5 * count].view(count, 5).clone()
+    if disorder == "shuffled":
+        order = torch.from_numpy(rng.permutation(count)).cuda()
+    else:
+        order = torch.arange(count, device="cuda")
+        i = count - 2 if disorder == "one_swap_at_the_end" else 0
+        order[i], order[i + 1] = i + 1, i
+    payloads[lo:lo + 5 * count] = entries[order].reshape(-1)
+    q, _ = random_q(rng, 3, 4 * kv_heads)
+    out = sz.decode_attention_top16(q, payloads, batch.out_offsets, [512] * 3, kv_heads,
+                                    codebooks=books).float().cpu()
+    assert torch.isnan(out[1]).all()
+    assert torch.isfinite(out[0]).all() and torch.isfinite(out[2]).all()
+
+
 def test_llama3_8b_decode_step_against_decode_then_attend(sz):
     """Llama-3-8B GQA (32 q heads, 8 kv heads), batch 32, 8192 tokens each, KV in
     the Top-16 format with ~0.1% escapes; reference = GPU decode into bf16 KV, then

@@ -22,11 +22,16 @@
 // and writes bf16.
 //
 // Escapes: the kernel needs the escape list in ascending position order (what the
-// encoder of this library writes). Each wave finds its first K and V escape with a
-// 64-way search and then walks the list with its steps, one 64-entry window per
-// plane prefetched a step ahead. An entry found below the current step or a
-// decrease between neighbouring entries, or a payload whose byte 0 is not 5, makes
-// the sequence's output NaN rather than silently wrong.
+// encoder of this library writes; the reference's encoder appends escapes in
+// atomic order, so its lists may be unordered). Each wave finds its first K and V
+// escape with a 64-way search and then walks the list with its steps, one 64-entry
+// window per plane prefetched a step ahead. The search is only meaningful on an
+// ordered list, so the list's order is checked up front as well: the split
+// kernel's workgroups of a sequence share the check of every neighbouring pair of
+// entries between them. A decrease anywhere in the list, an entry found below the
+// current step, or a payload whose byte 0 is not 5, makes every output of the
+// sequence NaN (the combine kernel looks at all of the sequence's partials)
+// rather than silently wrong.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -395,6 +400,18 @@ top16_attention_split(AttnArgs a) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) w.acc[nt] = f32x4{0, 0, 0, 0};
   w.ok = payload[0] == 5;
+  // this workgroup's share of the order check: entry pairs (i, i + 1) for i in
+  // [first, last), the list split evenly over the sequence's splits * pairs
+  // workgroups
+  bool order_bad = false;
+  {
+    const unsigned int groups = a.splits * pairs, g = split * pairs + hp;
+    const unsigned int chunk = (c.count + groups - 1) / groups;
+    const unsigned int first = min(g * chunk, c.count);
+    const unsigned int last = min(first + chunk, c.count > 0 ? c.count - 1 : 0u);
+    for (unsigned int i = first + tid; i < last; i += kThreads)
+      order_bad |= entry_pos(entries, i + 1) < entry_pos(entries, i);
+  }
   __syncthreads();  // decode tables
 
   // The four waves meet at a barrier after every second step, so that the two
@@ -447,7 +464,7 @@ top16_attention_split(AttnArgs a) {
   const float m_run = w.m_run;
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
-  const bool wave_bad = __ballot(!w.ok) != 0;
+  const bool wave_bad = __ballot(!w.ok || order_bad) != 0;
   if (lane == 0) sBad[wave] = wave_bad ? 1u : 0u;
   __syncthreads();  // every wave is done with its LDS region
   float* sm = reinterpret_cast<float*>(lds);  // [wave][head][kPartial]
@@ -495,11 +512,17 @@ top16_attention_split(AttnArgs a) {
 }
 
 // Merges the splits of one query head: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// A NaN running max in any partial of the sequence (a rejected payload or escape
+// list, flagged by the split kernel) makes the whole output row NaN.
 __global__ __launch_bounds__(kHeadDim) void top16_attention_combine(AttnArgs a) {
   const unsigned int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const unsigned int h = qh / kGroup, g = qh % kGroup;
-  const float* part = a.partial + (((unsigned long long)b * a.kv_heads + h) * a.splits) * kGroup * kPartial +
-                      g * kPartial;
+  const float* seq = a.partial + (unsigned long long)b * a.kv_heads * a.splits * kGroup * kPartial;
+  int flagged = 0;
+  for (unsigned int k = d; k < a.kv_heads * a.splits; k += kHeadDim)
+    flagged |= isnan(seq[(unsigned long long)k * kGroup * kPartial]) ? 1 : 0;
+  const bool bad = __syncthreads_or(flagged) != 0;
+  const float* part = seq + (unsigned long long)h * a.splits * kGroup * kPartial + g * kPartial;
   float big = -INFINITY;
   for (unsigned int s = 0; s < a.splits; ++s) big = fmaxf(big, part[s * kGroup * kPartial]);
   float num = 0.f, den = 0.f;
@@ -511,8 +534,8 @@ __global__ __launch_bounds__(kHeadDim) void top16_attention_combine(AttnArgs a) 
     den += p[1] * wgt;
     num += p[2 + d] * wgt;
   }
-  if (isnan(big)) num = NAN;
-  a.out[((unsigned long long)b * a.q_heads + qh) * kHeadDim + d] = (uint16_t)bf16_bits(num / den);
+  a.out[((unsigned long long)b * a.q_heads + qh) * kHeadDim + d] =
+      (uint16_t)bf16_bits(bad ? NAN : num / den);
 }
 
 }  // namespace
