@@ -278,9 +278,16 @@ def plan_fallbacks(torch, sz, w):
                                          w["device"])
                 offsets, sizes, _ = sub_send.palette_layout(6)
                 cache[over] = {"send": sub_send, "recv": sub_recv, "offsets": offsets,
-                               "sizes": sizes, "workspace": sub_send.new_palette_workspace()}
+                               "sizes": sizes, "workspace": sub_send.new_palette_workspace(),
+                               "presence_first": send.presence_first(over)}
             entry.update(cache[over])
             entry["buffer"] = entry["send"].new_palette_buffer(6)
+            # a layer that overflows is encoded with the presence-mask variant (the
+            # connector's choice for a layer whose Top-16 attempt is a probe after
+            # an overflow), so its fallback needs no presence pass
+            if "presence" not in w:
+                w["presence"] = send.new_presence()
+            entry["presence"] = w["presence"]
         if keep and over:
             key = ("keep", keep)
             if key not in cache:
@@ -290,20 +297,22 @@ def plan_fallbacks(torch, sz, w):
         w["plan"].append(entry)
 
 
-def encode_top16(sz, w, layer):
+def encode_top16(sz, w, layer, presence=None):
     got = sz.encode_top16_paged(w["kv"][layer], w["send"], w["payloads"][layer], w["workspace"],
-                                tables=w["tables"][layer], directory=w["dirs"][layer])
+                                tables=w["tables"][layer], directory=w["dirs"][layer],
+                                presence=presence)
     if got != w["send"].total_encoded_bytes:
         raise RuntimeError(f"layer {layer}: paged encode declined ({got})")
 
 
 def encode_layer(sz, w, layer):
     """Top-16 for every request; fixed6 for the requests whose Top-16 payload overflows."""
-    encode_top16(sz, w, layer)
     plan = w["plan"][layer]
+    encode_top16(sz, w, layer, plan.get("presence"))
     if plan["over"]:
         got = sz.encode_bf16_paged(w["kv"][layer], plan["send"], plan["buffer"],
-                                   plan["workspace"], bits=6)
+                                   plan["workspace"], bits=6, presence=plan["presence"],
+                                   presence_first=plan["presence_first"])
         if got != sum(plan["sizes"]):
             raise RuntimeError(f"layer {layer}: fixed6 fallback encode declined ({got})")
 
@@ -1170,12 +1179,16 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
     cap_bytes = sum(5 * codec_format.top16_escape_capacity(n) for n in send.count_words)
     top16_used = send.total_encoded_bytes - cap_bytes + 5 * escapes / layers
     # algorithmic HBM bytes per call (unused escape slots not counted):
-    # encode reads the raw KV and writes the Top-16 payloads (plus, for overflowed
-    # payloads, the fixed6 presence read, its encode read and its payload write);
+    # encode reads the raw KV and writes the Top-16 payloads (plus, on a layer
+    # that overflows, the tiles' presence masks, and for overflowed payloads the
+    # masks' read, the fixed6 encode read and its payload write);
     # decode reads the final payloads and writes the raw KV
     fallback_raw = sum(send.raw_bytes[r] for plan in w["plan"] for r in plan["over"]) / layers
     fallback_out = sum(sum(plan.get("sizes", [])) for plan in w["plan"]) / layers
-    b_enc = raw_layer + top16_used + 2 * fallback_raw + fallback_out
+    masks = sum(send.presence_bytes() + 32 * sum(2 * -(-(send.count_words[r] // 2) // 4096)
+                                                for r in plan["over"])
+                for plan in w["plan"] if plan["over"]) / layers
+    b_enc = raw_layer + top16_used + fallback_raw + fallback_out + masks
     if overflowed:
         kept_frac = 1 - overflowed / (layers * send.payload_count)
         b_dec = raw_layer + kept_frac * top16_used + fallback_out
@@ -1190,7 +1203,7 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
     kernels = {"encode": "top16_encode_tile+top16_encode_finalize",
                "decode": "top16_decode_tile_dir (escape directory)"}
     if overflowed:
-        kernels = {"encode": "top16 encode + palette_presence/reduce/encode_tile (fixed6)",
+        kernels = {"encode": "top16 encode (presence masks) + palette_reduce/encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
     traffic, traffic_source = (None, None) if overflowed else measured_traffic(name,

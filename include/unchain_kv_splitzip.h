@@ -149,6 +149,31 @@ long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
     unsigned long long directory_ptr, unsigned long long stream_ptr);
 
+/* High-byte presence mask bytes of a batch (no counterpart in the reference): 32
+ * bytes (a 256-bit mask of the high bytes present) per 4096-word tile of each plane
+ * of each payload, payload r's masks after those of payloads 0 .. r-1; 0 when
+ * block_words is not a multiple of 1024. */
+unsigned long long kvq_splitzip_top16_paged_presence_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count);
+
+/* kvq_splitzip_bf16_encode_top16_paged that also writes every tile's high-byte
+ * presence mask to presence_ptr (16-byte aligned, kvq_splitzip_top16_paged_presence_bytes()
+ * bytes; no counterpart in the reference). It is meant for a layer likely to
+ * overflow: the palette fallback of an overflowed payload
+ * (kvq_splitzip_bf16_encode_mode_paged_presence) then starts from the masks instead
+ * of reading the payload's words a third time. Declined (0) under the directory's
+ * conditions and when presence_ptr is 0. */
+long long kvq_splitzip_bf16_encode_top16_paged_presence(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long directory_ptr, unsigned long long presence_ptr,
+    unsigned long long stream_ptr);
+
 /* No counterpart in the reference: kvq_splitzip_bf16_encode_top16_paged for callers
  * that cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments, results and preconditions,
@@ -222,6 +247,21 @@ long long kvq_splitzip_bf16_encode_mode_paged(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long workspace_ptr,
     unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits);
+
+/* kvq_splitzip_bf16_encode_mode_paged with the high-byte presence masks already
+ * known (no counterpart in the reference): payload r's masks, one per 4096-word tile
+ * of each of its planes, start at mask presence_first[r] (a HOST array) of
+ * presence_ptr (a device buffer written by kvq_splitzip_bf16_encode_top16_paged_presence
+ * over the same blocks; 16-byte aligned), so the encode skips its presence pass.
+ * Same results and other preconditions. */
+long long kvq_splitzip_bf16_encode_mode_paged_presence(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long workspace_ptr,
+    unsigned long long workspace_bytes, unsigned long long presence_ptr,
+    const unsigned long long* presence_first, unsigned long long stream_ptr, int bits);
 
 /* Palette decode + scatter of a batch (no counterpart in the reference; it replaces
  * one kvq_splitzip_bf16_decode_fixed6_blocks call per request, and decodes fixed5 on

@@ -132,6 +132,41 @@ def test_top16_overflow_falls_back_to_fixed6_and_backs_off(sz, codebooks):
     assert codec._choose_bits(2, 1 << 20)[0] == BITS_FIXED6
 
 
+def test_probe_after_an_overflow_reencodes_from_presence_masks(sz, codebooks):
+    """Save 1 overflows (fixed6 fallback), save 2 waits out the window (fixed6
+    chosen directly), save 3 probes: the probe's Top-16 encode records presence
+    masks, overflows again, and the fixed6 re-encode starts from the masks. Every
+    fixed6 payload equals the oracle's."""
+    say("connector probe with presence masks")
+    books = codebooks[2 * 32:3 * 32]
+    rng = np.random.default_rng(12)
+    pool = 40
+    words = words_with_books(rng, books, pool, 0.0)
+    # 1.2% escapes (above the 0.5% capacity) over 16 exponents outside the
+    # codebooks, so the high bytes still fit the fixed6 palette
+    outside = np.array(sorted(set(range(256)) - set(books))[:16], np.uint16)
+    hit = rng.random(words.size) < 0.012
+    words[hit] = (words[hit] & 0x807F) | (outside[rng.integers(0, 16, int(hit.sum()))] << 7)
+    table = rng.permutation(pool)[:16].tolist()
+    expect = oracle.fixed6_encode(words.reshape(2, pool, BW)[:, table].reshape(-1))
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    for step, (probe, bits, fallback) in enumerate([(False, BITS_TOP16, True),
+                                                     (False, BITS_FIXED6, False),
+                                                     (True, BITS_TOP16, True)]):
+        kv = layer_from_words(words, pool)
+        pending = codec.save_kv_layer(2, kv, [table])
+        p = pending.payloads[0]
+        assert (p.probe, p.bits) == (probe, bits), step
+        assert (pending.presence is not None) == probe, step
+        assert (p._mask_first == 0) == probe, step
+        payloads = codec.ready(pending)
+        assert pending.presence is None
+        assert payloads[0].bits == BITS_FIXED6 and payloads[0].fallback == fallback, step
+        assert bytes(payloads[0].view) == bytes(expect), step
+    assert trace.names().count("splitzip_top16_probe") == 1
+
+
 def test_fixed6_overflow_falls_back_to_raw_mode(sz, codebooks):
     say("connector fixed6 overflow -> raw")
     rng = np.random.default_rng(3)

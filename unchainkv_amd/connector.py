@@ -136,6 +136,7 @@ class LayerPayload:
     _group: int = -1
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
+    _mask_first: int = -1            # first high-byte presence mask in the layer's masks
 
     def metadata(self, layer_index: int, block_words: int) -> dict:
         """Receiver metadata of a compressed-native layer payload."""
@@ -153,6 +154,7 @@ class PendingLayer:
     groups: list = field(default_factory=list)  # (host tensor, event, device buffer, status)
     slots: list = field(default_factory=list)   # pinned pool buffers behind the host tensors
     started: float = 0.0
+    presence: object = None  # high-byte presence masks of the Top-16 group (probe encodes)
 
 
 class SplitzipLayerCodec:
@@ -277,9 +279,15 @@ class SplitzipLayerCodec:
             raise ValueError("a KV layer is a bf16 (2, num_blocks, ...) paged cache")
         return kv_layer[0, 0].numel()
 
-    def _encode_group(self, kind: int, kv_layer, members: list, block_words: int, layer_index: int):
+    def _encode_group(self, kind: int, kv_layer, members: list, block_words: int, layer_index: int,
+                      pending: PendingLayer | None = None):
         """Batched encode of `members` with codec `kind`; returns (device buffer,
-        offsets, sizes, batch) or None when the library declines."""
+        offsets, sizes, batch) or None when the library declines.
+
+        With `pending`: a Top-16 group that holds a probe (the layer overflowed
+        before, so it may again) also records every tile's high-byte presence
+        mask in ``pending.presence``; a palette group whose members all have masks
+        there starts from them instead of reading the blocks once more."""
         sz = self._lib()
         batch = sz.PagedBatch([p.block_ids for p in members], block_words, kv_layer.device)
         if kind == BITS_TOP16:
@@ -287,11 +295,30 @@ class SplitzipLayerCodec:
             if tables is None:
                 return None
             out = batch.new_payload_buffer()
-            got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(), tables=tables)
+            presence = None
+            if pending is not None and any(p.probe for p in members):
+                presence = batch.new_presence()
+            got = None
+            if presence is not None:
+                got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(),
+                                            tables=tables, presence=presence)
+                if got:
+                    pending.presence = presence
+                    for p, first in zip(members, batch.presence_first(range(len(members)))):
+                        p._mask_first = first
+            if not got:
+                got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(),
+                                            tables=tables)
             return (out, batch.out_offsets, batch.encoded_bytes, batch) if got else None
         offsets, sizes, _ = batch.palette_layout(kind)
         out = batch.new_palette_buffer(kind)
-        got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind)
+        masks = {}
+        if pending is not None and pending.presence is not None and \
+                all(p._mask_first >= 0 for p in members):
+            masks = {"presence": pending.presence,
+                     "presence_first": [p._mask_first for p in members]}
+        got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind,
+                                   **masks)
         return (out, offsets, sizes, batch) if got else None
 
     def _host_buffer(self, nbytes: int, torch):
@@ -450,7 +477,8 @@ class SplitzipLayerCodec:
         top = [p for p in payloads if p.bits == BITS_TOP16]
         if top:
             try:
-                result = self._encode_group(BITS_TOP16, kv_layer, top, block_words, layer_index)
+                result = self._encode_group(BITS_TOP16, kv_layer, top, block_words, layer_index,
+                                            pending)
             except Exception:
                 for p in top:
                     self._cancel_splitzip_top16_probe(layer_index, p.epoch, p.probe)
@@ -531,7 +559,7 @@ class SplitzipLayerCodec:
             self.trace.event("splitzip_fixed5_overflow", layer=layer)
         if overflowed:
             result = self._encode_group(BITS_FIXED6, pending.kv_layer, overflowed,
-                                        pending.block_words, layer)
+                                        pending.block_words, layer, pending)
             if result is not None:
                 out, offsets, sizes, _ = result
                 host = out.cpu()
@@ -549,6 +577,7 @@ class SplitzipLayerCodec:
                 payload[1:] = memoryview(raw.numpy()).cast("B")
                 p.view, p.bits, p.encoded_bytes = memoryview(payload), BITS_RAW, len(payload)
                 self.trace.event("splitzip_fixed6_overflow", layer=layer)
+        pending.presence = None
         self.trace.event("splitzip_payload_ready", layer=layer,
                          raw_bytes=sum(p.raw_bytes for p in pending.payloads),
                          encoded_bytes=sum(p.encoded_bytes for p in pending.payloads))

@@ -38,7 +38,9 @@ struct PayloadDesc {
   unsigned int block_count;       // blocks per plane
   unsigned int tile_begin;        // first tile of this payload within the launch
   unsigned int slot_group_begin;  // first escape-patch workgroup of this payload
+  unsigned int mask_begin;        // palette codecs: first high-byte presence mask
 };
+static_assert(sizeof(PayloadDesc) == 32, "payload descriptor");
 
 // One launch covers up to kMaxPayloads payloads of one paged layer (or one
 // contiguous payload). Word i of a payload lives at
@@ -76,6 +78,11 @@ struct LaunchArgs {
   // tile dir_base[t] = payload slot of the tile's first escape.
   uint32_t* dir_rec;
   uint32_t* dir_base;
+  // 256-bit presence mask of the high bytes of each of the launch's tiles, written
+  // by the Top-16 tile kernel when not null (8 dwords per tile): the palette
+  // fallback encode of an overflowed payload then starts from these masks instead
+  // of reading the words again.
+  uint32_t* presence;
   PayloadDesc p[kMaxPayloads];
 };
 

@@ -123,7 +123,8 @@ __global__ __launch_bounds__(kThreads) void palette_presence_generic(LaunchArgs 
 }
 
 // Per payload: OR of masks [first, first + count) -> PaletteInfo. Masks of payload
-// r start at tile_begin (tile masks) or r * groups (generic masks).
+// r start at mask_begin (one mask per tile: the presence tile kernel's, or the
+// Top-16 tile kernel's) or r * groups (generic masks).
 template <int kBits>
 __global__ __launch_bounds__(kThreads) void palette_reduce(LaunchArgs a, unsigned int groups,
                                                            const unsigned int* masks,
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void palette_reduce(LaunchArgs a, unsigne
   const unsigned int tid = threadIdx.x, r = blockIdx.x;
   const PayloadDesc d = a.p[r];
   const unsigned long long n = payload_words(a, d);
-  const unsigned long long first = groups ? (unsigned long long)r * groups : d.tile_begin;
+  const unsigned long long first = groups ? (unsigned long long)r * groups : d.mask_begin;
   const unsigned long long count = groups ? groups : payload_tiles(a, n);
   if (tid < 8) s_mask[tid] = 0;
   __syncthreads();
@@ -439,12 +440,16 @@ unsigned int tiles_of(unsigned long long n) {
   return 2u * (unsigned int)(((n >> 1) + kTileWords - 1) >> kTileShift);
 }
 
+// masks_given: `masks` already holds one mask per tile of every payload (from the
+// Top-16 encode), at each payload's mask_begin; the presence pass is skipped.
 template <int kBits>
 long long launch_palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
                                 unsigned int presence_groups, PaletteInfo* info,
-                                unsigned int* masks, hipStream_t stream) {
+                                unsigned int* masks, bool masks_given, hipStream_t stream) {
   const dim3 block(kThreads);
-  if (tiles) {
+  if (masks_given) {
+    presence_groups = 0;
+  } else if (tiles) {
     if (a.ids)
       hipLaunchKernelGGL(palette_presence_tile<true>, dim3(a.total_tiles), block, 0, stream, a, g,
                          masks);
@@ -457,7 +462,7 @@ long long launch_palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
   }
   if (long long rc = check("palette_presence")) return rc;
   hipLaunchKernelGGL(palette_reduce<kBits>, dim3(a.payload_count), block, 0, stream, a,
-                     tiles ? 0u : presence_groups, masks, info);
+                     tiles || masks_given ? 0u : presence_groups, masks, info);
   if (long long rc = check("palette_reduce")) return rc;
   if (tiles) {
     if (a.ids)
@@ -493,9 +498,11 @@ long long launch_palette_decode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
 
 long long palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
                          unsigned int presence_groups, PaletteInfo* info, unsigned int* masks,
-                         hipStream_t stream, int bits) {
-  return bits == 6 ? launch_palette_encode<6>(a, g, tiles, presence_groups, info, masks, stream)
-                   : launch_palette_encode<5>(a, g, tiles, presence_groups, info, masks, stream);
+                         hipStream_t stream, int bits, bool masks_given = false) {
+  return bits == 6 ? launch_palette_encode<6>(a, g, tiles, presence_groups, info, masks,
+                                              masks_given, stream)
+                   : launch_palette_encode<5>(a, g, tiles, presence_groups, info, masks,
+                                              masks_given, stream);
 }
 
 long long palette_decode(LaunchArgs& a, const EncodeGeom& g, bool tiles, hipStream_t stream,
@@ -518,6 +525,7 @@ unsigned int fill_batch(LaunchArgs& a, const unsigned long long* block_offsets,
     a.p[k].ids_offset = block_offsets[r];
     a.p[k].block_count = (unsigned int)nblk;
     a.p[k].tile_begin = tiles;
+    a.p[k].mask_begin = tiles;
     tiles += tiles_of(2 * nblk * block_words);
     uniform_size = uniform_size && nblk == block_offsets[first + 1] - block_offsets[first];
   }
@@ -676,18 +684,25 @@ extern "C" unsigned long long kvq_splitzip_palette_paged_workspace_bytes(
   return batch_workspace_bytes(block_offsets, payload_count, block_words);
 }
 
-extern "C" long long kvq_splitzip_bf16_encode_mode_paged(
+namespace {
+
+long long encode_mode_paged_impl(
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long payload_count,
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long workspace_ptr,
-    unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits) {
+    unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits,
+    unsigned long long presence_ptr, const unsigned long long* presence_first) {
   if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || workspace_ptr == 0 ||
       block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 ||
       block_words == 0 || block_words > 0xFFFFFFFFULL || (bits != 5 && bits != 6) ||
-      workspace_ptr % 16 != 0)
+      workspace_ptr % 16 != 0 || presence_ptr % 16 != 0 ||
+      (presence_ptr != 0 && presence_first == nullptr))
     return 0;
+  if (presence_ptr != 0)
+    for (unsigned long long r = 0; r < payload_count; ++r)
+      if (presence_first[r] > 0xFFFFFFFFULL) return 0;
   unsigned long long total = 0, max_plane = 0;
   bool aligned = true;
   std::vector<std::pair<unsigned long long, unsigned long long>> spans;
@@ -723,12 +738,46 @@ extern "C" long long kvq_splitzip_bf16_encode_mode_paged(
     fill_batch(a, block_offsets, out_offsets, first, count, block_words);
     PaletteInfo* info = reinterpret_cast<PaletteInfo*>(ws);
     unsigned int* masks = reinterpret_cast<unsigned int*>(info + count);
-    const long long rc = palette_encode(a, g, tiles, kGenericGroups, info, masks, stream, bits);
+    if (presence_ptr != 0) {
+      masks = reinterpret_cast<unsigned int*>(presence_ptr);
+      for (unsigned int k = 0; k < count; ++k) a.p[k].mask_begin = (unsigned int)presence_first[first + k];
+    }
+    const long long rc =
+        palette_encode(a, g, tiles, kGenericGroups, info, masks, stream, bits, presence_ptr != 0);
     if (rc < 0) return rc;
     ws += count * sizeof(PaletteInfo) +
           32 * std::max<unsigned long long>(a.total_tiles, (unsigned long long)count * kGenericGroups);
   }
   return (long long)total;
+}
+
+}  // namespace
+
+extern "C" long long kvq_splitzip_bf16_encode_mode_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long workspace_ptr,
+    unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits) {
+  return encode_mode_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                block_offsets, payload_count, out_ptr, out_offsets, out_capacity,
+                                workspace_ptr, workspace_bytes, stream_ptr, bits, 0, nullptr);
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_mode_paged_presence(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long workspace_ptr,
+    unsigned long long workspace_bytes, unsigned long long presence_ptr,
+    const unsigned long long* presence_first, unsigned long long stream_ptr, int bits) {
+  if (presence_ptr == 0) return 0;
+  return encode_mode_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                block_offsets, payload_count, out_ptr, out_offsets, out_capacity,
+                                workspace_ptr, workspace_bytes, stream_ptr, bits, presence_ptr,
+                                presence_first);
 }
 
 extern "C" long long kvq_splitzip_bf16_decode_mode_paged(

@@ -608,10 +608,14 @@ __device__ __forceinline__ void zero_escape_span(unsigned char* payload, unsigne
   zero_fill(payload + 5 + n + (n + 1) / 2 + lo, hi - lo);
 }
 
-template <bool kIds>
+// kSeen: also writes the tile's high-byte presence mask to a.presence (the
+// variant for a layer likely to overflow, whose palette fallback then needs no
+// presence pass of its own).
+template <bool kIds, bool kSeen>
 __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
   __shared__ uint32_t s_tab[64];  // this tile's plane, 4 code bytes per dword
   __shared__ unsigned int s_wave[kThreads / kWave];
+  __shared__ uint32_t s_seen[kSeen ? 64 : 1];  // one byte per high byte value
   const unsigned int tid = threadIdx.x;
   const unsigned int lane = tid & (kWave - 1);
   const unsigned int wave = uniform(tid >> 6);
@@ -632,14 +636,24 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
 #pragma unroll
     for (int q = 0; q < 8; ++q) x[q] = 0;
   }
-  if (tid < 64)
+  if (tid < 64) {
     s_tab[tid] = pack_codes4(reinterpret_cast<const uint32_t*>(a.tables + t.plane * 256)[tid]);
+    if (kSeen) s_seen[tid] = 0;
+  }
   __syncthreads();  // s_tab ready
   const unsigned char* tab = reinterpret_cast<const unsigned char*>(s_tab);
 
   uint32_t body_a[2], body_b[2], code_a, code_b, mask_a, mask_b;
   encode_run8(x, tab, body_a, code_a, mask_a);
   encode_run8(x + 4, tab, body_b, code_b, mask_b);
+  if (kSeen && active) {
+    unsigned char* seen = reinterpret_cast<unsigned char*>(s_seen);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      seen[(x[k] >> 8) & 0xFF] = 1;
+      seen[x[k] >> 24] = 1;
+    }
+  }
   if (active) {
     unsigned char* pbody = t.payload + 5 + wstart;
     unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
@@ -669,6 +683,15 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
   const unsigned int wave_a = wave_tot & 0xFFFFu;
   if (lane == 0) s_wave[wave] = wave_a + (wave_tot >> 16);
   __syncthreads();
+  if (kSeen) {
+    // wave w reports high bytes 64w .. 64w + 63
+    const unsigned long long bits =
+        __ballot(reinterpret_cast<const unsigned char*>(s_seen)[tid] != 0);
+    if (lane == 0) {
+      a.presence[8ull * tile + 2 * wave] = (uint32_t)bits;
+      a.presence[8ull * tile + 2 * wave + 1] = (uint32_t)(bits >> 32);
+    }
+  }
   unsigned int before = 0, total = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / kWave; ++w) {
@@ -908,6 +931,9 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups];
   __shared__ unsigned int s_over_base[kFinChunk / kFinGroups];
   __shared__ unsigned int s_over_count;
+  __shared__ unsigned int s_dense_tile[kFinChunk / kFinGroups];  // tile | escapes << 24
+  __shared__ unsigned int s_dense_base[kFinChunk / kFinGroups];
+  __shared__ unsigned int s_dense_count;
   __shared__ unsigned int s_wave[kThreads / kWave];
   __shared__ unsigned char s_tab[512];
   const unsigned int tid = threadIdx.x;
@@ -945,7 +971,10 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
   // escapes sit in its own body bytes (u32 count, then the entries; tiles of at
   // least 64 words)
   const unsigned int inbody = kInBody ? a.inbody_slots : 0u;
-  if (tid == 0) s_over_count = 0;  // ordered by the barriers of the first scan
+  if (tid == 0) {  // ordered by the barriers of the first scan
+    s_over_count = 0;
+    s_dense_count = 0;
+  }
 
   unsigned long long running = 0;  // escapes in earlier chunks
   for (unsigned int chunk0 = 0; chunk0 < tiles; chunk0 += kFinChunk) {
@@ -1008,6 +1037,14 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
         const unsigned int q = atomicAdd(&s_over_count, 1u);
         s_over_tile[q] = chunk0 + own;
         s_over_base[q] = (unsigned int)base;
+      } else if (c > (unsigned int)kFinPreload) {
+        // more than the preloaded batch (dense escapes, e.g. outliers): placed
+        // below by a whole wave, one entry per lane, instead of batch after
+        // batch of dependent loads by this thread (c <= kStageSlots < 2^8,
+        // chunk tiles < 2^24)
+        const unsigned int q = atomicAdd(&s_dense_count, 1u);
+        s_dense_tile[q] = own | (c << 24);
+        s_dense_base[q] = (unsigned int)base;
       } else {
         unsigned long long start, end;
         tile_range(a, d, chunk0 + own, n, start, end);
@@ -1030,6 +1067,41 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       }
     }
     __syncthreads();
+    // dense tiles: wave w places the entries of list items w, w + 4, ...; two items
+    // per pass so that their loads are in flight together
+    const unsigned int dense = s_dense_count;
+    for (unsigned int i0 = uniform(tid >> 6); i0 < dense; i0 += 2 * (kThreads / kWave)) {
+      const unsigned int lane = tid & (kWave - 1);
+      unsigned int v[2][kStageSlots / kWave], tile[2], cnt[2];
+      unsigned long long start[2], bases[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const unsigned int i = min(i0 + h * (kThreads / kWave), dense - 1);
+        const unsigned int packed = s_dense_tile[i];
+        tile[h] = chunk0 + (packed & 0xFFFFFFu);
+        cnt[h] = i0 + h * (kThreads / kWave) < dense ? packed >> 24 : 0u;
+        bases[h] = s_dense_base[i];
+        unsigned long long end;
+        tile_range(a, d, tile[h], n, start[h], end);
+        const unsigned int* tst = staged + (unsigned long long)tile[h] * kStageSlots;
+        const unsigned char* tbody = nullptr;
+        if (kInBody) tbody = payload + 5 + start[h] + 4;
+#pragma unroll
+        for (int k = 0; k < kStageSlots / kWave; ++k) {
+          const unsigned int q = min(lane + k * kWave, cnt[h] > 0 ? cnt[h] - 1 : 0u);
+          v[h][k] = kInBody ? *reinterpret_cast<const u32_unaligned*>(tbody + 4 * q) : tst[q];
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int k = 0; k < kStageSlots / kWave; ++k) {
+          const unsigned int q = lane + k * kWave;
+          if (q < cnt[h] && bases[h] + q < cap)
+            put_entry(entries, bases[h] + q, (unsigned int)(start[h] + (v[h][k] >> 8)),
+                      v[h][k] & 0xFF);
+        }
+    }
     // tiles with more escapes than were staged are scanned again from the source
     const unsigned int over = s_over_count;
     if (over) {
@@ -1040,7 +1112,10 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
     }
     running += chunk_total;
     __syncthreads();
-    if (tid == 0) s_over_count = 0;
+    if (tid == 0) {
+      s_over_count = 0;
+      s_dense_count = 0;
+    }
   }
 
   // unused escape slots were zeroed by the tile kernel
@@ -1220,10 +1295,20 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   }
   switch (p.kernel) {
     case Kernel::kTile:
-      if (a.ids)
-        hipLaunchKernelGGL(top16_encode_tile<true>, dim3(a.total_tiles), block, 0, stream, a, g);
-      else
-        hipLaunchKernelGGL(top16_encode_tile<false>, dim3(a.total_tiles), block, 0, stream, a, g);
+      if (a.presence) {
+        if (a.ids)
+          hipLaunchKernelGGL((top16_encode_tile<true, true>), dim3(a.total_tiles), block, 0,
+                             stream, a, g);
+        else
+          hipLaunchKernelGGL((top16_encode_tile<false, true>), dim3(a.total_tiles), block, 0,
+                             stream, a, g);
+      } else if (a.ids) {
+        hipLaunchKernelGGL((top16_encode_tile<true, false>), dim3(a.total_tiles), block, 0,
+                           stream, a, g);
+      } else {
+        hipLaunchKernelGGL((top16_encode_tile<false, false>), dim3(a.total_tiles), block, 0,
+                           stream, a, g);
+      }
       break;
     case Kernel::kLanes:
       hipLaunchKernelGGL((top16_encode_lanes<true, false>), dim3(a.total_tiles), block, 0, stream,
@@ -1551,7 +1636,8 @@ long long encode_top16_paged_impl(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
-    unsigned long long directory_ptr, unsigned long long stream_ptr) {
+    unsigned long long directory_ptr, unsigned long long presence_ptr,
+    unsigned long long stream_ptr) {
   if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || tables_ptr == 0 || workspace_ptr == 0 ||
       block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 || block_words == 0 ||
       block_words > 0xFFFFFFFFULL)
@@ -1584,10 +1670,11 @@ long long encode_top16_paged_impl(
   const unsigned long long dir_tiles =
       kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count) /
       kDirBytesPerTile;
-  // a directory is written by the tile kernels only
+  // a directory and presence masks are written by the tile kernels only
   if (directory_ptr != 0 && (plan.kernel != Kernel::kTile || directory_ptr % 16 != 0 ||
                              dir_tiles == 0))
     return 0;
+  if (presence_ptr != 0 && (plan.kernel != Kernel::kTile || presence_ptr % 16 != 0)) return 0;
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned int* ws = reinterpret_cast<unsigned int*>(workspace_ptr);
@@ -1607,6 +1694,7 @@ long long encode_top16_paged_impl(
     const unsigned int tiles = fill_descs(a, pg, block_offsets, out_offsets, first, count, plan);
     a.workspace = ws;
     set_directory(a, directory_ptr, dir_tiles, tile_offset);
+    if (presence_ptr) a.presence = reinterpret_cast<uint32_t*>(presence_ptr) + 8 * tile_offset;
     long long rc = launch_encode(a, g, plan, stream);
     if (rc < 0) return rc;
     ws += workspace_words(tiles);
@@ -1671,7 +1759,36 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged(
   return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
                                  block_offsets, payload_count, out_ptr, out_offsets,
                                  out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
-                                 directory_ptr, stream_ptr);
+                                 directory_ptr, 0, stream_ptr);
+}
+
+extern "C" unsigned long long kvq_splitzip_top16_paged_presence_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count) {
+  if (block_offsets == nullptr || block_words == 0 || block_words % 1024 != 0) return 0;
+  unsigned long long tiles = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+    tiles += host_payload_tiles(2 * (block_offsets[r + 1] - block_offsets[r]) * block_words, true,
+                                kTileShift);
+  }
+  return 32 * tiles;
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_top16_paged_presence(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long directory_ptr, unsigned long long presence_ptr,
+    unsigned long long stream_ptr) {
+  if (presence_ptr == 0) return 0;
+  return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                 block_offsets, payload_count, out_ptr, out_offsets,
+                                 out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
+                                 directory_ptr, presence_ptr, stream_ptr);
 }
 
 extern "C" unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes() {
@@ -1699,7 +1816,7 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
   return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
                                  block_offsets, payload_count, out_ptr, out_offsets,
                                  out_capacity, tables_ptr, ws, kStaticScratchBytes,
-                                 directory_ptr, stream_ptr);
+                                 directory_ptr, 0, stream_ptr);
 }
 
 // Decodes payload r (src + src_offsets[r], encoded_bytes[r] long) and scatters it

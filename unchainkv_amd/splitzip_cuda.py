@@ -52,6 +52,7 @@ _SIGNATURES = (
     ("kvq_splitzip_last_error", [], ctypes.c_char_p, True),
     ("kvq_splitzip_top16_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
     ("kvq_splitzip_top16_paged_directory_bytes", [_U64, _U64P, _U64], _U64, False),
+    ("kvq_splitzip_top16_paged_presence_bytes", [_U64, _U64P, _U64], _U64, False),
     (
         "kvq_splitzip_top16_build_directory",
         [ctypes.c_void_p, _U64P, _U64P, _U64, _U64, _U64P, ctypes.c_void_p, _U64],
@@ -62,6 +63,13 @@ _SIGNATURES = (
         "kvq_splitzip_bf16_encode_top16_paged",
         [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64,
          _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_encode_top16_paged_presence",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64,
+         _U64, _U64],
         ctypes.c_longlong,
         False,
     ),
@@ -99,6 +107,13 @@ _SIGNATURES = (
         "kvq_splitzip_bf16_encode_mode_paged",
         [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64,
          ctypes.c_int],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_encode_mode_paged_presence",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64P,
+         _U64, ctypes.c_int],
         ctypes.c_longlong,
         False,
     ),
@@ -496,6 +511,32 @@ class PagedBatch:
         size = self.directory_bytes()
         return torch.empty(size, dtype=torch.uint8, device=self.device) if size else None
 
+    def presence_bytes(self) -> int:
+        """Bytes of the batch's high-byte presence masks (32 per 4096-word tile of
+        each plane; 0 when block words are not a multiple of 1024)."""
+        lib = _load()
+        query = getattr(lib, "kvq_splitzip_top16_paged_presence_bytes", None) if lib else None
+        if query is None:
+            raise RuntimeError(f"splitzip HIP library unavailable: {load_error()}")
+        return int(query(self.block_words, self._block_offsets, self.payload_count))
+
+    def new_presence(self, torch=None):
+        """Device buffer for the presence masks, or None when the batch has none."""
+        if torch is None:
+            import torch
+        size = self.presence_bytes()
+        return torch.empty(size, dtype=torch.uint8, device=self.device) if size else None
+
+    def presence_first(self, members) -> list[int]:
+        """Index of the first presence mask of each request in ``members`` (masks
+        of request r follow those of requests 0 .. r-1, one per 4096-word tile of
+        each plane)."""
+        firsts, at = [], 0
+        for n in self.count_words:
+            firsts.append(at)
+            at += 2 * (-(-(n // 2) // 4096))
+        return [firsts[r] for r in members]
+
     def payload(self, out, r: int):
         return out[self.out_offsets[r]:self.out_offsets[r] + self.encoded_bytes[r]]
 
@@ -567,15 +608,18 @@ def _directory_ptr(directory, batch: PagedBatch, torch) -> int | None:
 
 def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index: int = -1, *,
                        codebooks: bytes | None = None, tables=None,
-                       directory=None) -> int | None:
+                       directory=None, presence=None) -> int | None:
     """Gather + Top-16 encode every request of ``batch`` from one paged layer
     ``(2, num_blocks, ...)`` into ``out`` (a ``batch.out_bytes`` uint8 buffer).
     With ``directory`` (``batch.new_directory()``) the encoder also writes the
     escape directory that lets ``decode_top16_paged`` apply escapes without a
-    second pass. Returns the total encoded bytes or ``None`` when the codec
-    declines."""
+    second pass; with ``presence`` (``batch.new_presence()``) it writes the
+    high-byte presence masks that let ``encode_bf16_paged`` re-encode an
+    overflowed request without a presence pass. Returns the total encoded bytes
+    or ``None`` when the codec declines."""
     lib = _load()
-    encode = getattr(lib, "kvq_splitzip_bf16_encode_top16_paged", None) if lib else None
+    name = "kvq_splitzip_bf16_encode_top16_paged" + ("_presence" if presence is not None else "")
+    encode = getattr(lib, name, None) if lib else None
     if encode is None:
         return None
     import torch
@@ -589,12 +633,19 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
     dir_ptr = _directory_ptr(directory, batch, torch)
     if tables is None or dir_ptr is None:
         return None
+    extra = ()
+    if presence is not None:
+        if presence.dtype != torch.uint8 or not presence.is_contiguous() or \
+                presence.device != kv_layer.device or presence.numel() < batch.presence_bytes() \
+                or batch.presence_bytes() == 0:
+            return None
+        extra = (int(presence.data_ptr()),)
     stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), batch._out_offsets,
                      int(out.numel()), int(tables.data_ptr()), int(workspace.data_ptr()),
-                     int(workspace.numel()), dir_ptr, int(stream))
+                     int(workspace.numel()), dir_ptr, *extra, int(stream))
     if encoded < 0:
         _raise_last(lib, "splitzip top16 paged encode failed")
     return int(encoded) or None
@@ -712,14 +763,22 @@ def build_directory(host_payloads, src_offsets, encoded_bytes, batch: PagedBatch
 # ---------------------------------------------------------------------------
 # batched paged fixed6 / fixed5 (the Top-16 overflow fallback, one launch per layer)
 
-def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6) -> int | None:
+def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6, *,
+                      presence=None, presence_first=None) -> int | None:
     """Gather + fixed6 (bits 6) or fixed5 (bits 5) encode of every request of
     ``batch``; payload r goes to ``batch.palette_layout(bits)[0][r]`` of ``out``.
-    Returns the total encoded bytes or ``None`` when the codec declines."""
+    ``presence`` / ``presence_first``: the high-byte presence masks a Top-16
+    encode of the same blocks wrote (``encode_top16_paged(presence=...)``) and the
+    index of request r's first mask there (``PagedBatch.presence_first`` of that
+    batch); the encode then skips its own presence pass. Returns the total
+    encoded bytes or ``None`` when the codec declines."""
     if bits not in {5, 6}:
         raise ValueError("splitzip bf16 bits must be 5 or 6")
+    if (presence is None) != (presence_first is None):
+        raise ValueError("presence and presence_first go together")
     lib = _load()
-    encode = getattr(lib, "kvq_splitzip_bf16_encode_mode_paged", None) if lib else None
+    name = "kvq_splitzip_bf16_encode_mode_paged" + ("_presence" if presence is not None else "")
+    encode = getattr(lib, name, None) if lib else None
     if encode is None:
         return None
     import torch
@@ -730,11 +789,23 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
         return None
     batch.palette_layout(bits)
     offs = batch._palette[bits][3]
+    extra = ()
+    if presence is not None:
+        if presence.dtype != torch.uint8 or not presence.is_contiguous() or \
+                presence.device != kv_layer.device or len(presence_first) != batch.payload_count:
+            return None
+        # every request's masks must lie inside the buffer
+        for first, n in zip(presence_first, batch.count_words):
+            if first < 0 or 32 * (first + 2 * (-(-(n // 2) // 4096))) > presence.numel():
+                return None
+        extra = (int(presence.data_ptr()),
+                 (ctypes.c_ulonglong * batch.payload_count)(*map(int, presence_first)))
     stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
                      batch.payload_count, int(out.data_ptr()), offs, int(out.numel()),
-                     int(workspace.data_ptr()), int(workspace.numel()), int(stream), int(bits))
+                     int(workspace.data_ptr()), int(workspace.numel()), *extra, int(stream),
+                     int(bits))
     if encoded < 0:
         _raise_last(lib, "splitzip palette paged encode failed")
     return int(encoded) or None
