@@ -289,10 +289,30 @@ def test_layer_travels_in_compressed_native_frames(sz, codebooks):
 # ---------------------------------------------------------------------------
 # payload staging: copy stream and pinned pool (vllm_connector.py:3406-3458)
 
+def _independent_stream(copy, candidates):
+    """A candidate stream whose work is not held back by work on `copy`. HIP
+    multiplexes a process's streams over a few hardware queues
+    (GPU_MAX_HW_QUEUES), and two streams on one queue run in submission order; a
+    spin on `copy` that outlasts a marker on the candidate shows separate queues."""
+    for s in candidates:
+        with torch.cuda.stream(copy):
+            torch.cuda._sleep(50_000_000)  # tens of milliseconds
+        marker = torch.cuda.Event()
+        marker.record(s)
+        while not marker.query():
+            pass
+        free = not copy.query()
+        copy.synchronize()
+        if free:
+            return s
+    return None
+
+
 def test_payload_copy_runs_beside_the_forward_stream(sz, codebooks):
     """A kernel queued on the forward stream right after save_kv_layer finishes
     while the layer's device-to-host copy is still running: the copy is on its own
-    stream. The payloads still arrive whole."""
+    stream, which waits for the forward stream but holds nothing queued on it
+    later. The payloads still arrive whole."""
     say("connector staging overlap")
     books = codebooks[3 * 32:4 * 32]
     rng = np.random.default_rng(12)
@@ -300,11 +320,17 @@ def test_payload_copy_runs_beside_the_forward_stream(sz, codebooks):
     kv = layer_from_words(words_with_books(rng, books, pool, 0.0005), pool)
     tables = disjoint_tables(rng, pool, [256, 256, 256, 256])  # ~50 MB of payloads
     codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False))
+    copy = codec.copy_streams.get(kv.device, torch)
+    forward = _independent_stream(copy, [torch.cuda.Stream() for _ in range(4)])
+    assert forward is not None, "every candidate stream shares the copy stream's queue"
     torch.cuda.synchronize()
-    pending = codec.save_kv_layer(3, kv, tables)
-    marker = torch.cuda.Event()
-    marker.record(torch.cuda.current_stream())   # forward work after the save hook
-    marker.synchronize()
+    with torch.cuda.stream(forward):
+        pending = codec.save_kv_layer(3, kv, tables)
+        marker = torch.cuda.Event()
+        marker.record(forward)                    # forward work after the save hook
+    # poll without sleeping: a blocking synchronize may wake the host late
+    while not marker.query():
+        pass
     copies = [event for _, event, _, _ in pending.groups]
     assert copies and not all(event.query() for event in copies)
     payloads = codec.ready(pending)

@@ -74,9 +74,10 @@ typedef unsigned int u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 // kAligned: both runs start 16-byte aligned, a run holds a multiple of 16 bytes
 // (a lane's 16 destination bytes never straddle the two runs) and every payload
 // has at least 20 bytes. A lane
-// moves chunks base + k * 4 KiB (k < 4) of its workgroup's 16 KiB: every load of
-// the workgroup is issued before the first store, so a resident workgroup keeps
-// 16 KiB in flight.
+// moves chunks base + k * 4 KiB (k < 4) of its workgroup's 16 KiB: chunk 0 is
+// loaded together with the mode byte, chunks 1-3 once the mode byte has shown a
+// payload to move (an overflowed payload costs a quarter of its bytes in reads,
+// not all of them), and every load is issued before the first store.
 template <bool kAligned>
 __global__ __launch_bounds__(kThreads) void top16_writeback(WbArgs a) {
   const unsigned int g = group_index();
@@ -98,17 +99,19 @@ __global__ __launch_bounds__(kThreads) void top16_writeback(WbArgs a) {
   const unsigned int sh = (unsigned int)(reinterpret_cast<uintptr_t>(d.src) & 3);
   u32x4_a4 lo[kWbChunks];
   uint32_t hi[kWbChunks];
-  if (kAligned) {
-#pragma unroll
-    for (int k = 0; k < kWbChunks; ++k) {
-      const unsigned long long c = base + (unsigned long long)k * kWbSpan;
-      const unsigned char* w = d.src + (c + 20 <= d.bytes ? c : 0) - sh;
-      lo[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(w));
-      hi[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + 16));
-    }
-  }
+  auto load_chunk = [&](int k) {
+    const unsigned long long c = base + (unsigned long long)k * kWbSpan;
+    const unsigned char* w = d.src + (c + 20 <= d.bytes ? c : 0) - sh;
+    lo[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(w));
+    hi[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + 16));
+  };
+  if (kAligned) load_chunk(0);
   if (g == d.group_begin && threadIdx.x == 0) a.status[r] = (unsigned char)mode;
   if (mode != kModeTop16) return;
+  if (kAligned) {
+#pragma unroll
+    for (int k = 1; k < kWbChunks; ++k) load_chunk(k);
+  }
 #pragma unroll
   for (int k = 0; k < kWbChunks; ++k) {
     const unsigned long long c = base + (unsigned long long)k * kWbSpan;
