@@ -8,13 +8,18 @@
 // straight from the cache (no gather copy).
 //
 // Two kernels, no global atomics, deterministic output:
-//   exponent_hist_partial: each wave streams batches of twelve 1024-word chunks,
-//     two batches in flight (block ids fetched a batch ahead), and adds every
-//     word's exponent into the workgroup's LDS histogram. Lane l of every wave counts into copy l of the
-//     histogram, two 16-bit bins per dword, laid out so that copy l sits in bank
-//     l: an LDS atomic instruction never has two lanes on one bank (a bf16 plane
-//     concentrates on ~16 exponents, and colliding LDS atomics serialise). The
-//     workgroup then writes one 512-bin partial (K bins, then V bins).
+//   exponent_hist_partial: 512-thread workgroups, about one per CU; each wave
+//     streams batches of four 1024-word chunks, two batches in flight (block ids
+//     fetched a batch ahead), eight batches per wave, and adds every word's
+//     exponent into the workgroup's LDS histogram. Lane l counts into copy l % 16
+//     of the histogram, two 16-bit bins per dword, copy c in bank c: of the 32
+//     lanes an LDS instruction serves at once only lanes l and l + 16 can meet on
+//     one address (a bf16 plane concentrates on ~16 exponents, and colliding LDS
+//     atomics serialise). A chunk's 16 addresses per lane are computed before its
+//     16 LDS adds, so the adds go out back to back. The 16 KiB histogram leaves
+//     the CU's LDS and registers to deep streaming (Llama-3-8B layer: 64 copies
+//     and twelve-chunk batches 42.2 us, this layout 28.2 us). The workgroup then
+//     writes one 512-bin partial (K bins, then V bins).
 //   exponent_hist_reduce: sums the partials into 64-bit counts, every bin's
 //     groups split over sixteen threads.
 // Layouts that the chunk kernel cannot take (block words not a multiple of 1024,
@@ -23,6 +28,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <mutex>
 
 #include "splitzip_common.h"
 
@@ -30,16 +36,16 @@ namespace unchainkv {
 namespace {
 
 constexpr int kBins = 256;
-constexpr int kCopies = 64;                    // one per lane
+constexpr int kCopies = 16;                    // lane l counts into copy l % 16
 // 16-bit counters: a workgroup counts at most kCopies * 65535 words
 constexpr int kChunk = 1024;                   // words per wave step (one block)
 constexpr unsigned int kMaxPartials = 2048;    // workgroups of the partial kernel
 
-// Chunks per wave step: 24 KiB of loads per wave, two steps (48 KiB) in flight.
-// The kernel runs two waves per SIMD (64 KiB of LDS histogram per workgroup), so
-// the loads in flight per wave set its rate (16 chunks per step would need more
-// than the 256 VGPRs a wave has at that occupancy).
-constexpr int kBatch = 12;
+// Chunks per wave step: 8 KiB of loads per wave, two steps in flight.
+constexpr int kBatch = 4;
+// Threads of a partial-kernel workgroup and wave steps per wave (the grid size).
+constexpr int kHistThreads = 512;
+constexpr int kBatchesPerWave = 8;
 
 struct HistArgs {
   const uint16_t* kv;
@@ -52,7 +58,8 @@ struct HistArgs {
 };
 
 constexpr unsigned long long kMaxWordsPerGroup = (unsigned long long)kCopies * 65535;
-constexpr int kHistWords = kBins * kCopies;     // dwords: 2 planes x 256 bins / 2 per dword
+constexpr int kHistWords = kBins * kCopies;     // dwords: 2 planes x 256 bins / 2 per dword,
+                                                // per copy
 
 // LDS histogram of a workgroup: dword [plane][bin / 2][copy], bin parity selects
 // the 16-bit half.
@@ -63,15 +70,16 @@ __device__ __forceinline__ void add_word(unsigned int* h, unsigned int plane, ui
 }
 
 __device__ __forceinline__ void zero_hist(unsigned int* h) {
-  for (unsigned int i = threadIdx.x; i < kHistWords; i += kThreads) h[i] = 0;
+  for (unsigned int i = threadIdx.x; i < kHistWords; i += blockDim.x) h[i] = 0;
   __syncthreads();
 }
 
-// Sums the copies of every bin and writes the workgroup's partial: thread t sums
-// the bin pair t (both halves of the 64 copies' dwords).
+// Sums the copies of every bin and writes the workgroup's partial: thread t < 256
+// sums the bin pair t (both halves of the copies' dwords).
 __device__ __forceinline__ void write_partial(const unsigned int* h, unsigned int* partial) {
   __syncthreads();
   const unsigned int pair = threadIdx.x;  // 256 pairs = 512 bins
+  if (pair >= kBins) return;
   unsigned int lo = 0, hi = 0;
 #pragma unroll 8
   for (int c = 0; c < kCopies; ++c) {
@@ -141,24 +149,29 @@ __device__ __forceinline__ void count_batch(unsigned int* h, const Batch& r, uns
     const unsigned int plane = c >= chunks_per_plane ? 1u : 0u;
     const u32x4 x0 = r.d[2 * k], x1 = r.d[2 * k + 1];
     const uint32_t x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    // every address and increment first, then the 16 LDS adds
+    unsigned int addr[16], inc[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      add_word(h, plane, x[q], copy);
-      add_word(h, plane, x[q] >> 16, copy);
+    for (int q = 0; q < 16; ++q) {
+      const unsigned int bin = (x[q >> 1] >> (7 + 16 * (q & 1))) & 0xFFu;
+      addr[q] = (plane * (kBins / 2) + (bin >> 1)) * kCopies + copy;
+      inc[q] = 1u << (16 * (bin & 1));
     }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) atomicAdd(&h[addr[q]], inc[q]);
   }
 }
 
-__global__ __launch_bounds__(kThreads) void exponent_hist_partial(HistArgs a) {
+__global__ __launch_bounds__(kHistThreads) void exponent_hist_partial(HistArgs a) {
   __shared__ unsigned int h[kHistWords];
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = uniform(threadIdx.x / kWave);
   zero_hist(h);
-  const unsigned int copy = lane;
+  const unsigned int copy = lane % kCopies;
   const unsigned int total = 2 * a.chunks_per_plane;
   const unsigned int batches = (total + kBatch - 1) / kBatch;
-  const unsigned int stride = gridDim.x * (kThreads / kWave);
-  unsigned int b0 = blockIdx.x * (kThreads / kWave) + wave;
+  const unsigned int stride = gridDim.x * (kHistThreads / kWave);
+  unsigned int b0 = blockIdx.x * (kHistThreads / kWave) + wave;
   if (b0 < batches) {
     // Two batches in flight, in two buffers used in turn (a copy from one to the
     // other would wait for its loads). The block ids of a batch are loaded one
@@ -203,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_generic(HistArgs a) {
     const unsigned long long within = in_plane - j * a.block_words;
     const uint32_t w = a.kv[plane * a.plane_stride + (unsigned long long)a.ids[j] * a.block_stride +
                             within];
-    add_word(h, plane, w, lane);
+    add_word(h, plane, w, lane % kCopies);
   }
   write_partial(h, a.partial);
 }
@@ -239,18 +252,38 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_reduce(const unsigned 
   }
 }
 
+// Compute units of the current device, cached per device.
+unsigned long long device_cus() {
+  static std::mutex mu;
+  static unsigned long long cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = (unsigned long long)cus;
+  }
+  return cached[dev];
+}
+
 unsigned int partial_groups(unsigned long long block_count, unsigned long long block_words,
                             bool chunked) {
   const unsigned long long words = 2 * block_count * block_words;
   unsigned long long g;
   if (chunked) {
-    // about four batches per wave (per-layer call, Llama-3-8B: 2 -> 42.7 us,
-    // 4 -> 41.2, 8 -> 47.4; Llama-3-70B TP8: 1 -> 68.9, 2 -> 56.2, 4 -> 48.7,
-    // 8 -> 51.9), but a small layer still spreads over up to 64 workgroups, one
-    // batch per wave
+    // about eight batches per wave (per-layer call, Llama-3-8B: 4 -> 30.1 us,
+    // 8 -> 28.2, 16 -> 42.4 with too few workgroups to fill the GPU), rounded to
+    // whole rounds of one workgroup per CU (Llama-3-70B TP8 layer: 381 workgroups
+    // 48.9 us, 256 40.4 us, 512 41.8 us); a small layer still spreads over up to
+    // 64 workgroups, one batch per wave
     const unsigned long long batches = (words / kChunk + kBatch - 1) / kBatch;
-    const unsigned long long waves = kThreads / kWave;
-    g = (batches + 4 * waves - 1) / (4 * waves);
+    const unsigned long long waves = kHistThreads / kWave;
+    g = (batches + kBatchesPerWave * waves - 1) / (kBatchesPerWave * waves);
+    const unsigned long long cus = device_cus();
+    if (2 * g >= cus) g = std::max(1ull, (g + cus / 2) / cus) * cus;
     const unsigned long long spread = (batches + waves - 1) / waves;
     const unsigned long long floor_g = spread < 64 ? spread : 64;
     if (g < floor_g) g = floor_g;
@@ -327,7 +360,7 @@ extern "C" long long kvq_splitzip_exponent_histogram_paged(
   const unsigned int groups = partial_groups(block_count, block_words, chunked);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   if (chunked)
-    hipLaunchKernelGGL(exponent_hist_partial, dim3(groups), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(exponent_hist_partial, dim3(groups), dim3(kHistThreads), 0, stream, a);
   else
     hipLaunchKernelGGL(exponent_hist_generic, dim3(groups), dim3(kThreads), 0, stream, a);
   hipError_t st = hipGetLastError();
