@@ -338,10 +338,13 @@ def fit_top16_py(histogram) -> list[int] | None:
 
 
 def default_threads() -> int:
+    """Threads for the oracle's multi-threaded calls: the cores this process may
+    run on, at most 16 (one GPU's share of an 8-GPU node's cores)."""
     try:
-        return len(os.sched_getaffinity(0))
+        cores = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        return os.cpu_count() or 1
+        cores = os.cpu_count() or 1
+    return max(1, min(cores, 16))
 
 
 # ---------------------------------------------------------------------------

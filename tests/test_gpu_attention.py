@@ -209,18 +209,22 @@ def test_unordered_escape_list_gives_nan_for_every_head_of_that_sequence(sz, cod
     assert torch.isfinite(out[0]).all() and torch.isfinite(out[2]).all()
 
 
-def test_llama3_8b_decode_step_against_decode_then_attend(sz):
+@pytest.mark.parametrize("outliers", [0.0, 0.001])
+def test_llama3_8b_decode_step_against_decode_then_attend(sz, outliers):
     """Llama-3-8B GQA (32 q heads, 8 kv heads), batch 32, 8192 tokens each, KV in
-    the Top-16 format with ~0.1% escapes; reference = GPU decode into bf16 KV, then
+    the Top-16 format: the natural ~0.05% escapes, and the benchmark's input with
+    0.1% of the elements replaced by outliers of magnitude logU[1e2, 1e4];
+    reference = GPU decode into bf16 KV (checked equal to the original KV), then
     float32 attention."""
     from unchainkv_amd import workloads
 
-    say("llama3-8b decode attention 32 x 8192")
+    say("llama3-8b decode attention 32 x 8192", outliers)
     shape = workloads.LLAMA3_8B
     batch_size, ctx, kv_heads = 32, 8192, 8
     blocks = ctx // 16
     pool = batch_size * blocks
-    kv = workloads.make_kv_layer(torch, shape, pool, seed=4, layer=0, device="cuda")
+    kv = workloads.make_kv_layer(torch, shape, pool, seed=4, layer=0, device="cuda",
+                                 outlier_rate=outliers)
     tables = [list(range(b * blocks, (b + 1) * blocks)) for b in range(batch_size)]
     books = workloads.fit_codebook(torch, kv, tables)
     batch = sz.PagedBatch(tables, shape.block_words, "cuda")
@@ -245,6 +249,10 @@ def test_llama3_8b_decode_step_against_decode_then_attend(sz):
     ref = torch.matmul(p, v.permute(0, 2, 1, 3).contiguous())   # (b, h, 4, d)
     ref = ref.reshape(batch_size, 32, HEAD_DIM)
     torch.cuda.synchronize()
+    escapes = sum(int.from_bytes(bytes(payloads[o + 1:o + 5].cpu().numpy()), "little")
+                  for o in batch.out_offsets)
+    assert escapes > (0.0008 if outliers else 0.0002) * 2 * pool * shape.block_words, escapes
+    assert torch.isfinite(out.float()).all()
     err = (out.float() - ref).abs().amax(dim=-1)
     scale = ref.abs().amax(dim=-1).clamp_min(1e-6)
     assert (err <= TOL * scale).all(), float((err / scale).max())

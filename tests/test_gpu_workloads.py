@@ -1,7 +1,8 @@
 """Parity at the benchmark workloads' full sizes.
 
 * Llama-3-8B paged (8 x 4096 tokens, 4096-block pool): every one of the 32 layers
-  round-trips exactly into an independent receiver table.
+  is encoded with its escape directory (the benchmark's path), matches the oracle
+  byte for byte, and round-trips exactly into an independent receiver table.
 * The same shapes with 1% outliers: every Top-16 payload overflows (byte 0 = 255,
   capacity-clamped count, the first ``cap`` escapes in ascending order), matches
   the oracle byte for byte, and the fixed6 re-encode of the batch matches the
@@ -48,6 +49,7 @@ def test_llama3_8b_all_layers_round_trip(env):
     batch = sz.PagedBatch(tables, shape.block_words, "cuda")
     recv = sz.PagedBatch(recv_tables, shape.block_words, "cuda")
     out, ws = batch.new_payload_buffer(), batch.new_workspace()
+    directory = batch.new_directory()
     src = torch.tensor([b for t in tables for b in t], device="cuda")
     dst = torch.tensor([b for t in recv_tables for b in t], device="cuda")
     target = None
@@ -57,12 +59,19 @@ def test_llama3_8b_all_layers_round_trip(env):
         books = wl.fit_codebook(torch, kv, tables)
         if target is None:
             target = torch.zeros_like(kv)
-        assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books) == batch.total_encoded_bytes
+        assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books, directory=directory) \
+            == batch.total_encoded_bytes
         assert sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, target, recv,
-                                     codebooks=books) == batch.total_raw_bytes
+                                     codebooks=books, directory=directory) == batch.total_raw_bytes
         assert torch.equal(kv.view(torch.int16)[:, src], target.view(torch.int16)[:, dst])
-        heads = out.cpu()[torch.tensor(batch.out_offsets)]
-        assert (heads == 5).all()
+        host = out.cpu().numpy()
+        ref = oracle.encode_paged_batch(host_words(kv), 4096 * shape.block_words,
+                                        shape.block_words, shape.block_words, tables,
+                                        batch.out_offsets, batch.out_bytes,
+                                        oracle.top16_tables(books),
+                                        threads=oracle.default_threads())
+        for r, (a, e) in enumerate(zip(batch.out_offsets, batch.encoded_bytes)):
+            assert host[a] == 5 and bytes(host[a:a + e]) == bytes(ref[a:a + e]), (layer, r)
 
 
 def test_llama3_8b_outliers_overflow_then_fixed6(env):
