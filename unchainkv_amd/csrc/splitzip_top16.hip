@@ -60,7 +60,10 @@ namespace {
 // Llama-3-8B layer call (2048 tiles per payload), encode: 8 groups 48.6 us, 16
 // groups 48.1 us, 32 groups 48.4 us (the 1 % outlier encode: 135.9, 134.4, 133.0);
 // the Llama-3.2-1B payload (256 tiles): 8 groups 8.4 us, 16 groups 8.9 us.
-constexpr unsigned int kFinLargeTiles = 1024;  // payloads from this size take 16 groups
+// payloads from this size take 16 finalize groups, smaller ones 8 (fewer, fuller
+// workgroups: Llama-3-70B TP8 encode call 73.5 -> 72.9 us with 8 for its largest
+// payloads of 2048 tiles)
+constexpr unsigned int kFinLargeTiles = 4096;
 constexpr int kFinPreload = 8;                         // staged escapes loaded with the counts
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
