@@ -59,6 +59,7 @@ constexpr int kWaveLds = kStep * kKStride + kVtWords;   // u16 per wave
 constexpr int kMaxSeqs = 64;                // sequences per launch (kernel arguments)
 constexpr int kPartial = kHeadDim + 2;      // m, l, acc[128] per (split, query head)
 constexpr int kMaxSplits = 64;
+constexpr int kCheck = 8;                   // escape-order pairs per thread held through the walk
 static_assert(4 * kGroup * kPartial * 4 <= 4 * kWaveLds * 2, "merge area fits the wave LDS");
 
 struct AttnArgs {
@@ -100,6 +101,13 @@ __device__ __forceinline__ void decode8(uint32_t b0, uint32_t b1, uint32_t cd,
 }
 
 // Position (u32 LE) of escape entry i.
+// Position of entry i by one unaligned dword load (entries are 5 bytes apart).
+typedef unsigned int u32_unaligned __attribute__((aligned(1)));
+__device__ __forceinline__ unsigned int entry_pos_u32(const unsigned char* entries,
+                                                      unsigned int i) {
+  return *reinterpret_cast<const u32_unaligned*>(entries + 5ull * i);
+}
+
 __device__ __forceinline__ unsigned int entry_pos(const unsigned char* entries, unsigned int i) {
   const unsigned char* e = entries + 5ull * i;
   return (unsigned int)e[0] | ((unsigned int)e[1] << 8) | ((unsigned int)e[2] << 16) |
@@ -400,18 +408,20 @@ top16_attention_split(AttnArgs a) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) w.acc[nt] = f32x4{0, 0, 0, 0};
   w.ok = payload[0] == 5;
-  // this workgroup's share of the order check: entry pairs (i, i + 1) for i in
-  // [first, last), the list split evenly over the sequence's splits * pairs
-  // workgroups
-  bool order_bad = false;
-  {
-    const unsigned int groups = a.splits * pairs, g = split * pairs + hp;
-    const unsigned int chunk = (c.count + groups - 1) / groups;
-    const unsigned int first = min(g * chunk, c.count);
-    const unsigned int last = min(first + chunk, c.count > 0 ? c.count - 1 : 0u);
-    for (unsigned int i = first + tid; i < last; i += kThreads)
-      order_bad |= entry_pos(entries, i + 1) < entry_pos(entries, i);
-  }
+  // This workgroup's share of the order check: entry pairs (i, i + 1) for i in
+  // [chk_first, chk_last), the list split evenly over the sequence's splits * pairs
+  // workgroups. Thread t holds the positions of entries chk_first + kCheck*t ..
+  // + kCheck; their loads go out now and are compared once the walk's first loads
+  // are in flight, so they add no round trip of their own (entries past chk_last
+  // repeat its position).
+  const unsigned int chk_groups = a.splits * pairs, chk_g = split * pairs + hp;
+  const unsigned int chk_chunk = (c.count + chk_groups - 1) / chk_groups;
+  const unsigned int chk_first = min(chk_g * chk_chunk, c.count);
+  const unsigned int chk_last = min(chk_first + chk_chunk, c.count > 0 ? c.count - 1 : 0u);
+  const unsigned int chk0 = chk_first + tid * kCheck;
+  unsigned int chk[kCheck + 1];
+#pragma unroll
+  for (int k = 0; k <= kCheck; ++k) chk[k] = entry_pos_u32(entries, min(chk0 + k, chk_last));
   __syncthreads();  // decode tables
 
   // The four waves meet at a barrier after every second step, so that the two
@@ -426,6 +436,11 @@ top16_attention_split(AttnArgs a) {
   };
   const unsigned int steps_max = max(range_steps(0), range_steps(1));
   const unsigned int steps = wb < c.we ? (c.we - wb + kStep - 1) / kStep : 0u;
+  bool order_bad = false;
+  auto check_order = [&]() {
+#pragma unroll
+    for (int k = 0; k < kCheck; ++k) order_bad |= chk0 + k < chk_last && chk[k + 1] < chk[k];
+  };
   if (wb < c.we) {
     const unsigned int we = c.we;
     w.ptr_k = lower_bound_escapes(entries, c.count, wb * row_words);
@@ -441,6 +456,7 @@ top16_attention_split(AttnArgs a) {
                         (unsigned long long)min(t0 + 8, we - 1) * row_words + share, c.half);
     };
     RawShare r0 = load_step(wb);
+    check_order();
     RawShare r1;
     unsigned int ts = wb;
     for (unsigned int i = 0; i < steps_max; i += 2) {
@@ -456,8 +472,13 @@ top16_attention_split(AttnArgs a) {
       ts += 2 * kStep;
     }
   } else {
+    check_order();
     for (unsigned int i = 0; i < steps_max; i += 2) __builtin_amdgcn_s_barrier();
   }
+
+  // the rest of the order check (long lists only)
+  for (unsigned int i = chk_first + kThreads * kCheck + tid; i < chk_last; i += kThreads)
+    order_bad |= entry_pos_u32(entries, i + 1) < entry_pos_u32(entries, i);
 
   // ---- merge each head's 2 waves (m, l, acc), then write the split's partials ----
   float l_run = w.l_run;
@@ -518,10 +539,14 @@ __global__ __launch_bounds__(kHeadDim) void top16_attention_combine(AttnArgs a) 
   const unsigned int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const unsigned int h = qh / kGroup, g = qh % kGroup;
   const float* seq = a.partial + (unsigned long long)b * a.kv_heads * a.splits * kGroup * kPartial;
-  int flagged = 0;
-  for (unsigned int k = d; k < a.kv_heads * a.splits; k += kHeadDim)
-    flagged |= isnan(seq[(unsigned long long)k * kGroup * kPartial]) ? 1 : 0;
-  const bool bad = __syncthreads_or(flagged) != 0;
+  // the running max of the sequence's partials d, d + kHeadDim, ... (kv heads x
+  // splits of them): the first four loaded now, tested after the merge
+  float flag[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned int k = d + j * kHeadDim;
+    flag[j] = k < a.kv_heads * a.splits ? seq[(unsigned long long)k * kGroup * kPartial] : 0.f;
+  }
   const float* part = seq + (unsigned long long)h * a.splits * kGroup * kPartial + g * kPartial;
   float big = -INFINITY;
   for (unsigned int s = 0; s < a.splits; ++s) big = fmaxf(big, part[s * kGroup * kPartial]);
@@ -534,6 +559,12 @@ __global__ __launch_bounds__(kHeadDim) void top16_attention_combine(AttnArgs a) 
     den += p[1] * wgt;
     num += p[2 + d] * wgt;
   }
+  int flagged = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) flagged |= isnan(flag[j]) ? 1 : 0;
+  for (unsigned int k = d + 4 * kHeadDim; k < a.kv_heads * a.splits; k += kHeadDim)
+    flagged |= isnan(seq[(unsigned long long)k * kGroup * kPartial]) ? 1 : 0;
+  const bool bad = __syncthreads_or(flagged) != 0;
   a.out[((unsigned long long)b * a.q_heads + qh) * kHeadDim + d] =
       (uint16_t)bf16_bits(bad ? NAN : num / den);
 }
