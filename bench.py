@@ -744,6 +744,58 @@ def time_dropin(torch, sz, w, reps: int = 3):
     }
 
 
+def time_connector(torch, sz, w, layers: int = 8, rounds: int = 3):
+    """The connector's codec hooks over whole layers, as a serving engine calls them:
+    save_kv_layer (batched Top-16 encode with its escape directory, the payloads'
+    device-to-host copy on the copy stream into the pinned pool), ready (waits for
+    the copies; no fallback here), then load_kv_layer_batch on the receiver (one
+    pinned host-to-device copy, the escape directory built on the host, one decode
+    launch). Wall-clock per layer with the host's work included (PCIe-bound: the
+    payloads cross it twice), and the host time of each hook. Layer 0's restore is
+    checked against the sender's blocks."""
+    from unchainkv_amd.connector import CodecConfig, SplitzipLayerCodec
+
+    layers = min(layers, w["layers"])
+    if any(p["over"] for p in w["plan"][:layers]):
+        return {"skipped": "overflowed payloads in the first layers"}
+    send, recv = w["send"], w["recv"]
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False),
+                               codebooks={layer: w["books"][layer] for layer in range(layers)})
+
+    def one(layer):
+        t0 = time.perf_counter()
+        pending = codec.save_kv_layer(layer, w["kv"][layer], send.block_tables)
+        t1 = time.perf_counter()
+        payloads = codec.ready(pending)
+        t2 = time.perf_counter()
+        requests = [(rt, p.view, p.metadata(layer, send.block_words))
+                    for rt, p in zip(recv.block_tables, payloads)]
+        t3 = time.perf_counter()
+        got = codec.load_kv_layer_batch(layer, w["receiver"][layer], requests)
+        t4 = time.perf_counter()
+        torch.cuda.synchronize()
+        t5 = time.perf_counter()
+        codec.release(pending)
+        if got != [(len(t), 4 * len(t) * send.block_words) for t in send.block_tables]:
+            raise RuntimeError(f"layer {layer}: connector restore declined ({got})")
+        return t1 - t0, t2 - t1, t4 - t3, t5 - t0, sum(p.encoded_bytes for p in payloads)
+
+    one(0)
+    src = torch.tensor([b for t in send.block_tables for b in t], device=w["device"])
+    dst = torch.tensor([b for t in recv.block_tables for b in t], device=w["device"])
+    if not torch.equal(w["kv"][0].view(torch.int16)[:, src],
+                       w["receiver"][0].view(torch.int16)[:, dst]):
+        raise RuntimeError("connector round trip differs from the sender's blocks")
+    rows = [one(layer) for _ in range(rounds) for layer in range(layers)]
+    med = [statistics.median(r[k] for r in rows) * 1e3 for k in range(4)]
+    payload = rows[-1][4]
+    return {"layers": layers, "save_host_ms": round(med[0], 3), "ready_ms": round(med[1], 3),
+            "load_host_ms": round(med[2], 3), "wall_ms_per_layer": round(med[3], 3),
+            "raw_GBps_end_to_end": round(send.total_raw_bytes / (med[3] * 1e-3) / 1e9, 2),
+            "payload_bytes": payload,
+            "note": "PCIe-inclusive: the payloads go to host memory and back"}
+
+
 def time_overlap(torch, sz, w, repeats: int = 7):
     """Encode + device-to-host copy of a layer's payloads against the model's
     attention, in the modes of the reference's scripts/bench_codec_attention.py:
@@ -1273,6 +1325,7 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
         result["codec_writeback"] = time_writeback(torch, sz, w)
         result["dropin_per_request"] = time_dropin(torch, sz, w)
         result["staging_overlap"] = time_overlap(torch, sz, w)
+        result["connector_layer"] = time_connector(torch, sz, w)
         if not args.no_cpu_baseline:
             base = cpu_baseline(torch, w, args.cpu_baseline_layers, args.cpu_baseline_seconds)
             base["legs"] = {"ref-cpu-c": {k: base[k] for k in ("value", "cores", "sample")},

@@ -1,0 +1,46 @@
+"""Host staging copies of the connector's restore (staging.HostCopier): the
+threaded path places every payload's bytes exactly where the single-threaded
+path does, for byte strings, numpy-backed memoryviews and odd sizes."""
+
+import numpy as np
+
+from unchainkv_amd.staging import HostCopier
+
+
+def _pieces(rng, sizes, gap=37):
+    pieces, at = [], 0
+    for k, n in enumerate(sizes):
+        data = rng.integers(0, 256, n, dtype=np.uint8)
+        src = data.tobytes() if k % 2 else memoryview(data)
+        pieces.append((at, src))
+        at += n + gap
+    return pieces, at
+
+
+def test_threaded_copy_matches_serial():
+    rng = np.random.default_rng(3)
+    sizes = [9 << 20, 1, (5 << 20) + 3, 4 << 20, 12345]
+    pieces, end = _pieces(rng, sizes)
+    serial = np.zeros(end, np.uint8)
+    HostCopier(threads=1).copy(serial, pieces)
+    threaded = np.full(end, 7, np.uint8)
+    HostCopier(threads=4).copy(threaded, pieces)
+    for at, src in pieces:
+        assert bytes(serial[at:at + len(src)]) == bytes(src)
+    # gaps untouched by either path
+    mask = np.ones(end, bool)
+    for at, src in pieces:
+        mask[at:at + len(src)] = False
+    assert (serial[mask] == 0).all() and (threaded[mask] == 7).all()
+    assert np.array_equal(serial[~mask], threaded[~mask])
+
+
+def test_small_totals_stay_on_the_calling_thread():
+    rng = np.random.default_rng(4)
+    pieces, end = _pieces(rng, [100, 2000, 3])
+    copier = HostCopier(threads=4)
+    dst = np.zeros(end, np.uint8)
+    copier.copy(dst, pieces)
+    assert copier._pool is None
+    for at, src in pieces:
+        assert bytes(dst[at:at + len(src)]) == bytes(src)

@@ -46,7 +46,7 @@ from dataclasses import dataclass, field
 
 from . import codec_format, frames
 from .backoff import Top16Backoff
-from .staging import CopyStreams, PinnedPool
+from .staging import CopyStreams, HostCopier, PinnedPool
 from .codebooks import summarize_symbol_counts
 from .trace import TraceWriter
 
@@ -179,6 +179,7 @@ class SplitzipLayerCodec:
         self.codec_writeback_overwrite = self.codec_writeback and not config.preserve_source
         self.pinned = PinnedPool(config.host_mirror_bytes, config.host_mirror_layers)
         self.copy_streams = CopyStreams()
+        self.host_copier = HostCopier()
 
     # ------------------------------------------------------------------
     # library
@@ -730,9 +731,7 @@ class SplitzipLayerCodec:
                 end = dir_at + dir_bytes
         host, slot = self._host_buffer(max(end, 1), torch)
         host_np = host.numpy()
-        host_view = memoryview(host_np)
-        for mode, member, start in layout:
-            host_view[start:start + len(member[3])] = member[3]
+        self.host_copier.copy(host_np, [(start, member[3]) for _, member, start in layout])
         if dir_bytes:
             tops = [start for m, _, start in layout if m == codec_format.MODE_TOP16]
             built = sz.build_directory(host_np, tops, [len(m[3]) for m in top],

@@ -100,3 +100,50 @@ class CopyStreams:
             if stream is None:
                 stream = self._streams[index] = torch.cuda.Stream(device=index)
             return stream
+
+
+class HostCopier:
+    """Copies payload bytes into a staging buffer, large totals split over a few
+    threads (numpy releases the GIL for large contiguous copies: one Llama-3-8B
+    layer's 100 MB of payloads took ~4 ms on one thread)."""
+
+    PARALLEL_BYTES = 8 << 20
+    PIECE = 4 << 20
+
+    def __init__(self, threads: int = 8) -> None:
+        self.threads = max(1, threads)
+        self._pool = None
+        self._lock = threading.Lock()
+
+    def _executor(self):
+        with self._lock:
+            if self._pool is None:
+                from concurrent.futures import ThreadPoolExecutor
+
+                self._pool = ThreadPoolExecutor(self.threads, thread_name_prefix="ukv-stage")
+            return self._pool
+
+    def copy(self, dst, pieces) -> None:
+        """dst: writable uint8 numpy array; pieces: (offset in dst, bytes-like)."""
+        import numpy as np
+
+        total = sum(len(src) for _, src in pieces)
+        if total < self.PARALLEL_BYTES or self.threads == 1:
+            view = memoryview(dst)
+            for at, src in pieces:
+                view[at:at + len(src)] = src
+            return
+        jobs = []
+        for at, src in pieces:
+            arr = np.frombuffer(src, dtype=np.uint8)
+            for lo in range(0, arr.size, self.PIECE):
+                hi = min(lo + self.PIECE, arr.size)
+                jobs.append((at + lo, arr[lo:hi]))
+
+        def run(job):
+            at, arr = job
+            np.copyto(dst[at:at + arr.size], arr)
+
+        for _ in self._executor().map(run, jobs):
+            pass
+
