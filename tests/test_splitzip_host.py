@@ -159,6 +159,9 @@ def test_native_decoders_pass_noncontiguous_block_map(abi):
         def record_stream(self, stream):
             self.streams.append(stream)
 
+        def to(self, *_args, **_kwargs):  # the pinned host array's asynchronous upload
+            return self
+
     source = FakeTensor(11, (79,), (1,), uint8, device)
     target = FakeTensor(22, (2, 8, 2), (16, 2, 1), bfloat16, device)
     tables = FakeTensor(44, (544,), (1,), uint8, device)
