@@ -291,3 +291,42 @@ def test_writeback_skips_a_layer_that_is_not_contiguous():
     pending = PendingLayer(7, layer, 16384, members)
     assert not codec._stage_writeback(pending, members, (None, [0], [100], None), None)
     assert trace.rows == [("codec_writeback_skip", {"layer": 7, "reason": "layout"})]
+
+
+def test_two_chunk_rule_and_kvc2_frames():
+    """UNCHAIN_KV_SPLITZIP_CHUNKS=2 (vllm_connector.py:446-447, 2718-2737): only
+    with neither Top-16 nor fixed5 enabled, and only for an even number of blocks
+    in one ascending run; each half's frame is KVC2 with the whole request's block
+    count and raw bytes (:5551-5563)."""
+    from unchainkv_amd import frames
+    from unchainkv_amd.connector import LayerPayload
+
+    assert CodecConfig.from_env({"UNCHAIN_KV_SPLITZIP_CHUNKS": "2"}).chunks == 2
+    assert CodecConfig.from_env({"UNCHAIN_KV_SPLITZIP_CHUNKS": "3"}).chunks == 1
+    two, _ = codec(chunks=2)
+    assert two._two_chunks([4, 5, 6, 7]) and two._two_chunks([9, 10])
+    assert not two._two_chunks([4, 5, 6])         # odd
+    assert not two._two_chunks([4])               # a single block
+    assert not two._two_chunks([4, 6, 5, 7])      # not one ascending run
+    assert not codec(chunks=2, top16=True)[0]._two_chunks([4, 5, 6, 7])
+    assert not codec(chunks=2, fixed5=True)[0]._two_chunks([4, 5, 6, 7])
+    assert not codec()[0]._two_chunks([4, 5, 6, 7])
+
+    bw = 8
+    halves = []
+    for k, ids in enumerate(([4, 5], [6, 7])):
+        p = LayerPayload(0, ids, 2 * 2 * bw * 2, BITS_FIXED6, BITS_FIXED6, chunk_index=k,
+                         chunks_in_layer=2, request_blocks=4)
+        p.view = memoryview(bytes([3]) + bytes(40 + k))
+        p.encoded_bytes = len(p.view)
+        halves.append(p)
+    whole = LayerPayload(1, [9], 2 * bw * 2, BITS_FIXED6, BITS_FIXED6)
+    whole.view = memoryview(bytes([3]) + bytes(30))
+    whole.encoded_bytes = len(whole.view)
+    parts = SplitzipLayerCodec.frames(7, halves + [whole], bw, "t", ["req-a", "req-b"])
+    parsed = [frames.parse_compressed_native(b"".join(p[1:])) for p in parts]
+    for k, f in enumerate(parsed[:2]):
+        assert (f.request_id, f.layer_index, f.chunk_index, f.chunks_in_layer) == ("req-a", 7, k, 2)
+        assert (f.block_count, f.raw_block_size, f.raw_bytes) == (4, 2 * bw * 2, 4 * 2 * bw * 2)
+        assert bytes(f.payload) == bytes(halves[k].view)
+    assert (parsed[2].chunks_in_layer, parsed[2].block_count, parsed[2].request_id) == (1, 1, "req-b")

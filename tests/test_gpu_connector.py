@@ -286,6 +286,46 @@ def test_layer_travels_in_compressed_native_frames(sz, codebooks):
         assert np.array_equal(dst[:, recv[name]], src[:, t]), name
 
 
+def test_sender_splits_fixed6_requests_into_two_kvc2_chunks(sz, codebooks):
+    """UNCHAIN_KV_SPLITZIP_CHUNKS=2 on a fixed6 layer (vllm_connector.py:2718-2799):
+    a request with an even number of blocks in one run leaves as two fixed6
+    half-payloads in KVC2 frames, the others as one KVC1 frame; every payload equals
+    the oracle's fixed6 of its blocks and the receiver restores all of them."""
+    from unchainkv_amd import frames
+
+    say("connector two-chunk frames")
+    rng = np.random.default_rng(19)
+    pool = 80
+    highs = rng.choice(256, 40, replace=False).astype(np.uint16)   # fits the fixed6 palette
+    n = 2 * pool * BW
+    words = ((highs[rng.integers(0, 40, n)] << 8) | rng.integers(0, 256, n).astype(np.uint16))
+    words = words.astype(np.uint16)
+    kv = layer_from_words(words, pool)
+    tables = [list(range(10, 22)), [40, 41, 42], [60, 62, 61, 63]]  # run, odd, not a run
+    codec = SplitzipLayerCodec(CodecConfig(chunks=2), trace=RecordingTrace())
+    pending = codec.save_kv_layer(3, kv, tables)
+    payloads = codec.ready(pending)
+    assert [(p.request, p.chunk_index, p.chunks_in_layer) for p in payloads] == \
+        [(0, 0, 2), (0, 1, 2), (1, 0, 1), (2, 0, 1)]
+    host = words.reshape(2, pool, BW)
+    for p in payloads:
+        assert p.bits == BITS_FIXED6 and p.view[0] == codec_format.MODE_FIXED6
+        assert bytes(p.view) == bytes(oracle.fixed6_encode(host[:, p.block_ids].reshape(-1)))
+    parts = SplitzipLayerCodec.frames(3, payloads, BW, "t2", ["a", "b", "c"])
+    parsed = [frames.parse_compressed_native(b"".join(x[1:])) for x in parts]
+    assert [(f.request_id, f.chunks_in_layer, f.block_count) for f in parsed] == \
+        [("a", 2, 12), ("a", 2, 12), ("b", 1, 3), ("c", 1, 4)]
+    recv = {"a": list(range(50, 62)), "b": [1, 3, 5], "c": [70, 71, 72, 73]}
+    target = torch.zeros_like(kv)
+    got = codec.restore_frames(target, [b"".join(x[1:]) for x in parts], recv)
+    torch.cuda.synchronize()
+    codec.release(pending)
+    dst = u16(target).reshape(2, pool, BW)
+    for name, t in zip("abc", tables):
+        assert got[name] == (len(t), 4 * BW * len(t)), name
+        assert np.array_equal(dst[:, recv[name]], host[:, t]), name
+
+
 # ---------------------------------------------------------------------------
 # payload staging: copy stream and pinned pool (vllm_connector.py:3406-3458)
 

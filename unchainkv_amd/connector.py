@@ -78,6 +78,9 @@ class CodecConfig:
     # caps of the pinned staging pool (0: none), vllm_connector.py:480-486
     host_mirror_layers: int = 0           # UNCHAIN_KV_HOST_MIRROR_LAYERS (buffers)
     host_mirror_bytes: int = 0            # UNCHAIN_KV_HOST_MIRROR_BYTES
+    # 2: fixed6 layers send a contiguous request as two half-payloads in KVC2
+    # frames (vllm_connector.py:446-447, 2718-2799); anything else: one payload
+    chunks: int = 1                       # UNCHAIN_KV_SPLITZIP_CHUNKS
 
     @classmethod
     def from_env(cls, env=None) -> "CodecConfig":
@@ -92,6 +95,7 @@ class CodecConfig:
             writeback=_env_int(env, "UNCHAIN_KV_CODEC_WRITEBACK", int(top16)) > 0,
             host_mirror_layers=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_LAYERS", 0)),
             host_mirror_bytes=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_BYTES", 0)),
+            chunks=2 if _env_int(env, "UNCHAIN_KV_SPLITZIP_CHUNKS", 1) == 2 else 1,
         )
 
 
@@ -137,6 +141,9 @@ class LayerPayload:
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
     _mask_first: int = -1            # first high-byte presence mask in the layer's masks
+    chunk_index: int = 0             # which half of the request's blocks (two-chunk frames)
+    chunks_in_layer: int = 1
+    request_blocks: int = 0          # blocks of the whole request, for a chunk's frame
 
     def metadata(self, layer_index: int, block_words: int) -> dict:
         """Receiver metadata of a compressed-native layer payload."""
@@ -255,6 +262,13 @@ class SplitzipLayerCodec:
 
     def _cancel_splitzip_top16_probe(self, layer_index: int, epoch: int, probe: bool) -> None:
         self.top16_gate.cancel(layer_index, epoch, probe)
+
+    def _two_chunks(self, ids: list) -> bool:
+        """A request sent as two half-payloads (_try_send_splitzip_two_chunks,
+        vllm_connector.py:2718-2737): chunks = 2 with neither Top-16 nor fixed5
+        enabled, and an even number (at least 2) of blocks in one ascending run."""
+        return (self.config.chunks == 2 and not self.splitzip_top16 and not self.splitzip_fixed5
+                and len(ids) >= 2 and len(ids) % 2 == 0 and len(_contiguous_runs(ids)) == 1)
 
     def _choose_bits(self, layer_index: int, raw_bytes: int):
         """Codec choice of _splitzip_bf16_native_blocks (vllm_connector.py:3078-3094)."""
@@ -469,6 +483,15 @@ class SplitzipLayerCodec:
             if not ids:
                 raise ValueError("every request needs at least one block")
             raw = 2 * len(ids) * block_words * 2
+            if self._two_chunks(ids):
+                # each half of the blocks is its own fixed6 payload and frame
+                half = len(ids) // 2
+                for chunk in range(2):
+                    part = ids[chunk * half:(chunk + 1) * half]
+                    payloads.append(LayerPayload(r, part, raw // 2, BITS_FIXED6, BITS_FIXED6,
+                                                 chunk_index=chunk, chunks_in_layer=2,
+                                                 request_blocks=len(ids)))
+                continue
             bits, epoch, probe = self._choose_bits(layer_index, raw)
             payloads.append(LayerPayload(r, ids, raw, bits, bits, epoch, probe))
         pending = PendingLayer(layer_index, kv_layer, block_words, payloads)
@@ -627,14 +650,24 @@ class SplitzipLayerCodec:
     @staticmethod
     def frames(layer_index: int, payloads, block_words: int, transfer_id: str,
                request_ids) -> list:
-        """Compressed-native KVC1 frames (one per request, parts as
-        ``frames.pack_compressed_native`` returns them) carrying the ready payloads
-        of a layer; ``request_ids[p.request]`` names each request."""
+        """Compressed-native frames carrying the ready payloads of a layer (parts
+        as ``frames.pack_compressed_native`` returns them): KVC1, one per request,
+        or KVC2 for each half of a request sent in two chunks;
+        ``request_ids[p.request]`` names each request."""
         out = []
         for p in payloads:
             if p.view is None:
                 raise ValueError("payload is not ready")
             meta = p.metadata(layer_index, block_words)
+            if p.chunks_in_layer > 1:
+                # a KVC2 chunk carries the whole request's block count and raw
+                # bytes (vllm_connector.py:5551-5563)
+                out.append(frames.pack_compressed_native(
+                    transfer_id, request_ids[p.request], layer_index, p.view,
+                    raw_block_size=meta["raw_block_size"], block_count=p.request_blocks,
+                    raw_bytes=meta["raw_block_size"] * p.request_blocks, codec=meta["codec"],
+                    chunk_index=p.chunk_index, chunks_in_layer=p.chunks_in_layer))
+                continue
             out.append(frames.pack_compressed_native(
                 transfer_id, request_ids[p.request], layer_index, p.view,
                 raw_block_size=meta["raw_block_size"], block_count=meta["block_count"],
