@@ -65,6 +65,12 @@ namespace {
 // payloads of 2048 tiles)
 constexpr unsigned int kFinLargeTiles = 4096;
 constexpr int kFinPreload = 8;                         // staged escapes loaded with the counts
+// Dense tiles (more staged escapes than the preload) placed per wave pass by the
+// finalize: 2 normally; 8 after a presence-mask encode, the variant for a layer
+// that overflowed before (1 % outlier layer encode call 112.0 -> 108.7 us; with 8
+// in every finalize the Llama-3-8B call lost 0.9 us to the larger kernel).
+constexpr int kDenseItemsSparse = 2;
+constexpr int kDenseItemsDense = 8;
 
 __host__ __device__ inline unsigned long long escape_capacity(unsigned long long n) {
   return (n + 199) / 200;
@@ -927,7 +933,7 @@ __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned 
   }
 }
 
-template <int kFinGroups, bool kInBody>
+template <int kFinGroups, bool kInBody, int kDenseItems>
 __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
   constexpr int kFinPerThread = kFinGroups;             // tile counts per thread per pass
   constexpr int kFinChunk = kThreads * kFinPerThread;   // tiles scanned per pass
@@ -1070,15 +1076,16 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
       }
     }
     __syncthreads();
-    // dense tiles: wave w places the entries of list items w, w + 4, ...; two items
-    // per pass so that their loads are in flight together
+    // dense tiles: wave w places the entries of list items w, w + 4, ...;
+    // kDenseItems items per pass so that their loads are in flight together
     const unsigned int dense = s_dense_count;
-    for (unsigned int i0 = uniform(tid >> 6); i0 < dense; i0 += 2 * (kThreads / kWave)) {
+    for (unsigned int i0 = uniform(tid >> 6); i0 < dense;
+         i0 += kDenseItems * (kThreads / kWave)) {
       const unsigned int lane = tid & (kWave - 1);
-      unsigned int v[2][kStageSlots / kWave], tile[2], cnt[2];
-      unsigned long long start[2], bases[2];
+      unsigned int v[kDenseItems][kStageSlots / kWave], tile[kDenseItems], cnt[kDenseItems];
+      unsigned long long start[kDenseItems], bases[kDenseItems];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kDenseItems; ++h) {
         const unsigned int i = min(i0 + h * (kThreads / kWave), dense - 1);
         const unsigned int packed = s_dense_tile[i];
         tile[h] = chunk0 + (packed & 0xFFFFFFu);
@@ -1096,7 +1103,7 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
         }
       }
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < kDenseItems; ++h)
 #pragma unroll
         for (int k = 0; k < kStageSlots / kWave; ++k) {
           const unsigned int q = lane + k * kWave;
@@ -1332,13 +1339,24 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   const dim3 fin_grid(a.payload_count * (large ? 16 : 8));
   if (a.inbody_slots) {
     if (large)
-      hipLaunchKernelGGL((top16_encode_finalize<16, true>), fin_grid, block, 0, stream, a);
+      hipLaunchKernelGGL((top16_encode_finalize<16, true, kDenseItemsSparse>), fin_grid, block, 0,
+                         stream, a);
     else
-      hipLaunchKernelGGL((top16_encode_finalize<8, true>), fin_grid, block, 0, stream, a);
+      hipLaunchKernelGGL((top16_encode_finalize<8, true, kDenseItemsSparse>), fin_grid, block, 0,
+                         stream, a);
+  } else if (a.presence) {
+    if (large)
+      hipLaunchKernelGGL((top16_encode_finalize<16, false, kDenseItemsDense>), fin_grid, block, 0,
+                         stream, a);
+    else
+      hipLaunchKernelGGL((top16_encode_finalize<8, false, kDenseItemsDense>), fin_grid, block, 0,
+                         stream, a);
   } else if (large) {
-    hipLaunchKernelGGL((top16_encode_finalize<16, false>), fin_grid, block, 0, stream, a);
+    hipLaunchKernelGGL((top16_encode_finalize<16, false, kDenseItemsSparse>), fin_grid, block, 0,
+                       stream, a);
   } else {
-    hipLaunchKernelGGL((top16_encode_finalize<8, false>), fin_grid, block, 0, stream, a);
+    hipLaunchKernelGGL((top16_encode_finalize<8, false, kDenseItemsSparse>), fin_grid, block, 0,
+                       stream, a);
   }
   if (long long rc = check_launch("top16_encode_finalize")) return rc;
   if (a.inbody_slots) {
