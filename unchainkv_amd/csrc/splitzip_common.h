@@ -402,4 +402,45 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Top-16 decode of 8 words in registers (the decode tile kernels and the fused
+// attention)
+
+// Per-byte 0xFF/0x00 masks from bit 3 of each byte of s (byte permute with the
+// sign-replicating selectors 8-11).
+__device__ __forceinline__ uint32_t bit3_mask(uint32_t s) {
+  return __builtin_amdgcn_perm(s << 12, s << 4, 0x090B080Au);
+}
+
+// Exponents of four 4-bit codes (one per byte of s) from a 16-byte codebook held
+// in four dwords: two byte permutes (codes 0-7 and 8-15) merged by bit 3.
+__device__ __forceinline__ uint32_t codebook_lookup4(uint32_t s, const uint32_t (&cb)[4]) {
+  const uint32_t s7 = s & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(cb[1], cb[0], s7);
+  const uint32_t hi = __builtin_amdgcn_perm(cb[3], cb[2], s7);
+  const uint32_t mask = bit3_mask(s);
+  return (hi & mask) | (lo & ~mask);
+}
+
+// Two decoded words from bytes [b0, e0, b1, e1] (body byte, exponent): mantissa
+// from b, exponent into bits 7-14, b's bit 7 into the sign bit 15.
+__device__ __forceinline__ uint32_t assemble_pair(uint32_t x) {
+  const uint32_t y = (x & 0x007F007Fu) | ((x >> 1) & ~0x007F007Fu);
+  return ((x << 8) & 0x80008000u) | (y & ~0x80008000u);
+}
+
+// Decodes one 8-word run: 8 body bytes (2 dwords) and 4 code bytes -> 4 dwords.
+__device__ __forceinline__ u32x4 decode_run8(u32x2 body, uint32_t cd, const uint32_t (&cb)[4]) {
+  const uint32_t u = cd >> 4;
+  // codes of the 8 words as bytes (low nibble first)
+  const uint32_t sa = __builtin_amdgcn_perm(u, cd, 0x05010400u) & 0x0F0F0F0Fu;
+  const uint32_t sb = __builtin_amdgcn_perm(u, cd, 0x07030602u) & 0x0F0F0F0Fu;
+  const uint32_t ea = codebook_lookup4(sa, cb);
+  const uint32_t eb = codebook_lookup4(sb, cb);
+  return u32x4{assemble_pair(__builtin_amdgcn_perm(ea, body.x, 0x05010400u)),
+               assemble_pair(__builtin_amdgcn_perm(ea, body.x, 0x07030602u)),
+               assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x05010400u)),
+               assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x07030602u))};
+}
+
 }  // namespace unchainkv
