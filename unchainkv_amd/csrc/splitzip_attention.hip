@@ -99,18 +99,11 @@ __device__ __forceinline__ void decode8(uint32_t b0, uint32_t b1, uint32_t cd,
   o[3] = (t3 & kExp) | (__builtin_amdgcn_perm(b1, b1, 0x03030202u) & ~kExp);
 }
 
-// Position (u32 LE) of escape entry i.
-// Position of entry i by one unaligned dword load (entries are 5 bytes apart).
+// Position (u32 LE) of escape entry i by one unaligned dword load (entries are
+// 5 bytes apart; the load stays inside the entry).
 typedef unsigned int u32_unaligned __attribute__((aligned(1)));
-__device__ __forceinline__ unsigned int entry_pos_u32(const unsigned char* entries,
-                                                      unsigned int i) {
-  return *reinterpret_cast<const u32_unaligned*>(entries + 5ull * i);
-}
-
 __device__ __forceinline__ unsigned int entry_pos(const unsigned char* entries, unsigned int i) {
-  const unsigned char* e = entries + 5ull * i;
-  return (unsigned int)e[0] | ((unsigned int)e[1] << 8) | ((unsigned int)e[2] << 16) |
-         ((unsigned int)e[3] << 24);
+  return *reinterpret_cast<const u32_unaligned*>(entries + 5ull * i);
 }
 
 // Packed bytes of one lane's share of a step, per plane: 16 body bytes (mantissa |
@@ -420,7 +413,7 @@ top16_attention_split(AttnArgs a) {
   const unsigned int chk0 = chk_first + tid * kCheck;
   unsigned int chk[kCheck + 1];
 #pragma unroll
-  for (int k = 0; k <= kCheck; ++k) chk[k] = entry_pos_u32(entries, min(chk0 + k, chk_last));
+  for (int k = 0; k <= kCheck; ++k) chk[k] = entry_pos(entries, min(chk0 + k, chk_last));
   __syncthreads();  // decode tables
 
   // The four waves meet at a barrier after every second step, so that the two
@@ -477,7 +470,7 @@ top16_attention_split(AttnArgs a) {
 
   // the rest of the order check (long lists only)
   for (unsigned int i = chk_first + kThreads * kCheck + tid; i < chk_last; i += kThreads)
-    order_bad |= entry_pos_u32(entries, i + 1) < entry_pos_u32(entries, i);
+    order_bad |= entry_pos(entries, i + 1) < entry_pos(entries, i);
 
   // ---- merge each head's 2 waves (m, l, acc), then write the split's partials ----
   float l_run = w.l_run;
