@@ -192,6 +192,36 @@ def test_paged_encode_decode_matches_oracle(sz, bits, bw, pool, requests, offset
 
 
 @pytest.mark.parametrize("bits", [6, 5])
+@pytest.mark.parametrize("shift", [1, 7])
+def test_paged_decode_of_payloads_at_unaligned_offsets(sz, bits, shift):
+    """Payloads from the oracle packed back to back at odd offsets (low bytes and
+    codes at any byte address) decode on the tile kernels, exactly."""
+    say("paged palette unaligned offsets", bits, shift)
+    rng = np.random.default_rng(90 + bits + shift)
+    bw, pool = 2048, 60
+    kv_host = palette_words(rng, 2 * pool * bw, limit(bits) - 4).reshape(2, pool, bw)
+    perm = rng.permutation(pool).tolist()
+    block_tables = [perm[0:5], perm[5:6], perm[6:20]]
+    payloads = [oracle.palette_encode(kv_host[:, t].reshape(-1), bits) for t in block_tables]
+    offsets, packed = [], bytearray()
+    for p in payloads:
+        packed += bytes(shift)
+        offsets.append(len(packed))
+        packed += bytes(p)
+    assert any(o % 16 for o in offsets)
+    source = torch.tensor(list(packed), dtype=torch.uint8, device="cuda")
+    recv_tables = [[(b + 11) % pool for b in t] for t in block_tables]
+    recv = sz.PagedBatch(recv_tables, bw, "cuda")
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    assert sz.decode_bf16_paged(source, offsets, [len(p) for p in payloads], target, recv,
+                                bits=bits) == recv.total_raw_bytes
+    torch.cuda.synchronize()
+    got = u16(target).reshape(2, pool, bw)
+    for src_t, dst_t in zip(block_tables, recv_tables):
+        assert np.array_equal(got[:, dst_t], kv_host[:, src_t])
+
+
+@pytest.mark.parametrize("bits", [6, 5])
 def test_paged_overflow_marks_only_that_payload(sz, bits):
     say("paged palette overflow", bits)
     rng = np.random.default_rng(17)

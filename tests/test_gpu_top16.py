@@ -7,6 +7,7 @@ payloads with shuffled escapes and garbage padding (the byte streams the
 reference's atomic-ordered encoder produces).
 """
 
+import ctypes
 import random
 
 import numpy as np
@@ -350,6 +351,55 @@ def test_paged_encode_decode_matches_oracle(sz, codebooks, bw, pool, requests, r
     used = {b for t in recv_tables for b in t}
     free = [b for b in range(pool) if b not in used]
     assert not got[:, free].any()
+
+
+@pytest.mark.parametrize("shift", [1, 6, 11])
+def test_paged_payloads_at_unaligned_offsets(sz, codebooks, shift):
+    """Payloads packed back to back at offsets of odd residues (bodies and code
+    sections at any byte address) take the tile kernels: encode with the escape
+    directory, byte-identical to the oracle, the gaps between payloads untouched;
+    then the one-kernel decode through that directory restores every block."""
+    say("paged unaligned offsets", shift)
+    bw, pool = 2048, 96
+    books = codebooks[5 * 32:6 * 32]
+    tables = oracle.top16_tables(books)
+    rng = np.random.default_rng(70 + shift)
+    words = random_words(rng, 2 * pool * bw, books, 0.003)
+    kv_host = words.reshape(2, pool, bw)
+    kv = bf16(words).view(2, pool, bw)
+    perm = rng.permutation(pool).tolist()
+    block_tables = [perm[0:9], perm[9:10], perm[10:40], perm[40:43]]
+    batch = sz.PagedBatch(block_tables, bw, "cuda")
+    offsets, at = [], 0
+    for e in batch.encoded_bytes:
+        at += shift
+        offsets.append(at)
+        at += e
+    assert any((o + 5) % 16 for o in offsets)
+    batch.out_offsets = offsets  # the batch's own offsets would be aligned
+    batch._out_offsets = (ctypes.c_ulonglong * len(offsets))(*offsets)
+    out = torch.full((at + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    directory = batch.new_directory()
+    assert sz.encode_top16_paged(kv, batch, out, batch.new_workspace(), codebooks=books,
+                                 directory=directory) == batch.total_encoded_bytes
+    torch.cuda.synchronize()
+    host = out.cpu().numpy()
+    prev = 0
+    for r, t in enumerate(block_tables):
+        o, e = offsets[r], batch.encoded_bytes[r]
+        assert bytes(host[o:o + e]) == bytes(oracle.top16_encode(kv_host[:, t].reshape(-1),
+                                                                 tables)), f"payload {r}"
+        assert not (host[prev:o] != 0xA5).any(), f"gap before payload {r}"
+        prev = o + e
+    assert not (host[prev:] != 0xA5).any()
+    recv_tables = [[(b + 7) % pool for b in t] for t in block_tables]
+    recv = sz.PagedBatch(recv_tables, bw, "cuda")
+    target = torch.zeros_like(kv)
+    assert sz.decode_top16_paged(out, offsets, batch.encoded_bytes, target, recv,
+                                 codebooks=books, directory=directory) == batch.total_raw_bytes
+    got = u16(target).reshape(2, pool, bw)
+    for src_t, dst_t in zip(block_tables, recv_tables):
+        assert np.array_equal(got[:, dst_t], kv_host[:, src_t])
 
 
 @pytest.mark.parametrize("label", ["dense tile", "overflow"])

@@ -741,8 +741,9 @@ class SplitzipLayerCodec:
         if not groups:
             return results
         block_words = kv_layer[0, 0].numel()
-        # one pinned staging buffer, each payload placed where the decode kernels
-        # find its sections aligned
+        # one pinned staging buffer, each payload's sections starting on a
+        # 256-byte boundary (the decode kernels take any offset; whole cache
+        # lines per tile span are cheaper)
         header = {codec_format.MODE_TOP16: 5, codec_format.MODE_FIXED6: 65,
                   codec_format.MODE_FIXED5: 33, codec_format.MODE_RAW: 1, TORCHOP: 0}
         layout, end = [], 0

@@ -29,6 +29,9 @@ constexpr int kChunkWords = 8;
 // rarely has a tile to re-scan); tiles with more are re-scanned by the finalize
 // kernel.
 constexpr int kStageSlots = 128;
+// Escapes staged in a tile's own first 512 body bytes after its u32 count, when
+// a drop-in encode has no room for a workspace.
+constexpr unsigned int kInBodySlots = kStageSlots - 1;
 // Payload descriptors passed by value in the kernel arguments.
 constexpr int kMaxPayloads = 64;
 

@@ -19,9 +19,10 @@
 //   palette_encode_tile / _generic     header + palette, low bytes, packed codes
 //   palette_decode_tile / _generic     decode + scatter (no-op unless byte 0 is the
 //       format's mode byte)
-// The tile kernels take the aligned batched layout (block words a multiple of
-// 1024): waves own 1024 words of one block, lanes two 8-word runs, and the packed
-// codes of a tile are staged in LDS so they move as whole dwords.
+// The tile kernels take block words a multiple of 1024 and a payload at any byte
+// address (global memory takes unaligned vector accesses): waves own 1024 words of
+// one block, lanes two 8-word runs, and the packed codes of a tile are staged in
+// LDS so they move as whole dwords.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -291,8 +292,8 @@ __global__ __launch_bounds__(kThreads) void palette_encode_tile(LaunchArgs a, En
     stage_run<kBits>(stage, kBits * (64 + lane), pack_run<kBits>(x + 4, rank));
   }
   __syncthreads();
-  // the tile's code bytes as whole dwords (the section is 16-byte aligned and a
-  // tile's share is a multiple of 16 bytes)
+  // the tile's code bytes as whole dwords (a tile's share is a multiple of 16
+  // bytes, so no dword reaches into a neighbour tile's share)
   const unsigned long long tile_word = t.plane * (t.n >> 1) + t.in_plane0;
   uint32_t* codes = reinterpret_cast<uint32_t*>(t.payload + P::kHeader + t.n +
                                                 tile_word * kBits / 8);
@@ -430,11 +431,9 @@ inline bool tile_geometry(unsigned long long kv_ptr, unsigned long long plane_st
          block_stride % 8 == 0 && max_plane_words < (1ull << 31);
 }
 
-// Low and code sections of a payload at `base` start 16-byte aligned.
-inline bool palette_aligned(unsigned long long base, unsigned long long n, int bits) {
-  const unsigned long long header = bits == 6 ? 65 : 33;
-  return (base + header) % 16 == 0 && n % 16 == 0;
-}
+// A payload of n words suits the tile kernels at any byte address when its
+// sections are whole multiples of 16 bytes.
+inline bool palette_sections(unsigned long long n) { return n % 16 == 0; }
 
 unsigned int tiles_of(unsigned long long n) {
   return 2u * (unsigned int)(((n >> 1) + kTileWords - 1) >> kTileShift);
@@ -593,7 +592,7 @@ extern "C" long long kvq_splitzip_bf16_encode_mode(unsigned long long src_ptr,
   const unsigned long long room = dst_ptr + capacity > ws ? dst_ptr + capacity - ws : 0;
   const bool tiles = count % 2 == 0 &&
                      tile_geometry(src_ptr, count / 2, 0, count / 2, count / 2) &&
-                     palette_aligned(dst_ptr, count, bits) &&
+                     palette_sections(count) &&
                      room >= sizeof(PaletteInfo) + 32ull * tiles_of(count);
   a.total_tiles = tiles ? tiles_of(count) : 0;
   // Generic path: one presence mask per workgroup of the presence pass, as many as
@@ -645,7 +644,7 @@ long long decode_blocks(unsigned long long src_ptr, unsigned long long encoded_b
   a.tile_shift = kTileShift;
   const bool tiles = tile_geometry(dst_ptr, plane_stride, block_stride, block_words,
                                    count_words / 2) &&
-                     palette_aligned(src_ptr, count_words, bits);
+                     palette_sections(count_words);
   a.total_tiles = tiles_of(count_words);
   const long long rc = palette_decode(a, make_geom(block_words), tiles,
                                       reinterpret_cast<hipStream_t>(stream_ptr), bits);
@@ -704,7 +703,7 @@ long long encode_mode_paged_impl(
     for (unsigned long long r = 0; r < payload_count; ++r)
       if (presence_first[r] > 0xFFFFFFFFULL) return 0;
   unsigned long long total = 0, max_plane = 0;
-  bool aligned = true;
+  bool sections = true;
   std::vector<std::pair<unsigned long long, unsigned long long>> spans;
   for (unsigned long long r = 0; r < payload_count; ++r) {
     if (block_offsets[r + 1] <= block_offsets[r]) return 0;
@@ -714,14 +713,14 @@ long long encode_mode_paged_impl(
     spans.emplace_back(out_offsets[r], out_offsets[r] + e);
     total += e;
     max_plane = std::max(max_plane, n >> 1);
-    aligned = aligned && palette_aligned(out_ptr + out_offsets[r], n, bits);
+    sections = sections && palette_sections(n);
   }
   std::sort(spans.begin(), spans.end());
   for (size_t k = 1; k < spans.size(); ++k)
     if (spans[k].first < spans[k - 1].second) return 0;  // overlapping payloads
   if (batch_workspace_bytes(block_offsets, payload_count, block_words) > workspace_bytes) return 0;
   const bool tiles =
-      aligned && tile_geometry(kv_ptr, plane_stride, block_stride, block_words, max_plane);
+      sections && tile_geometry(kv_ptr, plane_stride, block_stride, block_words, max_plane);
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace_ptr);
@@ -791,17 +790,17 @@ extern "C" long long kvq_splitzip_bf16_decode_mode_paged(
       block_words == 0 || block_words > 0xFFFFFFFFULL || (bits != 5 && bits != 6))
     return 0;
   unsigned long long total = 0, max_plane = 0;
-  bool aligned = true;
+  bool sections = true;
   for (unsigned long long r = 0; r < payload_count; ++r) {
     if (block_offsets[r + 1] <= block_offsets[r]) return 0;
     const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
     if (encoded_bytes[r] != palette_encoded_size(n, bits) || (n >> 1) > 0xFFFFFFFFULL) return 0;
     total += 2 * n;
     max_plane = std::max(max_plane, n >> 1);
-    aligned = aligned && palette_aligned(src_ptr + src_offsets[r], n, bits);
+    sections = sections && palette_sections(n);
   }
   const bool tiles =
-      aligned && tile_geometry(kv_ptr, plane_stride, block_stride, block_words, max_plane);
+      sections && tile_geometry(kv_ptr, plane_stride, block_stride, block_words, max_plane);
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {

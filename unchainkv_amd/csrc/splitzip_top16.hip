@@ -15,18 +15,21 @@
 // payload deterministic.
 //
 // Kernels (all launched on the caller's stream, no host synchronisation):
-//   top16_encode_tile        the batched layout (aligned sections, block words a
-//       multiple of 1024): gather through the block table + encode one 4096-word
-//       tile per workgroup, one block per wave so addressing is scalar; escapes
-//       are counted per tile and up to kStageSlots of them staged in the workspace.
-//   top16_encode_lanes<fast, sequential>  any section alignment or geometry:
-//       16 consecutive words per lane (misaligned stores realigned through
-//       neighbour-lane shuffles); or one workgroup walking every tile in order.
+//   top16_encode_tile        block words a multiple of 1024, payload at any byte
+//       address: gather through the block table + encode one 4096-word tile per
+//       workgroup, one block per wave so addressing is scalar; escapes are
+//       counted per tile and up to kStageSlots of them staged in the workspace.
+//   top16_encode_lanes<fast, sequential>  any geometry: 16 consecutive words per
+//       lane (stores realigned through neighbour-lane shuffles); or one workgroup
+//       walking every tile in order.
 //   top16_encode_finalize    per payload (8 or 16 workgroups): scan tile counts,
 //       place escapes in ascending order, write the header (the tile kernel
 //       zeroes the escape slots of its span).
 //   top16_decode_tile / top16_decode_lanes / top16_decode_generic
-//       decode + scatter for aligned sections, any alignment, any geometry.
+//       decode + scatter for the tile geometry, 16-word lanes, any geometry.
+// Global memory takes unaligned vector accesses (the code object's unaligned
+// access mode), so a payload's sections need no alignment: the reference
+// connector's payloads start at a buffer's first byte, their body at byte 5.
 //   top16_patch_escapes      apply escapes (any order) after decode.
 #include <hip/hip_runtime.h>
 
@@ -546,7 +549,7 @@ __global__ __launch_bounds__(kThreads) void top16_body_lanes(LaunchArgs a, Encod
 }
 
 // ---------------------------------------------------------------------------
-// Tile kernels: the batched layout (aligned sections) with one block per wave.
+// Tile kernels: block words a multiple of 1024, one block per wave.
 //
 // A workgroup handles one 4096-word tile of one plane; wave w covers words
 // [start + 1024w, start + 1024w + 1024), which lie in one KV block (block words a
@@ -555,7 +558,10 @@ __global__ __launch_bounds__(kThreads) void top16_body_lanes(LaunchArgs a, Encod
 // ("run A") and 512 + 8l .. 512 + 8l + 7 ("run B"), so that every vector memory
 // instruction of the wave covers one contiguous span (1 KiB of bf16, 512 B of body
 // bytes, 256 B of code bytes). The per-word work is a handful of VALU operations
-// (byte permutes, bit-field inserts) plus one LDS lookup for the encoder.
+// (byte permutes, bit-field inserts) plus one LDS lookup for the encoder. Body and
+// code spans may start at any byte (a payload at a buffer's first byte has its
+// body at byte 5): the memory system splits an unaligned access, and each store
+// writes only bytes of its own tile.
 
 // Code table byte for each of four exponents packed in a dword of the 544-byte
 // table: the code (0..15), or 0x10 for an escape (a code byte other than 255 keeps
@@ -620,8 +626,13 @@ __device__ __forceinline__ void zero_escape_span(unsigned char* payload, unsigne
 // kSeen: also writes the tile's high-byte presence mask to a.presence (the
 // variant for a layer likely to overflow, whose palette fallback then needs no
 // presence pass of its own).
-template <bool kIds, bool kSeen>
+// kInBody (drop-in encode with no room for a workspace): the tile's escape count
+// and its first kInBodySlots escapes are staged in the tile's first 512 body
+// bytes (run A of wave 0, left unwritten here); top16_body_tile writes those
+// body bytes once the finalize has read the staging.
+template <bool kIds, bool kSeen, bool kInBody>
 __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, EncodeGeom geo) {
+  static_assert(!(kSeen && kInBody), "presence masks come with a workspace");
   __shared__ uint32_t s_tab[64];  // this tile's plane, 4 code bytes per dword
   __shared__ unsigned int s_wave[kThreads / kWave];
   __shared__ uint32_t s_seen[kSeen ? 64 : 1];  // one byte per high byte value
@@ -663,10 +674,11 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
       seen[x[k] >> 24] = 1;
     }
   }
+  unsigned char* const tile_body = t.payload + 5 + t.plane * (t.n >> 1) + t.in_plane0;
   if (active) {
     unsigned char* pbody = t.payload + 5 + wstart;
     unsigned char* pcode = t.payload + 5 + t.n + (wstart >> 1);
-    store_through8(pbody + 8 * lane, u32x2{body_a[0], body_a[1]});
+    if (!kInBody || wave != 0) store_through8(pbody + 8 * lane, u32x2{body_a[0], body_a[1]});
     store_through8(pbody + 512 + 8 * lane, u32x2{body_b[0], body_b[1]});
     store_through4(pcode + 4 * lane, code_a);
     store_through4(pcode + 256 + 4 * lane, code_b);
@@ -708,7 +720,12 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
     if (w < (int)wave) before += v;
     total += v;
   }
-  if (tid == 0) a.workspace[tile] = total;
+  if (tid == 0) {
+    if (kInBody)
+      *reinterpret_cast<u32_unaligned*>(tile_body) = total;
+    else
+      a.workspace[tile] = total;
+  }
   // directory record of this wave's chunk: its first escape's slot within the tile,
   // its escape count, and its first kDirInline escapes (written by the lanes that
   // hold them, below)
@@ -716,14 +733,22 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
   if (rec && lane == 0) rec[0] = before | ((wave_a + (wave_tot >> 16)) << 16);
   if (mask_a | mask_b) {
     const unsigned int excl = incl - cnt;
-    unsigned int* staged = a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
+    unsigned int* staged =
+        kInBody ? nullptr : a.workspace + a.total_tiles + (unsigned long long)tile * kStageSlots;
+    auto stage = [&](unsigned int idx, uint32_t e) {
+      if (kInBody) {
+        if (idx < kInBodySlots) *reinterpret_cast<u32_unaligned*>(tile_body + 4 + 4 * idx) = e;
+      } else if (idx < kStageSlots) {
+        staged[idx] = e;
+      }
+    };
     const unsigned int local = wave * 1024 + lane * 8;
     unsigned int idx = before + (excl & 0xFFFFu);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (!((mask_a >> j) & 1)) continue;
       const uint32_t e = ((local + j) << 8) | ((x[j >> 1] >> (7 + 16 * (j & 1))) & 0xFF);
-      if (idx < kStageSlots) staged[idx] = e;
+      stage(idx, e);
       if (rec && idx - before < kDirInline) rec[1 + idx - before] = e;
       ++idx;
     }
@@ -733,12 +758,35 @@ __global__ __launch_bounds__(kThreads) void top16_encode_tile(LaunchArgs a, Enco
       if (!((mask_b >> j) & 1)) continue;
       const uint32_t e =
           ((local + 512 + j) << 8) | ((x[4 + (j >> 1)] >> (7 + 16 * (j & 1))) & 0xFF);
-      if (idx < kStageSlots) staged[idx] = e;
+      stage(idx, e);
       if (rec && idx - before < kDirInline) rec[1 + idx - before] = e;
       ++idx;
     }
   }
   zero_escape_span(t.payload, t.n, t.local_tile);
+}
+
+// The first 512 body bytes of every tile (run A of wave 0), from the source: the
+// last pass of a drop-in encode whose tiles staged their escapes there. One wave
+// per tile, 8 words per lane.
+template <bool kIds>
+__global__ __launch_bounds__(kThreads) void top16_body_tile(LaunchArgs a, EncodeGeom geo) {
+  const unsigned int lane = threadIdx.x & (kWave - 1);
+  const unsigned int tile = blockIdx.x * (kThreads / kWave) + uniform(threadIdx.x >> 6);
+  if (tile >= a.total_tiles) return;  // whole waves
+  const PlaneTile t = plane_tile<kTileShift>(a, tile);
+  const uint16_t* src = a.kv + wave_source<kIds>(a, t, geo, t.in_plane0);
+  const u32x4 v = load_stream16(src + 8 * lane);
+  uint32_t body[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t w0 = q ? v.z : v.x, w1 = q ? v.w : v.y;
+    const uint32_t t0 = (w0 & 0x007F007Fu) | ((w0 >> 8) & ~0x007F007Fu);
+    const uint32_t t1 = (w1 & 0x007F007Fu) | ((w1 >> 8) & ~0x007F007Fu);
+    body[q] = __builtin_amdgcn_perm(t1, t0, 0x06040200u);
+  }
+  unsigned char* pbody = t.payload + 5 + t.plane * (t.n >> 1) + t.in_plane0;
+  store_through8(pbody + 8 * lane, u32x2{body[0], body[1]});
 }
 
 template <bool kIds>
@@ -1216,15 +1264,8 @@ inline unsigned int host_payload_tiles(unsigned long long n, bool per_plane,
   return (unsigned int)((n + tile - 1) >> shift);
 }
 
-// A payload at `base` has its body 16-byte and its code section 8-byte aligned
-// (what the tile kernels load and store).
-inline bool sections_aligned(unsigned long long base, unsigned long long n) {
-  return (base + 5) % 16 == 0 && (base + 5 + n) % 8 == 0;
-}
-
 // tile_ok: every wave's 1024 words lie in one block (block words a multiple of
-// 1024), sections aligned for 16-byte body and 8-byte code stores, table dword
-// aligned.
+// 1024) and the code table is dword aligned.
 Plan make_plan(bool geometry_fast, bool tile_ok, bool sequential) {
   Plan p;
   p.sequential = sequential;
@@ -1270,17 +1311,24 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     case Kernel::kTile:
       if (a.presence) {
         if (a.ids)
-          hipLaunchKernelGGL((top16_encode_tile<true, true>), dim3(a.total_tiles), block, 0,
-                             stream, a, g);
+          hipLaunchKernelGGL((top16_encode_tile<true, true, false>), dim3(a.total_tiles), block,
+                             0, stream, a, g);
         else
-          hipLaunchKernelGGL((top16_encode_tile<false, true>), dim3(a.total_tiles), block, 0,
-                             stream, a, g);
+          hipLaunchKernelGGL((top16_encode_tile<false, true, false>), dim3(a.total_tiles), block,
+                             0, stream, a, g);
+      } else if (a.inbody_slots) {
+        if (a.ids)
+          hipLaunchKernelGGL((top16_encode_tile<true, false, true>), dim3(a.total_tiles), block,
+                             0, stream, a, g);
+        else
+          hipLaunchKernelGGL((top16_encode_tile<false, false, true>), dim3(a.total_tiles), block,
+                             0, stream, a, g);
       } else if (a.ids) {
-        hipLaunchKernelGGL((top16_encode_tile<true, false>), dim3(a.total_tiles), block, 0,
+        hipLaunchKernelGGL((top16_encode_tile<true, false, false>), dim3(a.total_tiles), block, 0,
                            stream, a, g);
       } else {
-        hipLaunchKernelGGL((top16_encode_tile<false, false>), dim3(a.total_tiles), block, 0,
-                           stream, a, g);
+        hipLaunchKernelGGL((top16_encode_tile<false, false, false>), dim3(a.total_tiles), block,
+                           0, stream, a, g);
       }
       break;
     case Kernel::kLanes:
@@ -1324,6 +1372,14 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   if (long long rc = check_launch("top16_encode_finalize")) return rc;
   if (a.inbody_slots) {
     // the staging in the body bytes has been read: write the body
+    if (p.kernel == Kernel::kTile) {
+      const dim3 grid((a.total_tiles + kThreads / kWave - 1) / (kThreads / kWave));
+      if (a.ids)
+        hipLaunchKernelGGL(top16_body_tile<true>, grid, block, 0, stream, a, g);
+      else
+        hipLaunchKernelGGL(top16_body_tile<false>, grid, block, 0, stream, a, g);
+      return check_launch("top16_body_tile");
+    }
     if (p.kernel == Kernel::kGeneric)
       hipLaunchKernelGGL(top16_body_lanes<false>, dim3(a.total_tiles), block, 0, stream, a, g);
     else
@@ -1420,33 +1476,29 @@ extern "C" long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr,
   a.block_start = 0;
   a.p[0].block_count = 1;
   const EncodeGeom g = make_geom(count / 2);
-  const bool aligned = sections_aligned(dst_ptr, count) && tables_ptr % 4 == 0 &&
-                       (count / 2) % 1024 == 0;
-  // Parallel tiles need a workspace for per-tile escape counts; it lives in the
-  // caller's buffer past the payload when the capacity allows, else one
-  // workgroup walks the tiles in order.
+  const bool tile_ok = tables_ptr % 4 == 0 && (count / 2) % 1024 == 0;
+  // Parallel tiles need a workspace for per-tile escape counts and staged escapes;
+  // it lives in the caller's buffer past the payload when the capacity allows.
   // Without that room (the ABI only promises align4(E) + 8 bytes) the tiles are still
   // encoded in parallel: each stages its escape count and escapes in its own body
-  // bytes, the finalize places them, and a last pass writes the body from the source
-  // (every tile needs 64 words for its staging); otherwise one workgroup walks them.
-  Plan plan = make_plan(geometry_fast, aligned, false);
+  // bytes, the finalize places them, and a last pass writes those body bytes from
+  // the source (the first 512 of each tile after the tile kernel, the whole body
+  // after the lanes kernels, whose tiles need 64 words for the staging); otherwise
+  // one workgroup walks the tiles in order.
+  Plan plan = make_plan(geometry_fast, tile_ok, false);
   unsigned int tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
   const unsigned long long ws_offset = align_up(dst_ptr + encoded, 16) - dst_ptr;
   const unsigned long long ws_bytes = workspace_words(tiles) * 4;
   if (tiles > 1 && ws_offset + ws_bytes <= capacity) {
     a.workspace = reinterpret_cast<unsigned int*>(dst_ptr + ws_offset);
   } else {
-    Plan staged = make_plan(geometry_fast, false, false);  // lanes or generic kernels
-    const unsigned long long tile_words = 1ull << staged.tile_shift;
-    const unsigned long long span = staged.per_plane ? count / 2 : count;
+    const unsigned long long tile_words = 1ull << plan.tile_shift;
+    const unsigned long long span = plan.per_plane ? count / 2 : count;
     const unsigned long long last = span % tile_words ? span % tile_words : tile_words;
-    const unsigned int staged_tiles = host_payload_tiles(count, staged.per_plane, staged.tile_shift);
-    if (staged_tiles > 1 && std::min(last, span) >= 64) {
-      plan = staged;
-      tiles = staged_tiles;
-      a.inbody_slots = kStageSlots - 1;  // 512 bytes: count + 127 escapes
+    if (tiles > 1 && std::min(last, span) >= 64) {
+      a.inbody_slots = kInBodySlots;  // 512 bytes: count + 127 escapes
     } else {
-      plan = make_plan(geometry_fast, aligned, true);
+      plan = make_plan(geometry_fast, tile_ok, true);
       tiles = host_payload_tiles(count, plan.per_plane, plan.tile_shift);
     }
   }
@@ -1485,9 +1537,8 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
   a.p[0].block_count = (unsigned int)block_count;
   const bool geometry_fast = block_words % 16 == 0 && dst_ptr % 16 == 0 && plane_stride % 8 == 0 &&
                              block_stride % 8 == 0 && (count_words >> 1) <= 0xFFFFFFFFULL;
-  const Plan plan = make_decode_plan(
-      geometry_fast, sections_aligned(src_ptr, count_words) && tables_ptr % 4 == 0 &&
-                         block_words % 1024 == 0 && (count_words >> 1) < kTilePlaneLimit);
+  const Plan plan = make_decode_plan(geometry_fast, tables_ptr % 4 == 0 && block_words % 1024 == 0 &&
+                                                        (count_words >> 1) < kTilePlaneLimit);
   apply_plan(a, plan);
   a.total_tiles = host_payload_tiles(count_words, true, plan.tile_shift);
   long long rc = launch_decode(a, make_geom(block_words), plan,
@@ -1560,16 +1611,6 @@ struct PagedGeometry {
 bool paged_fast(const PagedGeometry& pg) {
   return pg.block_words % 16 == 0 && pg.kv_ptr % 16 == 0 && pg.plane_stride % 8 == 0 &&
          pg.block_stride % 8 == 0;
-}
-
-bool paged_aligned(unsigned long long buf, const unsigned long long* block_offsets,
-                   const unsigned long long* buf_offsets, unsigned long long count,
-                   unsigned long long block_words) {
-  for (unsigned long long r = 0; r < count; ++r) {
-    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
-    if (!sections_aligned(buf + buf_offsets[r], n)) return false;
-  }
-  return true;
 }
 
 // Fills a.p for payloads [first, first + count) and returns the tile total.
@@ -1646,11 +1687,8 @@ long long encode_top16_paged_impl(
   if (workspace_ptr % 4 != 0) return 0;
 
   const PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
-  const Plan plan = make_plan(
-      paged_fast(pg),
-      paged_aligned(out_ptr, block_offsets, out_offsets, payload_count, block_words) &&
-          tables_ptr % 4 == 0 && block_words % 1024 == 0,
-      false);
+  const Plan plan =
+      make_plan(paged_fast(pg), tables_ptr % 4 == 0 && block_words % 1024 == 0, false);
   const unsigned long long dir_tiles =
       kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count) /
       kDirBytesPerTile;
@@ -1828,8 +1866,7 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_paged(
   const PagedGeometry pg{kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr};
   const Plan plan = make_decode_plan(
       paged_fast(pg),
-      paged_aligned(src_ptr, block_offsets, src_offsets, payload_count, block_words) &&
-          tables_ptr % 4 == 0 && block_words % 1024 == 0 && max_plane < kTilePlaneLimit);
+      tables_ptr % 4 == 0 && block_words % 1024 == 0 && max_plane < kTilePlaneLimit);
   const unsigned long long dir_tiles =
       kvq_splitzip_top16_paged_directory_bytes(block_words, block_offsets, payload_count) /
       kDirBytesPerTile;
