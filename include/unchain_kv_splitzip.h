@@ -68,10 +68,12 @@ long long kvq_splitzip_bf16_decode_fixed6(
  * (mode 5) of `count` contiguous bf16 words; the K/V split is at count/2. tables_ptr
  * is the 544-byte device table. Returns E = 5 + n + ceil(n/2) + 5*ceil(n/200); 0 if
  * count is 0 or above 2^32-1, if E >= 2*count, or if capacity < align4(E) + 8.
- * When capacity leaves room past the payload (16-byte aligned, 260 bytes per
+ * When capacity leaves room past the payload (16-byte aligned, 516 bytes per
  * 4096-word tile) the tiles are encoded in parallel using it as workspace;
- * otherwise one workgroup encodes the tiles in order. Escapes are written in
- * ascending position order and unused escape slots are zeroed. */
+ * otherwise they stage their escapes in their own body bytes, which a last pass
+ * rewrites (one workgroup walks the tiles in order only for payloads whose
+ * tiles hold fewer than 64 words). dst_ptr may be at any byte address. Escapes are
+ * written in ascending position order and unused escape slots are zeroed. */
 long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr, unsigned long long dst_ptr,
                                          unsigned long long count, unsigned long long capacity,
                                          unsigned long long tables_ptr,
@@ -96,6 +98,32 @@ long long kvq_splitzip_bf16_decode_top16(
     unsigned long long block_words, unsigned long long plane_stride,
     unsigned long long block_stride, unsigned long long block_start,
     unsigned long long tables_ptr, unsigned long long stream_ptr);
+
+/* No counterpart in the reference: kvq_splitzip_bf16_decode_top16_blocks with the
+ * block table in HOST memory (host_block_ids[0 .. block_count)), for callers whose
+ * table is a host list (the reference's decode_top16 uploads it with torch.tensor
+ * first, src/unchain_kv/splitzip_cuda.py:226-229). Up to 256 ids, each below 2^32,
+ * travel in the kernel arguments, so no host-to-device copy precedes the launch;
+ * the table is read before the call returns. Returns 0 (declined: use the
+ * device-table entry) for more blocks or a geometry the tile kernels do not take
+ * (block_words not a multiple of 1024, dst or strides off alignment). */
+long long kvq_splitzip_bf16_decode_top16_host_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, const long long* host_block_ids,
+    unsigned long long tables_ptr, unsigned long long stream_ptr);
+
+/* No counterpart in the reference: kvq_splitzip_bf16_decode_fixed6_blocks with the
+ * block table in host memory, under the same rules as
+ * kvq_splitzip_bf16_decode_top16_host_blocks (the reference's decode_fixed6
+ * uploads its list through the same _decode_layout). */
+long long kvq_splitzip_bf16_decode_fixed6_host_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, const long long* host_block_ids,
+    unsigned long long stream_ptr);
 
 /* ------------------------------------------------------------------------------
  * Additions: every request of one paged layer in one launch.

@@ -108,6 +108,23 @@ def test_dropin_decode_fixed6_scatter(sz, bw, blocks, pool, contiguous):
     assert np.array_equal(u16(target).reshape(2, pool, bw), expected)
 
 
+@pytest.mark.parametrize("blocks", [256, 257])
+def test_dropin_decode_fixed6_host_table_limit(sz, blocks):
+    """256 shuffled ids ride in the kernel arguments, 257 go through a device copy."""
+    say("dropin fixed6 decode host table", blocks)
+    rng = np.random.default_rng(blocks + 1)
+    bw, pool = 1024, 600
+    n = 2 * blocks * bw
+    words = palette_words(rng, n, 40)
+    comp = torch.from_numpy(oracle.fixed6_encode(words).copy()).cuda()
+    ids = rng.permutation(pool)[:blocks].tolist()
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    assert sz.decode_fixed6(comp, target, ids, 2 * n) == 2 * n
+    got = u16(target).reshape(2, pool, bw)
+    assert np.array_equal(got[:, ids].reshape(-1), words)
+    assert not got[:, np.setdiff1d(np.arange(pool), ids)].any()
+
+
 def test_dropin_decode_accepts_any_palette_order_and_skips_other_modes(sz):
     say("fixed6 permuted palette")
     rng = np.random.default_rng(9)

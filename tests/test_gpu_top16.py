@@ -234,6 +234,27 @@ def test_dropin_decode_scatter_matches_oracle(sz, codebooks, rate, bw, blocks, p
     assert np.array_equal(u16(target), expected.reshape(-1))
 
 
+@pytest.mark.parametrize("blocks", [256, 257])
+def test_dropin_decode_host_table_limit(sz, codebooks, blocks):
+    """A shuffled table of 256 ids rides in the kernel arguments; 257 ids go through
+    the device copy of the table. Both restore every block exactly."""
+    say("dropin decode host table", blocks)
+    rng = np.random.default_rng(blocks)
+    books = codebooks[2 * 32:3 * 32]
+    bw, pool = 1024, 700
+    n = 2 * blocks * bw
+    words = random_words(rng, n, books, 0.004)
+    payload = oracle.top16_encode(words, oracle.top16_tables(books))
+    ids = rng.permutation(pool)[:blocks].tolist()
+    target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+    comp = torch.from_numpy(payload.copy()).cuda()
+    assert sz.decode_top16(comp, target, ids, 2 * n, -1, codebooks=books) == 2 * n
+    got = u16(target).reshape(2, pool, bw)
+    assert np.array_equal(got[:, ids].reshape(-1), words)
+    rest = np.setdiff1d(np.arange(pool), ids)
+    assert not got[:, rest].any()
+
+
 def test_decode_accepts_shuffled_escapes_and_garbage_padding(sz, codebooks):
     say("decode shuffled escapes")
     rng = np.random.default_rng(21)

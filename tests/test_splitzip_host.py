@@ -184,6 +184,62 @@ def test_native_decoders_pass_noncontiguous_block_map(abi):
     assert block_map.streams == [current, current]
 
 
+@pytest.mark.parametrize("declined", [False, True])
+def test_noncontiguous_decode_passes_the_host_table_first(declined):
+    """A non-contiguous table of at most HOST_TABLE_BLOCKS ids goes to the host-table
+    entry points (no device copy); when they decline (0) the ids are uploaded and
+    the device-table entry points run, as without them."""
+    host_calls, device_calls = [], []
+
+    def host_entry(*args):
+        table = (ctypes.c_longlong * args[4]).from_address(args[8])
+        host_calls.append((args[:8], list(table), args[9:]))
+        return 0 if declined else 16
+
+    class FakeLib:
+        kvq_splitzip_bf16_decode_fixed6 = kvq_splitzip_bf16_decode_top16 = staticmethod(
+            lambda *a: pytest.fail("contiguous decoder used"))
+        kvq_splitzip_bf16_decode_fixed6_host_blocks = staticmethod(host_entry)
+        kvq_splitzip_bf16_decode_top16_host_blocks = staticmethod(host_entry)
+        kvq_splitzip_bf16_decode_fixed6_blocks = kvq_splitzip_bf16_decode_top16_blocks = \
+            staticmethod(lambda *a: device_calls.append(a) or 16)
+
+    class Uploaded(FakeTensor):
+        def __init__(self):
+            super().__init__(777, (2,), (1,), object(), SimpleNamespace(type="cuda"))
+
+        def record_stream(self, _stream):
+            pass
+
+        def to(self, *_a, **_k):
+            return self
+
+    device = SimpleNamespace(type="cuda")
+    uint8, bfloat16 = object(), object()
+    source = FakeTensor(11, (79,), (1,), uint8, device)
+    target = FakeTensor(22, (2, 8, 2), (16, 2, 1), bfloat16, device)
+    tables = FakeTensor(44, (544,), (1,), uint8, device)
+    uploads = []
+    fake_torch = _fake_torch(SimpleNamespace(cuda_stream=99), uint8=uint8, bfloat16=bfloat16,
+                             int64=object(), tensor=lambda *a, **k: uploads.append(a) or Uploaded())
+    old = splitzip_cuda._LIB
+    splitzip_cuda._LIB = FakeLib()
+    try:
+        with patch.dict(sys.modules, {"torch": fake_torch}), patch.object(
+                splitzip_cuda, "_top16_tables", return_value=tables):
+            assert splitzip_cuda.decode_fixed6(source, target, [5, 2], 16) == 16
+            assert splitzip_cuda.decode_top16(source, target, [5, 2], 16, 7) == 16
+    finally:
+        splitzip_cuda._LIB = old
+    common = (11, 79, 22, 8, 2, 2, 16, 2)
+    assert host_calls == [(common, [5, 2], (99,)), (common, [5, 2], (44, 99))]
+    if declined:
+        assert len(uploads) == 2
+        assert device_calls == [common + (5, 777, 99), common + (5, 777, 44, 99)]
+    else:
+        assert uploads == [] and device_calls == []
+
+
 @pytest.mark.parametrize("block_ids,raw_bytes", [
     ([], 16), ([3, 3], 16), ([3, 8], 16), ([-1, 2], 16), ([3, 4], 15), ([3, 4], 0), ([3, 4, 5], 16)])
 def test_decode_layout_rejects_bad_inputs_before_any_call(block_ids, raw_bytes):

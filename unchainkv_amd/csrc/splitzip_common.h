@@ -203,18 +203,27 @@ __device__ __forceinline__ unsigned int payload_tiles(const LaunchArgs& a, unsig
 }
 
 // Element offset of payload word i in the KV cache (any geometry).
-__device__ __forceinline__ unsigned long long word_offset(const LaunchArgs& a,
-                                                          const PayloadDesc& d,
-                                                          unsigned long long i) {
+// Element offset of word i with the payload's j-th block from block_of(j).
+template <typename BlockOf>
+__device__ __forceinline__ unsigned long long word_offset_by(const LaunchArgs& a,
+                                                             const PayloadDesc& d,
+                                                             unsigned long long i,
+                                                             BlockOf block_of) {
   if (a.linear_words) return i;
   unsigned long long plane_words = (unsigned long long)d.block_count * a.block_words;
   unsigned long long plane = i / plane_words;
   unsigned long long in_plane = i - plane * plane_words;
   unsigned long long j = in_plane / a.block_words;
   unsigned long long within = in_plane - j * a.block_words;
-  unsigned long long blk =
-      a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
-  return plane * a.plane_stride + blk * a.block_stride + within;
+  return plane * a.plane_stride + block_of(j) * a.block_stride + within;
+}
+
+__device__ __forceinline__ unsigned long long word_offset(const LaunchArgs& a,
+                                                          const PayloadDesc& d,
+                                                          unsigned long long i) {
+  return word_offset_by(a, d, i, [&](unsigned long long j) {
+    return a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -321,18 +330,38 @@ __device__ __forceinline__ PlaneTile plane_tile(const LaunchArgs& a, unsigned in
   return t;
 }
 
-// Wave-uniform element offset in the layer of in-plane word `in_plane` of tile t
-// (block from the payload's block table, or block_start + j without one).
+// Wave-uniform element offset in the layer of in-plane word `in_plane` of tile t,
+// with the payload's j-th block from block_of(j).
+template <typename BlockOf>
+__device__ __forceinline__ unsigned long long wave_offset_by(const LaunchArgs& a,
+                                                             const PlaneTile& t,
+                                                             const EncodeGeom& geo,
+                                                             unsigned int in_plane,
+                                                             BlockOf block_of) {
+  const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
+  const unsigned int within = in_plane - j * geo.bw;
+  const unsigned long long blk = block_of(j);
+  return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
+}
+
+// The same with the block from the payload's block table, or block_start + j
+// without one.
 template <bool kIds>
 __device__ __forceinline__ unsigned long long wave_source(const LaunchArgs& a, const PlaneTile& t,
                                                           const EncodeGeom& geo,
                                                           unsigned int in_plane) {
-  const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
-  const unsigned int within = in_plane - j * geo.bw;
-  const unsigned long long blk =
-      kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
-  return uniform64(t.plane * a.plane_stride + uniform64(blk) * a.block_stride + within);
+  return wave_offset_by(a, t, geo, in_plane, [&](unsigned int j) {
+    return kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
+  });
 }
+
+// A request's block table of at most kInlineBlocks ids carried in the kernel
+// arguments: a table that is a host list then needs no copy to the device before
+// the decode (its ids are read with scalar loads from the kernel-argument segment).
+constexpr unsigned int kInlineBlocks = 256;
+struct InlineBlocks {
+  unsigned int id[kInlineBlocks];
+};
 
 
 inline EncodeGeom make_geom(unsigned long long block_words) {

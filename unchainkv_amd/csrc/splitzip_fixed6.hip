@@ -339,8 +339,11 @@ __global__ __launch_bounds__(kThreads) void palette_encode_generic(LaunchArgs a,
 // ---------------------------------------------------------------------------
 // decode (DecodeFixed6 semantics, kvq_splitzip_cuda.cu:113-144)
 
-template <bool kIds, int kBits>
-__global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, EncodeGeom geo) {
+// Decode + scatter of one tile; the destination's j-th block from block_of(t, j).
+template <int kBits, typename BlockOf>
+__device__ __forceinline__ void palette_decode_tile_body(const LaunchArgs& a,
+                                                         const EncodeGeom& geo,
+                                                         BlockOf block_of) {
   using P = Palette<kBits>;
   constexpr unsigned int kWaveCodeBytes = 128 * kBits;
   constexpr unsigned int kMask = (1u << kBits) - 1u;
@@ -368,7 +371,8 @@ __global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, En
     const unsigned char* low = t.payload + P::kHeader + wstart;
     low_a = load_stream8(low + 8 * lane);
     low_b = load_stream8(low + 512 + 8 * lane);
-    dst = a.kv + wave_source<kIds>(a, t, geo, in_plane);
+    dst = a.kv + wave_offset_by(a, t, geo, in_plane,
+                                [&](unsigned int j) { return block_of(t, j); });
   }
   __syncthreads();
   if (mode != P::kMode || !active) return;  // the reference leaves other payloads untouched
@@ -388,6 +392,23 @@ __global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, En
     }
     store_through16(dst + run * 512 + 8 * lane, u32x4{out[0], out[1], out[2], out[3]});
   }
+}
+
+template <bool kIds, int kBits>
+__global__ __launch_bounds__(kThreads) void palette_decode_tile(LaunchArgs a, EncodeGeom geo) {
+  palette_decode_tile_body<kBits>(a, geo, [&](const PlaneTile& t, unsigned int j) {
+    return kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
+  });
+}
+
+// One request whose block table rides in the kernel arguments.
+template <int kBits>
+__global__ __launch_bounds__(kThreads) void palette_decode_tile_inline(LaunchArgs a,
+                                                                       EncodeGeom geo,
+                                                                       InlineBlocks table) {
+  palette_decode_tile_body<kBits>(a, geo, [&](const PlaneTile&, unsigned int j) {
+    return (unsigned long long)table.id[j];
+  });
 }
 
 // Any geometry: grid = payload_count x kGenericGroups, grid-stride over words.
@@ -479,10 +500,13 @@ long long launch_palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
 
 template <int kBits>
 long long launch_palette_decode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
-                                hipStream_t stream) {
+                                hipStream_t stream, const InlineBlocks* table) {
   const dim3 block(kThreads);
   if (tiles) {
-    if (a.ids)
+    if (table)
+      hipLaunchKernelGGL(palette_decode_tile_inline<kBits>, dim3(a.total_tiles), block, 0, stream,
+                         a, g, *table);
+    else if (a.ids)
       hipLaunchKernelGGL((palette_decode_tile<true, kBits>), dim3(a.total_tiles), block, 0, stream,
                          a, g);
     else
@@ -504,10 +528,11 @@ long long palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
                                               masks_given, stream);
 }
 
+// `table`: one request's block table in the kernel arguments (tile kernels only).
 long long palette_decode(LaunchArgs& a, const EncodeGeom& g, bool tiles, hipStream_t stream,
-                         int bits) {
-  return bits == 6 ? launch_palette_decode<6>(a, g, tiles, stream)
-                   : launch_palette_decode<5>(a, g, tiles, stream);
+                         int bits, const InlineBlocks* table = nullptr) {
+  return bits == 6 ? launch_palette_decode<6>(a, g, tiles, stream, table)
+                   : launch_palette_decode<5>(a, g, tiles, stream, table);
 }
 
 // Fills a.p for payloads [first, first + count) of a batch (tiles of 4096 words
@@ -622,7 +647,8 @@ long long decode_blocks(unsigned long long src_ptr, unsigned long long encoded_b
                         unsigned long long block_count, unsigned long long block_words,
                         unsigned long long plane_stride, unsigned long long block_stride,
                         unsigned long long block_start, unsigned long long block_ids_ptr,
-                        unsigned long long stream_ptr, int bits) {
+                        unsigned long long stream_ptr, int bits,
+                        const long long* host_ids = nullptr) {
   // kvq_splitzip_cuda.cu:351-357
   if (src_ptr == 0 || dst_ptr == 0 || count_words == 0 || block_count == 0 || block_words == 0 ||
       count_words != 2 * block_count * block_words)
@@ -646,8 +672,18 @@ long long decode_blocks(unsigned long long src_ptr, unsigned long long encoded_b
                                    count_words / 2) &&
                      palette_sections(count_words);
   a.total_tiles = tiles_of(count_words);
+  // a host block table rides in the kernel arguments (tile kernels only)
+  InlineBlocks table{};
+  if (host_ids) {
+    if (!tiles || block_count > kInlineBlocks) return 0;
+    for (unsigned long long j = 0; j < block_count; ++j) {
+      if (host_ids[j] < 0 || host_ids[j] > 0xFFFFFFFFll) return 0;
+      table.id[j] = (unsigned int)host_ids[j];
+    }
+  }
   const long long rc = palette_decode(a, make_geom(block_words), tiles,
-                                      reinterpret_cast<hipStream_t>(stream_ptr), bits);
+                                      reinterpret_cast<hipStream_t>(stream_ptr), bits,
+                                      host_ids ? &table : nullptr);
   return rc < 0 ? rc : (long long)(count_words * sizeof(uint16_t));
 }
 
@@ -671,6 +707,17 @@ extern "C" long long kvq_splitzip_bf16_decode_fixed6(
     unsigned long long stream_ptr) {
   return decode_blocks(src_ptr, encoded_bytes, dst_ptr, count_words, block_count, block_words,
                        plane_stride, block_stride, block_start, 0, stream_ptr, 6);
+}
+
+extern "C" long long kvq_splitzip_bf16_decode_fixed6_host_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, const long long* host_block_ids,
+    unsigned long long stream_ptr) {
+  if (host_block_ids == nullptr) return 0;
+  return decode_blocks(src_ptr, encoded_bytes, dst_ptr, count_words, block_count, block_words,
+                       plane_stride, block_stride, 0, 0, stream_ptr, 6, host_block_ids);
 }
 
 // ---------------------------------------------------------------------------

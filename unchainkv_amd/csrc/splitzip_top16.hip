@@ -789,8 +789,10 @@ __global__ __launch_bounds__(kThreads) void top16_body_tile(LaunchArgs a, Encode
   store_through8(pbody + 8 * lane, u32x2{body[0], body[1]});
 }
 
-template <bool kIds>
-__global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
+// Decode + scatter of one tile; the destination's j-th block from block_of(t, j).
+template <typename BlockOf>
+__device__ __forceinline__ void decode_tile(const LaunchArgs& a, const EncodeGeom& geo,
+                                            BlockOf block_of) {
   const unsigned int lane = threadIdx.x & (kWave - 1);
   const unsigned int wave = uniform(threadIdx.x >> 6);
   const PlaneTile t = plane_tile<kTileShift>(a, group_index());
@@ -809,7 +811,8 @@ __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, Enco
   // The block-id load and the destination address come after the payload loads
   // are issued, so the two round trips overlap.
   __builtin_amdgcn_sched_barrier(0);
-  uint16_t* dst = a.kv + wave_source<kIds>(a, t, geo, in_plane);
+  uint16_t* dst =
+      a.kv + wave_offset_by(a, t, geo, in_plane, [&](unsigned int j) { return block_of(t, j); });
   const u32x4 out_a = decode_run8(body_a, code_a, cb);
   const u32x4 out_b = decode_run8(body_b, code_b, cb);
   // Keeps the payload loads ahead of the mode test below: without this use the
@@ -819,6 +822,21 @@ __global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, Enco
   if (mode != 5) return;
   store_through16(dst + 8 * lane, out_a);
   store_through16(dst + 512 + 8 * lane, out_b);
+}
+
+template <bool kIds>
+__global__ __launch_bounds__(kThreads) void top16_decode_tile(LaunchArgs a, EncodeGeom geo) {
+  decode_tile(a, geo, [&](const PlaneTile& t, unsigned int j) {
+    return kIds ? (unsigned long long)t.ids[j] : a.block_start + j;
+  });
+}
+
+// One request whose block table rides in the kernel arguments.
+__global__ __launch_bounds__(kThreads) void top16_decode_tile_inline(LaunchArgs a, EncodeGeom geo,
+                                                                     InlineBlocks table) {
+  decode_tile(a, geo, [&](const PlaneTile&, unsigned int j) {
+    return (unsigned long long)table.id[j];
+  });
 }
 
 // Replaces the exponent of word w (0..1023) of this wave's chunk, held in run A
@@ -1207,7 +1225,9 @@ __global__ __launch_bounds__(kThreads) void top16_decode_generic(LaunchArgs a) {
 // The decode kernel wrote sign and mantissa from the body byte, so the patched word
 // is rebuilt from that byte and stored (no read of the destination). One thread
 // per escape slot; payload r owns workgroups [slot_group_begin, + ceil(cap_r/256)).
-__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
+// The destination's j-th block of payload d from block_of(d, j).
+template <typename BlockOf>
+__device__ __forceinline__ void patch_escapes(const LaunchArgs& a, BlockOf block_of) {
   const unsigned int r = find_slot_payload(a, blockIdx.x);
   const PayloadDesc d = a.p[r];
   const unsigned long long s =
@@ -1233,8 +1253,22 @@ __global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
   // written through like the tile kernels' output (after the kernel's last load):
   // the scattered 2-byte writes leave no dirty lines for the write-back at the
   // kernel's end (Llama-3-8B decode call 50.4 -> 50.3 us, step 3.166 -> 3.152 ms)
-  asm volatile("global_store_short %0, %1, off nt sc1" ::"v"(a.kv + word_offset(a, d, pos)),
-               "v"(word) : "memory");
+  const unsigned long long at =
+      word_offset_by(a, d, pos, [&](unsigned long long j) { return block_of(d, j); });
+  asm volatile("global_store_short %0, %1, off nt sc1" ::"v"(a.kv + at), "v"(word) : "memory");
+}
+
+__global__ __launch_bounds__(kThreads) void top16_patch_escapes(LaunchArgs a) {
+  patch_escapes(a, [&](const PayloadDesc& d, unsigned long long j) {
+    return a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : a.block_start + j;
+  });
+}
+
+__global__ __launch_bounds__(kThreads) void top16_patch_escapes_inline(LaunchArgs a,
+                                                                       InlineBlocks table) {
+  patch_escapes(a, [&](const PayloadDesc&, unsigned long long j) {
+    return (unsigned long long)table.id[j];
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -1389,7 +1423,10 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   return 0;
 }
 
-long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream) {
+// `table`: the request's block table in the kernel arguments (one payload on the
+// tile plan) instead of a.ids.
+long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipStream_t stream,
+                        const InlineBlocks* table = nullptr) {
   const dim3 block(kThreads);
   if (a.dir_rec) {  // the host only passes a directory with the tile plan
     if (a.ids)
@@ -1400,7 +1437,10 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   }
   switch (p.kernel) {
     case Kernel::kTile:
-      if (a.ids)
+      if (table)
+        hipLaunchKernelGGL(top16_decode_tile_inline, dim3(a.total_tiles), block, 0, stream, a, g,
+                           *table);
+      else if (a.ids)
         hipLaunchKernelGGL(top16_decode_tile<true>, dim3(a.total_tiles), block, 0, stream, a, g);
       else
         hipLaunchKernelGGL(top16_decode_tile<false>, dim3(a.total_tiles), block, 0, stream, a, g);
@@ -1433,7 +1473,11 @@ long long launch_decode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   }
   // equal payloads: a workgroup finds its payload by one division
   a.uniform_slot_groups = uniform ? (unsigned int)first_groups : 0u;
-  hipLaunchKernelGGL(top16_patch_escapes, dim3((unsigned int)groups), block, 0, stream, a);
+  if (table)
+    hipLaunchKernelGGL(top16_patch_escapes_inline, dim3((unsigned int)groups), block, 0, stream, a,
+                       *table);
+  else
+    hipLaunchKernelGGL(top16_patch_escapes, dim3((unsigned int)groups), block, 0, stream, a);
   return check_launch("top16_patch_escapes");
 }
 
@@ -1509,13 +1553,19 @@ extern "C" long long kvq_splitzip_bf16_encode_top16(unsigned long long src_ptr,
   return (long long)encoded;
 }
 
-extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
-    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
-    unsigned long long count_words, unsigned long long block_count,
-    unsigned long long block_words, unsigned long long plane_stride,
-    unsigned long long block_stride, unsigned long long block_start,
-    unsigned long long block_ids_ptr, unsigned long long tables_ptr,
-    unsigned long long stream_ptr) {
+namespace unchainkv {
+namespace {
+
+// One payload's decode + scatter; the block table from block_ids_ptr (device),
+// host_ids (host, carried in the kernel arguments: tile plan only, else declined),
+// or neither (block_start + j).
+long long decode_top16_one(unsigned long long src_ptr, unsigned long long encoded_bytes,
+                           unsigned long long dst_ptr, unsigned long long count_words,
+                           unsigned long long block_count, unsigned long long block_words,
+                           unsigned long long plane_stride, unsigned long long block_stride,
+                           unsigned long long block_start, unsigned long long block_ids_ptr,
+                           const long long* host_ids, unsigned long long tables_ptr,
+                           unsigned long long stream_ptr) {
   // Preconditions of kvq_splitzip_cuda.cu:423-432.
   if (src_ptr == 0 || dst_ptr == 0 || tables_ptr == 0 || count_words == 0 || block_count == 0 ||
       block_words == 0 || count_words != 2 * block_count * block_words)
@@ -1541,10 +1591,46 @@ extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
                                                         (count_words >> 1) < kTilePlaneLimit);
   apply_plan(a, plan);
   a.total_tiles = host_payload_tiles(count_words, true, plan.tile_shift);
+  InlineBlocks table{};
+  if (host_ids) {
+    if (plan.kernel != Kernel::kTile || block_count > kInlineBlocks) return 0;
+    for (unsigned long long j = 0; j < block_count; ++j) {
+      if (host_ids[j] < 0 || host_ids[j] > 0xFFFFFFFFll) return 0;
+      table.id[j] = (unsigned int)host_ids[j];
+    }
+  }
   long long rc = launch_decode(a, make_geom(block_words), plan,
-                               reinterpret_cast<hipStream_t>(stream_ptr));
+                               reinterpret_cast<hipStream_t>(stream_ptr),
+                               host_ids ? &table : nullptr);
   if (rc < 0) return rc;
   return (long long)(count_words * sizeof(uint16_t));
+}
+
+}  // namespace
+}  // namespace unchainkv
+
+extern "C" long long kvq_splitzip_bf16_decode_top16_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, unsigned long long block_start,
+    unsigned long long block_ids_ptr, unsigned long long tables_ptr,
+    unsigned long long stream_ptr) {
+  return decode_top16_one(src_ptr, encoded_bytes, dst_ptr, count_words, block_count, block_words,
+                          plane_stride, block_stride, block_start, block_ids_ptr, nullptr,
+                          tables_ptr, stream_ptr);
+}
+
+extern "C" long long kvq_splitzip_bf16_decode_top16_host_blocks(
+    unsigned long long src_ptr, unsigned long long encoded_bytes, unsigned long long dst_ptr,
+    unsigned long long count_words, unsigned long long block_count,
+    unsigned long long block_words, unsigned long long plane_stride,
+    unsigned long long block_stride, const long long* host_block_ids,
+    unsigned long long tables_ptr, unsigned long long stream_ptr) {
+  if (host_block_ids == nullptr) return 0;
+  return decode_top16_one(src_ptr, encoded_bytes, dst_ptr, count_words, block_count, block_words,
+                          plane_stride, block_stride, 0, 0, host_block_ids, tables_ptr,
+                          stream_ptr);
 }
 
 extern "C" long long kvq_splitzip_bf16_decode_top16(

@@ -24,6 +24,7 @@ Everything runs asynchronously on ``torch.cuda.current_stream(device)``.
 
 from __future__ import annotations
 
+import array
 import ctypes
 import os
 from pathlib import Path
@@ -49,6 +50,9 @@ _SIGNATURES = (
     ("kvq_splitzip_bf16_encode_top16", [_U64] * 6, ctypes.c_longlong, False),
     ("kvq_splitzip_bf16_decode_top16", [_U64] * 11, ctypes.c_longlong, False),
     ("kvq_splitzip_bf16_decode_top16_blocks", [_U64] * 12, ctypes.c_longlong, False),
+    # the host block table's address travels as a u64
+    ("kvq_splitzip_bf16_decode_top16_host_blocks", [_U64] * 11, ctypes.c_longlong, False),
+    ("kvq_splitzip_bf16_decode_fixed6_host_blocks", [_U64] * 10, ctypes.c_longlong, False),
     ("kvq_splitzip_last_error", [], ctypes.c_char_p, True),
     ("kvq_splitzip_top16_paged_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
     ("kvq_splitzip_top16_paged_directory_bytes", [_U64, _U64P, _U64], _U64, False),
@@ -228,16 +232,18 @@ def encode_bf16(source, out, bits: int = 6) -> int | None:
     return int(encoded)
 
 
+# Block tables of at most this many ids go to the decode in its kernel arguments.
+HOST_TABLE_BLOCKS = 256
+
+
 def _decode_layout(source, out, block_ids, raw_bytes, torch):
     """Validation and geometry of a decode (src/unchain_kv/splitzip_cuda.py:200-230):
     unique in-range block ids, uint8 source and bf16 (2, blocks, ...) target on the
     same CUDA device, both contiguous, raw_bytes an even multiple of 2 * blocks.
-    Returns (count_words, block_words, first block, stream handle, stream, ids):
-    a contiguous ascending run needs no id array; otherwise the ids go to the
-    device by an asynchronous copy from pinned memory, and ``stream`` is the
-    current stream object their tensor is recorded on. The checks use builtins
-    over the id list: with per-id Python checks and a pageable upload a 256-block
-    request took 69 us of host time, 31 us this way."""
+    Returns (count_words, block_words, first block, stream handle, contiguous): a
+    contiguous ascending run needs no id table. The checks use builtins over the
+    id list: with per-id Python checks and a pageable upload a 256-block request
+    took 69 us of host time, 31 us this way."""
     if not block_ids or raw_bytes <= 0 or raw_bytes % 2:
         return None
     if not _is_cuda(source) or source.device != getattr(out, "device", None):
@@ -261,12 +267,33 @@ def _decode_layout(source, out, block_ids, raw_bytes, torch):
     if count_words % (2 * count):
         return None
     block_words = count_words // (2 * count)
-    if contiguous:
-        return count_words, block_words, start, _stream_handle(out.device, torch), None, None
+    return count_words, block_words, start, _stream_handle(out.device, torch), contiguous
+
+
+def _decode_with_table(lib, host_name, device_name, block_ids, source, out, count_words,
+                       block_words, stream, tail, torch):
+    """Decode through a non-contiguous block table: in the kernel arguments when the
+    library takes the host list (up to HOST_TABLE_BLOCKS ids, tile geometry), else
+    from a device copy made asynchronously from pinned memory (recorded on the
+    current stream). `tail` = the arguments after the table. Returns the C result,
+    or None when no entry point is available."""
+    common = (int(source.data_ptr()), int(source.numel()), int(out.data_ptr()), count_words,
+              len(block_ids), block_words, int(out.stride(0)), int(out.stride(1)))
+    host_decode = getattr(lib, host_name, None)
+    if host_decode is not None and len(block_ids) <= HOST_TABLE_BLOCKS:
+        table = array.array("q", block_ids)
+        copied = host_decode(*common, table.buffer_info()[0], *tail, stream)
+        if copied != 0:
+            return copied
+    device_decode = getattr(lib, device_name, None)
+    if device_decode is None:
+        return None
     current = torch.cuda.current_stream(out.device)
     ids = torch.tensor(block_ids, dtype=torch.int64, pin_memory=True).to(out.device,
                                                                          non_blocking=True)
-    return count_words, block_words, start, int(current.cuda_stream), current, ids
+    copied = device_decode(*common, block_ids[0], int(ids.data_ptr()), *tail, stream)
+    ids.record_stream(current)
+    return copied
 
 
 def decode_fixed6(source, out, block_ids: list[int], raw_bytes: int) -> int | None:
@@ -279,18 +306,17 @@ def decode_fixed6(source, out, block_ids: list[int], raw_bytes: int) -> int | No
     layout = _decode_layout(source, out, block_ids, raw_bytes, torch)
     if layout is None:
         return None
-    count_words, block_words, start, stream, current, ids = layout
-    decode_blocks = getattr(lib, "kvq_splitzip_bf16_decode_fixed6_blocks", None)
-    if ids is not None and decode_blocks is None:
-        return None
-    common = (int(source.data_ptr()), int(source.numel()), int(out.data_ptr()), count_words,
-              len(block_ids), block_words, int(out.stride(0)), int(out.stride(1)), start)
-    if decode_blocks is not None:
-        copied = decode_blocks(*common, int(ids.data_ptr()) if ids is not None else 0, stream)
+    count_words, block_words, start, stream, contiguous = layout
+    if contiguous:
+        copied = decode(int(source.data_ptr()), int(source.numel()), int(out.data_ptr()),
+                        count_words, len(block_ids), block_words, int(out.stride(0)),
+                        int(out.stride(1)), start, stream)
     else:
-        copied = decode(*common, stream)
-    if ids is not None:
-        ids.record_stream(current)
+        copied = _decode_with_table(lib, "kvq_splitzip_bf16_decode_fixed6_host_blocks",
+                                    "kvq_splitzip_bf16_decode_fixed6_blocks", block_ids, source,
+                                    out, count_words, block_words, stream, (), torch)
+        if copied is None:
+            return None
     if copied < 0:
         _raise_last(lib, "splitzip cuda decode failed")
     return int(copied) or None
@@ -376,19 +402,18 @@ def decode_top16(source, out, block_ids: list[int], raw_bytes: int, layer_index:
     tables = _resolve_tables(layer_index, codebooks, source.device, torch)
     if tables is None:
         return None
-    count_words, block_words, start, stream, current, ids = layout
-    decode_blocks = getattr(lib, "kvq_splitzip_bf16_decode_top16_blocks", None)
-    if ids is not None and decode_blocks is None:
-        return None
-    common = (int(source.data_ptr()), int(source.numel()), int(out.data_ptr()), count_words,
-              len(block_ids), block_words, int(out.stride(0)), int(out.stride(1)), start)
-    if decode_blocks is not None:
-        copied = decode_blocks(*common, int(ids.data_ptr()) if ids is not None else 0,
-                               int(tables.data_ptr()), stream)
+    count_words, block_words, start, stream, contiguous = layout
+    if contiguous:
+        copied = decode(int(source.data_ptr()), int(source.numel()), int(out.data_ptr()),
+                        count_words, len(block_ids), block_words, int(out.stride(0)),
+                        int(out.stride(1)), start, int(tables.data_ptr()), stream)
     else:
-        copied = decode(*common, int(tables.data_ptr()), stream)
-    if ids is not None:
-        ids.record_stream(current)
+        copied = _decode_with_table(lib, "kvq_splitzip_bf16_decode_top16_host_blocks",
+                                    "kvq_splitzip_bf16_decode_top16_blocks", block_ids, source,
+                                    out, count_words, block_words, stream,
+                                    (int(tables.data_ptr()),), torch)
+        if copied is None:
+            return None
     if copied < 0:
         _raise_last(lib, "splitzip top16 decode failed")
     return int(copied) or None
