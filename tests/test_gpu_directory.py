@@ -181,19 +181,33 @@ def test_directory_of_shuffled_lists_and_overflow(sz, codebooks):
 
 
 def test_directory_declines_without_the_tile_layout(sz, codebooks):
+    """A directory needs the tile kernels: a KV layer 2 bytes off 16-byte alignment
+    (generic kernels) or a directory one word short is declined. Payload sections
+    at odd byte offsets do take the tile kernels, directory included."""
     say("directory declines")
     books = codebooks[:32]
     batch = sz.PagedBatch([[0, 1], [2]], 2048, "cuda")
-    kv = torch.zeros((2, 4, 16, 1, 128), dtype=torch.bfloat16, device="cuda")
     ws = batch.new_workspace()
     directory = batch.new_directory()
-    # payload sections not 16-byte aligned: the tile kernels (and a directory) are out
-    out = torch.zeros(batch.out_bytes + 16, dtype=torch.uint8, device="cuda")[3:]
-    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books, directory=directory) is None
-    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books) == batch.total_encoded_bytes
-    assert sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, kv, batch,
-                                 codebooks=books, directory=directory) is None
-    short = torch.zeros(batch.directory_bytes() - 4, dtype=torch.uint8, device="cuda")
     aligned = batch.new_payload_buffer()
+    backing = torch.zeros(2 * 4 * 2048 + 1, dtype=torch.bfloat16, device="cuda")
+    kv_off = backing[1:].view(2, 4, 2048)
+    assert sz.encode_top16_paged(kv_off, batch, aligned, ws, codebooks=books,
+                                 directory=directory) is None
+    assert sz.encode_top16_paged(kv_off, batch, aligned, ws, codebooks=books) == \
+        batch.total_encoded_bytes
+    assert sz.decode_top16_paged(aligned, batch.out_offsets, batch.encoded_bytes, kv_off, batch,
+                                 codebooks=books, directory=directory) is None
+    words = random_words(np.random.default_rng(8), 2 * 4 * 2048, books, 0.003)
+    kv = bf16(words).view(2, 4, 16, 1, 128)
+    short = torch.zeros(batch.directory_bytes() - 4, dtype=torch.uint8, device="cuda")
     assert sz.encode_top16_paged(kv, batch, aligned, ws, codebooks=books, directory=short) is None
+    out = torch.zeros(batch.out_bytes + 16, dtype=torch.uint8, device="cuda")[3:]
+    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books, directory=directory) == \
+        batch.total_encoded_bytes
+    target = torch.full_like(kv, 1.0)
+    assert sz.decode_top16_paged(out, batch.out_offsets, batch.encoded_bytes, target, batch,
+                                 codebooks=books, directory=directory) == batch.total_raw_bytes
     torch.cuda.synchronize()
+    assert torch.equal(target[:, :3].view(torch.int16), kv[:, :3].view(torch.int16))
+    assert bool((target[:, 3] == 1.0).all())
