@@ -22,7 +22,7 @@
 //   top16_encode_lanes<fast, sequential>  any geometry: 16 consecutive words per
 //       lane (stores realigned through neighbour-lane shuffles); or one workgroup
 //       walking every tile in order.
-//   top16_encode_finalize    per payload (8 or 16 workgroups): scan tile counts,
+//   top16_encode_finalize    per payload (8, 16 or 32 workgroups): scan tile counts,
 //       place escapes in ascending order, write the header (the tile kernel
 //       zeroes the escape slots of its span).
 //   top16_decode_tile / top16_decode_lanes / top16_decode_generic
@@ -67,6 +67,7 @@ namespace {
 // workgroups: Llama-3-70B TP8 encode call 73.5 -> 72.9 us with 8 for its largest
 // payloads of 2048 tiles)
 constexpr unsigned int kFinLargeTiles = 4096;
+constexpr int kFinPresenceGroups = 32;
 constexpr int kFinPreload = 8;                         // staged escapes loaded with the counts
 // Dense tiles (more staged escapes than the preload) placed per wave pass by the
 // finalize: 2 normally; 8 after a presence-mask encode, the variant for a layer
@@ -1381,7 +1382,11 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     max_tiles = std::max(max_tiles, end - a.p[r].tile_begin);
   }
   const bool large = max_tiles >= kFinLargeTiles;
-  const dim3 fin_grid(a.payload_count * (large ? 16 : 8));
+  // a presence-mask encode (a layer that overflowed before: dense tiles
+  // everywhere) spreads its placement over 32 groups per payload: 1 % outlier
+  // layer encode call 109.2 -> 105.8 us (16 groups: 106.5 us)
+  const dim3 fin_grid(a.payload_count *
+                      (a.presence && !a.inbody_slots ? kFinPresenceGroups : large ? 16 : 8));
   if (a.inbody_slots) {
     if (large)
       hipLaunchKernelGGL((top16_encode_finalize<16, true, kDenseItemsSparse>), fin_grid, block, 0,
@@ -1390,12 +1395,8 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
       hipLaunchKernelGGL((top16_encode_finalize<8, true, kDenseItemsSparse>), fin_grid, block, 0,
                          stream, a);
   } else if (a.presence) {
-    if (large)
-      hipLaunchKernelGGL((top16_encode_finalize<16, false, kDenseItemsDense>), fin_grid, block, 0,
-                         stream, a);
-    else
-      hipLaunchKernelGGL((top16_encode_finalize<8, false, kDenseItemsDense>), fin_grid, block, 0,
-                         stream, a);
+    hipLaunchKernelGGL((top16_encode_finalize<kFinPresenceGroups, false, kDenseItemsDense>),
+                       fin_grid, block, 0, stream, a);
   } else if (large) {
     hipLaunchKernelGGL((top16_encode_finalize<16, false, kDenseItemsSparse>), fin_grid, block, 0,
                        stream, a);
