@@ -652,6 +652,82 @@ def python_decoder_rate(w, words: int = 1 << 20):
             "raw_GBps": round(2 * sample.size / elapsed / 1e9, 6), "threads": 1}
 
 
+def time_dropin_fixed6(torch, sz, w, reps: int = 3):
+    """The reference connector's per-request fallback for an overflowed request:
+    gather by index_select, encode_bf16 (fixed6) into a raw-sized buffer, and
+    decode_fixed6 of each payload into the receiver's blocks; for the overflowed
+    requests of layer 0, checked against the batched fixed6 payloads and the
+    source blocks."""
+    plan = w["plan"][0]
+    if not plan["over"]:
+        return {"skipped": "layer 0 has no overflowed payload"}
+    send, recv = w["send"], w["recv"]
+    kv = w["kv"][0]
+    stream = torch.cuda.current_stream(w["device"])
+    members = list(plan["over"])
+    ids = [torch.tensor(send.block_tables[r], dtype=torch.int64, device=w["device"])
+           for r in members]
+    sources = [kv.index_select(1, i) for i in ids]
+    outs = [torch.empty(send.raw_bytes[r], dtype=torch.uint8, device=w["device"])
+            for r in members]
+    target = torch.zeros_like(kv)
+
+    def encode_all(gather: bool):
+        for k, r in enumerate(members):
+            src = kv.index_select(1, ids[k]) if gather else sources[k]
+            if sz.encode_bf16(src, outs[k], bits=6) != plan["sizes"][k]:
+                raise RuntimeError("drop-in fixed6 encode declined")
+
+    def decode_all():
+        for k, r in enumerate(members):
+            got = sz.decode_fixed6(outs[k][:plan["sizes"][k]], target, recv.block_tables[r],
+                                   send.raw_bytes[r])
+            if got != send.raw_bytes[r]:
+                raise RuntimeError("drop-in fixed6 decode declined")
+
+    def timed(fn, *a):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        runs = []
+        for _ in range(reps):
+            hold_queue(torch)
+            e0.record(stream)
+            fn(*a)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            runs.append(e0.elapsed_time(e1))
+        return statistics.median(runs)
+
+    encode_all(False)
+    decode_all()
+    torch.cuda.synchronize()
+    for k, r in enumerate(members):
+        off, size = plan["offsets"][k], plan["sizes"][k]
+        if not torch.equal(outs[k][:size], plan["buffer"][off:off + size]):
+            raise RuntimeError("drop-in fixed6 payload differs from the batched one")
+        dst = torch.tensor(recv.block_tables[r], dtype=torch.int64, device=w["device"])
+        if not torch.equal(kv.view(torch.int16).index_select(1, ids[k]),
+                           target.view(torch.int16).index_select(1, dst)):
+            raise RuntimeError("drop-in fixed6 round trip differs")
+    raw = sum(send.raw_bytes[r] for r in members)
+    ms_gather_enc = timed(encode_all, True)
+    ms_enc = timed(encode_all, False)
+    ms_dec = timed(decode_all)
+
+    def rate(ms):
+        return round(raw / (ms * 1e-3) / 1e9, 2)
+
+    return {
+        "requests": len(members),
+        "gather_encode_ms_per_request": round(ms_gather_enc / len(members), 5),
+        "encode_ms_per_request": round(ms_enc / len(members), 5),
+        "encode_raw_GBps": rate(ms_enc),
+        "decode_ms_per_request": round(ms_dec / len(members), 5),
+        "decode_raw_GBps": rate(ms_dec),
+        "layout": "payload at the start of a raw-sized uint8 buffer (low bytes 65 bytes in); "
+                  "gather by index_select as the reference connector",
+    }
+
+
 def time_dropin(torch, sz, w, reps: int = 3):
     """The reference-ABI per-request path an unchanged reference connector takes:
     index_select gather of a request's blocks into a packed copy, encode_top16 into
@@ -1333,6 +1409,8 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
                                                                 args.cpu_baseline_seconds),
                             "python_decoder": python_decoder_rate(w)}
             result["cpu_baseline"] = base
+    if w["plan"][0]["over"]:
+        result["dropin_fixed6_per_request"] = time_dropin_fixed6(torch, sz, w)
     return result
 
 
@@ -1344,7 +1422,7 @@ def _sub_summary(result: dict) -> dict:
             "compression_ratio", "escapes_per_layer", "overflowed_payloads", "roofline",
             "verified", "ms_per_layer_call", "escape_fraction",
             "max_rel_error_vs_decode_then_attend", "decode_only_ms_per_layer", "mfma_TFLOPs",
-            "dtype", "data")
+            "dtype", "data", "dropin_fixed6_per_request")
     return {k: result[k] for k in keep if k in result}
 
 
