@@ -44,3 +44,38 @@ def test_small_totals_stay_on_the_calling_thread():
     assert copier._pool is None
     for at, src in pieces:
         assert bytes(dst[at:at + len(src)]) == bytes(src)
+
+
+def test_streamed_copy_reports_each_finished_prefix_in_order():
+    """copy_streamed hands out ascending, contiguous ranges from 0 to the end, each
+    at least the window long except the last, and every byte of a range is in
+    place when the range is reported (what lets the connector start a range's
+    host-to-device copy while later payloads are still being copied)."""
+    rng = np.random.default_rng(5)
+    sizes = [9 << 20, 1, (5 << 20) + 3, 4 << 20, 12345, 7 << 20]
+    pieces, end = _pieces(rng, sizes)
+    expected = np.full(end, 9, np.uint8)
+    for at, src in pieces:
+        expected[at:at + len(src)] = np.frombuffer(src, np.uint8)
+    dst = np.full(end, 9, np.uint8)
+    ranges = []
+
+    def on_ready(lo, hi):
+        assert np.array_equal(dst[lo:hi], expected[lo:hi]), (lo, hi)
+        ranges.append((lo, hi))
+
+    HostCopier(threads=4).copy_streamed(dst, pieces, on_ready, end=end, window=6 << 20)
+    assert ranges[0][0] == 0 and ranges[-1][1] == end
+    assert all(a[1] == b[0] for a, b in zip(ranges, ranges[1:]))
+    assert all(hi - lo >= 6 << 20 for lo, hi in ranges[:-1])
+    assert len(ranges) > 2
+    assert np.array_equal(dst, expected)
+
+
+def test_streamed_copy_of_a_small_total_reports_one_range():
+    rng = np.random.default_rng(6)
+    pieces, end = _pieces(rng, [100, 2000])
+    got = []
+    dst = np.zeros(end, np.uint8)
+    HostCopier(threads=4).copy_streamed(dst, pieces, lambda lo, hi: got.append((lo, hi)))
+    assert got == [(0, pieces[-1][0] + 2000)]

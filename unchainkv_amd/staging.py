@@ -125,13 +125,27 @@ class HostCopier:
 
     def copy(self, dst, pieces) -> None:
         """dst: writable uint8 numpy array; pieces: (offset in dst, bytes-like)."""
+        self.copy_streamed(dst, pieces, None)
+
+    def copy_streamed(self, dst, pieces, on_ready, end: int | None = None,
+                      window: int = 16 << 20) -> None:
+        """copy() that also calls ``on_ready(lo, hi)`` on the calling thread each
+        time a further prefix of ``dst`` holds its bytes: ascending, contiguous
+        ranges of at least ``window`` bytes from 0, the last one ending at ``end``
+        (default: the end of the last piece; bytes between pieces are whatever
+        ``dst`` held). A device copy of each range can then run while later pieces
+        are still being copied. ``pieces`` must be in ascending offset order."""
         import numpy as np
 
+        if end is None:
+            end = max((at + len(src) for at, src in pieces), default=0)
         total = sum(len(src) for _, src in pieces)
         if total < self.PARALLEL_BYTES or self.threads == 1:
             view = memoryview(dst)
             for at, src in pieces:
                 view[at:at + len(src)] = src
+            if on_ready is not None and end > 0:
+                on_ready(0, end)
             return
         jobs = []
         for at, src in pieces:
@@ -139,11 +153,22 @@ class HostCopier:
             for lo in range(0, arr.size, self.PIECE):
                 hi = min(lo + self.PIECE, arr.size)
                 jobs.append((at + lo, arr[lo:hi]))
+        if any(jobs[k + 1][0] < jobs[k][0] for k in range(len(jobs) - 1)):
+            raise ValueError("pieces must be in ascending offset order")
 
         def run(job):
             at, arr = job
             np.copyto(dst[at:at + arr.size], arr)
 
-        for _ in self._executor().map(run, jobs):
-            pass
+        pool = self._executor()
+        futures = [pool.submit(run, job) for job in jobs]
+        issued = 0
+        for (at, arr), fut in zip(jobs, futures):
+            fut.result()  # in order: every earlier job has finished too
+            done = at + arr.size
+            if on_ready is not None and done - issued >= window:
+                on_ready(issued, done)
+                issued = done
+        if on_ready is not None and end > issued:
+            on_ready(issued, end)
 
