@@ -441,3 +441,40 @@ def test_restore_of_reference_ordered_escapes_through_the_host_directory(sz, cod
     src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
     for t, rt in zip(tables, recv):
         assert np.array_equal(dst[:, rt], src[:, t])
+
+
+def test_restore_streams_large_batches_and_resends_sorted_escape_lists(sz, codebooks):
+    """About 22 MB of Top-16 payloads in one restore: the staging buffer goes to the
+    GPU in several ranges while later payloads are still being staged, and the
+    escape lists that arrive in atomic order (two of the payloads, one in the first
+    range and one in the last) are sorted by the host directory build after their
+    range has left, so they go up again. Every block is restored exactly."""
+    say("connector restore, streamed ranges")
+    books = codebooks[9 * 32:10 * 32]
+    rng = np.random.default_rng(23)
+    pool = 9 * 48
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.002), pool)
+    tables = disjoint_tables(rng, pool, [48] * 9)
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=RecordingTrace())
+    payloads = codec.ready(codec.save_kv_layer(9, kv, tables))
+    assert sum(p.encoded_bytes for p in payloads) > 16 << 20  # more than one range
+    sent = []
+    for k, p in enumerate(payloads):
+        data = bytearray(p.view)
+        if k in (0, 8):
+            n = p.raw_bytes // 2
+            lo, _ = codec_format.top16_sections(n)["escapes"]
+            count = int.from_bytes(data[1:5], "little")
+            assert count > 100
+            entries = [bytes(data[lo + 5 * i:lo + 5 * i + 5]) for i in range(count)]
+            data[lo:lo + 5 * count] = b"".join(entries[i] for i in rng.permutation(count))
+        sent.append(bytes(data))
+    target = torch.zeros_like(kv)
+    recv = [[(b + 5) % pool for b in t] for t in tables]
+    requests = [(rt, data, p.metadata(9, BW)) for rt, data, p in zip(recv, sent, payloads)]
+    assert codec.load_kv_layer_batch(9, target, requests) == [(len(t), 4 * len(t) * BW)
+                                                              for t in tables]
+    torch.cuda.synchronize()
+    src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
+    for t, rt in zip(tables, recv):
+        assert np.array_equal(dst[:, rt], src[:, t])
