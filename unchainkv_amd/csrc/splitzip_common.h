@@ -20,9 +20,6 @@ constexpr int kWordsPerLane = 16;
 constexpr int kTileWords = kThreads * kWordsPerLane;  // 4096 words per workgroup tile
 constexpr int kTileShift = 12;
 static_assert((1 << kTileShift) == kTileWords, "tile size");
-// Chunk kernels (aligned sections): a lane handles 8-word chunks so that one
-// vector memory instruction of a wave covers 64 consecutive chunks.
-constexpr int kChunkWords = 8;
 
 // Escapes staged per tile by the encode kernel (3.1% of a 4096-word tile, three
 // times the 0.5% escape capacity of a payload, so that a payload with 1% outliers
