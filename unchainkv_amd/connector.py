@@ -187,6 +187,9 @@ class SplitzipLayerCodec:
         self.pinned = PinnedPool(config.host_mirror_bytes, config.host_mirror_layers)
         self.copy_streams = CopyStreams()
         self.host_copier = HostCopier()
+        # batches by block tables: a request keeps its block ids in every layer, so
+        # a step's layers share them (built once, ids uploaded once)
+        self._batches: dict = {}
 
     # ------------------------------------------------------------------
     # library
@@ -304,7 +307,7 @@ class SplitzipLayerCodec:
         mask in ``pending.presence``; a palette group whose members all have masks
         there starts from them instead of reading the blocks once more."""
         sz = self._lib()
-        batch = sz.PagedBatch([p.block_ids for p in members], block_words, kv_layer.device)
+        batch = self._batch([p.block_ids for p in members], block_words, kv_layer.device)
         if kind == BITS_TOP16:
             tables = self._top16_tables(layer_index, kv_layer.device)
             if tables is None:
@@ -335,6 +338,20 @@ class SplitzipLayerCodec:
         got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind,
                                    **masks)
         return (out, offsets, sizes, batch) if got else None
+
+    BATCH_CACHE = 16
+
+    def _batch(self, tables, block_words: int, device):
+        """PagedBatch of these block tables, reused while they recur (the most recent
+        BATCH_CACHE table sets are kept)."""
+        key = (tuple(tuple(t) for t in tables), block_words, str(device))
+        batch = self._batches.pop(key, None)
+        if batch is None:
+            batch = self._lib().PagedBatch([list(t) for t in tables], block_words, device)
+            if len(self._batches) >= self.BATCH_CACHE:
+                self._batches.pop(next(iter(self._batches)))
+        self._batches[key] = batch  # most recent last
+        return batch
 
     def _host_buffer(self, nbytes: int, torch):
         """(pinned host tensor of nbytes, its pool buffer): from the pool, or a fresh
@@ -754,7 +771,7 @@ class SplitzipLayerCodec:
                 start = -(-(end + header[mode]) // 256) * 256 - header[mode]
                 layout.append((mode, member, start))
                 end = start + len(member[3])
-        batches = {mode: sz.PagedBatch([m[1] for m in members], block_words, kv_layer.device)
+        batches = {mode: self._batch([m[1] for m in members], block_words, kv_layer.device)
                    for mode, members in groups.items()}
         # the Top-16 payloads' escape directory rides along in the same copy, so
         # their decode is one kernel
