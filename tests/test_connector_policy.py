@@ -330,3 +330,34 @@ def test_two_chunk_rule_and_kvc2_frames():
         assert (f.block_count, f.raw_block_size, f.raw_bytes) == (4, 2 * bw * 2, 4 * 2 * bw * 2)
         assert bytes(f.payload) == bytes(halves[k].view)
     assert (parsed[2].chunks_in_layer, parsed[2].block_count, parsed[2].request_id) == (1, 1, "req-b")
+
+
+def test_batches_are_reused_for_recurring_block_tables():
+    """The codec builds one PagedBatch per block-table set and reuses it while the
+    set recurs (a request keeps its block ids in every layer); the least recently
+    used set goes once more than BATCH_CACHE sets are held."""
+    built = []
+
+    class FakeLib:
+        def available(self):
+            return True
+
+        def PagedBatch(self, tables, block_words, device):
+            built.append((tuple(map(tuple, tables)), block_words, device))
+            return SimpleNamespace(tables=tables)
+
+    c = SplitzipLayerCodec(CodecConfig(), trace=RecordingTrace(), lib=FakeLib())
+    a = c._batch([[1, 2], [7]], 2048, "cuda:0")
+    assert c._batch([[1, 2], [7]], 2048, "cuda:0") is a
+    assert c._batch([(1, 2), (7,)], 2048, "cuda:0") is a    # same ids, any sequence type
+    assert c._batch([[1, 2], [7]], 1024, "cuda:0") is not a  # other geometry
+    assert c._batch([[1, 2], [7]], 2048, "cuda:1") is not a  # other device
+    assert len(built) == 3
+    for k in range(c.BATCH_CACHE):
+        c._batch([[100 + k]], 2048, "cuda:0")
+    assert len(c._batches) == c.BATCH_CACHE
+    before = len(built)
+    c._batch([[1, 2], [7]], 2048, "cuda:0")  # evicted meanwhile: built again
+    assert len(built) == before + 1
+    c._batch([[100 + c.BATCH_CACHE - 1]], 2048, "cuda:0")  # still held
+    assert len(built) == before + 1
