@@ -165,9 +165,9 @@ unsigned long long kvq_splitzip_top16_paged_directory_bytes(
  * workspace must hold kvq_splitzip_top16_paged_workspace_bytes() bytes.
  * directory_ptr: 0, or a 16-byte aligned device buffer of
  * kvq_splitzip_top16_paged_directory_bytes() bytes that receives the escape
- * directory (declined unless block_words is a multiple of 1024 and every body
- * section is 16-byte aligned: (out + out_offsets[r] + 5) % 16 == 0). Returns the
- * sum of the encoded sizes, or 0 when a precondition fails. */
+ * directory (declined unless block_words is a multiple of 1024 and tables_ptr is
+ * 4-byte aligned; payloads may start at any byte address). Returns the sum of the
+ * encoded sizes, or 0 when a precondition fails. */
 long long kvq_splitzip_bf16_encode_top16_paged(
     unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
     unsigned long long block_words, unsigned long long block_ids_ptr,
