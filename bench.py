@@ -60,6 +60,10 @@ SUB_STEPS = 10
 # 20, 156.1 over 40, measured standalone), so the longer region reports its steady
 # state
 SUB_STEPS_ATTENTION = 40
+# configurations whose ride-along summary also carries the C oracle's CPU rate (the
+# small contiguous model and the mixed-context share), each on a bounded sample
+SUB_CPU_BASELINE = ("llama32-1b-contiguous", "llama3-70b-tp8-mixed")
+SUB_CPU_SECONDS = 4.0
 
 
 def parse_args():
@@ -1246,7 +1250,8 @@ def run_attention(args, torch, sz, workloads, headline: bool = True):
 def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
     """One codec workload (encode + decode of every layer per step); the JSON object
     of its run. The headline run adds the histogram, writeback, graph replay,
-    drop-in, overlap and CPU-baseline legs."""
+    drop-in, overlap and CPU-baseline legs; the ride-along runs of SUB_CPU_BASELINE
+    add the C oracle's CPU rate on a short sample."""
     from unchainkv_amd import codec_format
 
     w = build_workload(torch, sz, workloads, name, args.seed)
@@ -1414,6 +1419,8 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
                                                                 args.cpu_baseline_seconds),
                             "python_decoder": python_decoder_rate(w)}
             result["cpu_baseline"] = base
+    elif name in SUB_CPU_BASELINE and not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, w, 1, SUB_CPU_SECONDS)
     if w["plan"][0]["over"]:
         result["dropin_fixed6_per_request"] = time_dropin_fixed6(torch, sz, w)
     return result
@@ -1427,7 +1434,7 @@ def _sub_summary(result: dict) -> dict:
             "compression_ratio", "escapes_per_layer", "overflowed_payloads", "roofline",
             "verified", "ms_per_layer_call", "escape_fraction",
             "max_rel_error_vs_decode_then_attend", "decode_only_ms_per_layer", "mfma_TFLOPs",
-            "dtype", "data", "dropin_fixed6_per_request")
+            "dtype", "data", "dropin_fixed6_per_request", "cpu_baseline")
     return {k: result[k] for k in keep if k in result}
 
 
