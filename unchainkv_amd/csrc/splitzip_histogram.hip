@@ -223,7 +223,9 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_generic(HistArgs a) {
 
 // Sums the partials into 64-bit counts. Workgroup w owns bins [16w, 16w + 16); its
 // threads split the groups into 16 slices (each row of 16 bins is one 64-byte
-// segment) and keep eight loads in flight, then add the slices in LDS.
+// segment) and keep sixteen loads in flight (one round for a grid of 256 partials:
+// Llama-3-8B call 28.5 -> 28.1 us against two rounds of eight), then add the slices
+// in LDS.
 constexpr unsigned int kReduceBins = 16;
 constexpr unsigned int kReduceSlices = kThreads / kReduceBins;
 
@@ -235,13 +237,13 @@ __global__ __launch_bounds__(kThreads) void exponent_hist_reduce(const unsigned 
   const unsigned int slice = threadIdx.x / kReduceBins;
   unsigned long long s = 0;
   unsigned int g = slice;
-  for (; g + 7 * kReduceSlices < groups; g += 8 * kReduceSlices) {
-    unsigned int v[8];
+  for (; g + 15 * kReduceSlices < groups; g += 16 * kReduceSlices) {
+    unsigned int v[16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < 16; ++k)
       v[k] = partial[(unsigned long long)(g + k * kReduceSlices) * 2 * kBins + bin];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s += v[k];
+    for (int k = 0; k < 16; ++k) s += v[k];
   }
   for (; g < groups; g += kReduceSlices) s += partial[(unsigned long long)g * 2 * kBins + bin];
   s_sum[threadIdx.x] = s;
