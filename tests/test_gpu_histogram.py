@@ -44,6 +44,8 @@ def bincount_planes(kv_host, tables):
     (16384, 12, [[11, 2, 5, 0, 9]], 0),                      # chunk kernel, Llama-3-8B blocks
     (48, 200, [list(range(0, 200, 3)), [199, 1]], 0),        # generic kernel
     (2048, 24, [[5, 6, 5], [23]], 1),                        # misaligned layer, repeated block
+    (1024, 64, [list(range(1, 64, 2)) + [0], [9, 4, 60]], 0),  # odd chunk count (36 blocks)
+    (16384, 520, [list(range(519, 6, -1))], 0),              # many batches per wave (513 blocks)
 ])
 def test_histogram_matches_bincount(sz, bw, pool, tables, offset):
     say("histogram", bw, pool, offset)

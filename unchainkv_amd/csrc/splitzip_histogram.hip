@@ -9,8 +9,8 @@
 //
 // Two kernels, no global atomics, deterministic output:
 //   exponent_hist_partial: 512-thread workgroups, about one per CU; each wave
-//     streams batches of four 1024-word chunks, two batches in flight (block ids
-//     fetched a batch ahead), eight batches per wave, and adds every word's
+//     streams batches of two 1024-word chunks, two batches in flight (block ids
+//     fetched a batch ahead), sixteen batches per wave, and adds every word's
 //     exponent into the workgroup's LDS histogram. Lane l counts into copy l % 16
 //     of the histogram, two 16-bit bins per dword, copy c in bank c: of the 32
 //     lanes an LDS instruction serves at once only lanes l and l + 16 can meet on
@@ -18,8 +18,9 @@
 //     atomics serialise). A chunk's 16 addresses per lane are computed before its
 //     16 LDS adds, so the adds go out back to back. The 16 KiB histogram leaves
 //     the CU's LDS and registers to deep streaming (Llama-3-8B layer: 64 copies
-//     and twelve-chunk batches 42.2 us, this layout 28.2 us). The workgroup then
-//     writes one 512-bin partial (K bins, then V bins).
+//     and twelve-chunk batches 42.2 us, four-chunk batches 28.2 us, two-chunk
+//     batches 26.3 us: as fast as the same loop with no LDS adds at all). The
+//     workgroup then writes one 512-bin partial (K bins, then V bins).
 //   exponent_hist_reduce: sums the partials into 64-bit counts, every bin's
 //     groups split over sixteen threads.
 // Layouts that the chunk kernel cannot take (block words not a multiple of 1024,
@@ -41,11 +42,12 @@ constexpr int kCopies = 16;                    // lane l counts into copy l % 16
 constexpr int kChunk = 1024;                   // words per wave step (one block)
 constexpr unsigned int kMaxPartials = 2048;    // workgroups of the partial kernel
 
-// Chunks per wave step: 8 KiB of loads per wave, two steps in flight.
-constexpr int kBatch = 4;
+// Chunks per wave step: 4 KiB of loads per wave, two steps in flight (63 VGPRs;
+// Llama-3-8B call with 1, 2, 3, 4 and 6 chunks: 26.4, 26.3, 27.5, 28.1, 32.1 us).
+constexpr int kBatch = 2;
 // Threads of a partial-kernel workgroup and wave steps per wave (the grid size).
 constexpr int kHistThreads = 512;
-constexpr int kBatchesPerWave = 8;
+constexpr int kBatchesPerWave = 16;
 
 struct HistArgs {
   const uint16_t* kv;
@@ -276,8 +278,9 @@ unsigned int partial_groups(unsigned long long block_count, unsigned long long b
   const unsigned long long words = 2 * block_count * block_words;
   unsigned long long g;
   if (chunked) {
-    // about eight batches per wave (per-layer call, Llama-3-8B: 4 -> 30.1 us,
-    // 8 -> 28.2, 16 -> 42.4 with too few workgroups to fill the GPU), rounded to
+    // about 32 chunks per wave (per-layer call, Llama-3-8B, four-chunk batches:
+    // 4 batches per wave 30.1 us, 8 28.2, 16 42.4 with too few workgroups to fill
+    // the GPU; two-chunk batches: 16 per wave 26.3 us, 8 27.5), rounded to
     // whole rounds of one workgroup per CU (Llama-3-70B TP8 layer: 381 workgroups
     // 48.9 us, 256 40.4 us, 512 41.8 us); a small layer still spreads over up to
     // 64 workgroups, one batch per wave
