@@ -812,9 +812,9 @@ class SplitzipLayerCodec:
             else:
                 host_np[dir_at:dir_at + dir_bytes] = built
                 upload(dir_at, dir_at + dir_bytes)
-                for lo, hi, before in lists:
-                    if (before != host_np[lo:hi]).any():
-                        upload(lo, hi)
+            for lo, hi, before in lists:
+                if (before != host_np[lo:hi]).any():
+                    upload(lo, hi)
         if slot is not None:
             # back to the pool at once: reused after the host-to-device copy ends
             slot.event = torch.cuda.Event()
