@@ -3,9 +3,11 @@ block sizes of 1 to 16 KiB words, one to five requests of 1 to 12 blocks, payloa
 buffers at every byte offset mod 16, escape rates from none to overflow. Every
 payload is compared byte for byte with the oracle's, every decode with the source
 words (through the host block table, the device table and the escape directory).
+UNCHAIN_KV_TEST_SEEDS sets the number of seeds (16 by default).
 """
 
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -47,7 +49,11 @@ def words_for(rng, n, books, rate):
             rng.integers(0, 128, n).astype(np.uint16)).astype(np.uint16)
 
 
-@pytest.mark.parametrize("seed", range(16))
+# more seeds for a wider sweep: UNCHAIN_KV_TEST_SEEDS=<count>
+SEEDS = int(os.environ.get("UNCHAIN_KV_TEST_SEEDS", "16"))
+
+
+@pytest.mark.parametrize("seed", range(SEEDS))
 def test_seeded_shapes(sz, codebooks, seed):
     rng = np.random.default_rng(1000 + seed)
     bw = int(rng.choice([1024, 2048, 3072, 8192, 16384]))
