@@ -9,6 +9,8 @@ followed by float32 attention. Tolerance: 1e-2 relative to each output row's
 largest magnitude (bf16 output and bf16 softmax weights).
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -20,6 +22,8 @@ pytestmark = pytest.mark.gpu
 
 HEAD_DIM = 128
 TOL = 1e-2
+# seeds of the shape sweep below (UNCHAIN_KV_TEST_SEEDS=<count> for a wider one)
+SEEDS = int(os.environ.get("UNCHAIN_KV_TEST_SEEDS", "16"))
 
 
 @pytest.fixture(scope="module")
@@ -122,6 +126,36 @@ def test_fused_attention_matches_oracle_decode_then_attend(sz, codebooks, kv_hea
         assert payload[0] == 5
         decoded = oracle.top16_decode(payload, w.size, tables)
         assert np.array_equal(decoded, w.reshape(-1))  # the exact decode the kernel must match
+        kv = bf16_to_f64(decoded).reshape(2, span_of(t), kv_heads, HEAD_DIM)[:, :t]
+        check_close(got[b], attention_f64(q64[b], kv[0], kv[1]))
+
+
+@pytest.mark.parametrize("seed", range(SEEDS))
+def test_seeded_attention_shapes(sz, codebooks, seed):
+    """Seeded sweep: 1, 2, 4 or 8 kv heads, one to six sequences of 1 to 3000
+    tokens (partial last blocks included), escape rates up to 0.4 %, any layer's
+    codebooks; every output row within the tolerance of the oracle's decode
+    followed by float64 attention."""
+    rng = np.random.default_rng(9000 + seed)
+    kv_heads = int(rng.choice([1, 2, 4, 8]))
+    contexts = rng.integers(1, 3001, int(rng.integers(1, 7))).tolist()
+    rate = float(rng.choice([0.0, 0.001, 0.004]))
+    layer = int(rng.integers(0, 32))
+    say("seeded attention", seed, kv_heads, contexts, rate, layer)
+    books = codebooks[32 * layer:32 * layer + 32]
+    tables = oracle.top16_tables(books)
+    words = [kv_words(rng, books, t, kv_heads, rate) for t in contexts]
+    payloads, batch = encode_sequences(sz, words, kv_heads, books)
+    q, q64 = random_q(rng, len(contexts), 4 * kv_heads)
+    out = sz.decode_attention_top16(q, payloads, batch.out_offsets, contexts, kv_heads,
+                                    codebooks=books)
+    torch.cuda.synchronize()
+    assert out is not None
+    got = out.float().cpu().numpy()
+    host = payloads.cpu().numpy()
+    for b, (w, t) in enumerate(zip(words, contexts)):
+        a = batch.out_offsets[b]
+        decoded = oracle.top16_decode(host[a:a + batch.encoded_bytes[b]], w.size, tables)
         kv = bf16_to_f64(decoded).reshape(2, span_of(t), kv_heads, HEAD_DIM)[:, :t]
         check_close(got[b], attention_f64(q64[b], kv[0], kv[1]))
 
