@@ -1,8 +1,10 @@
 """GPU decode + scatter of the reference connector's torch-op payloads (modes 0,
 1, 2) against the oracle: every width of each mode, odd sizes and block
 geometries, mixed modes in one launch with a refused header left unapplied, two
-launches, and the connector's restore of the reference tests' own inputs
-(tests/test_vllm_connector.py:2437-2549) into a (2, 16, 8) layer."""
+launches, the connector's restore of the reference tests' own inputs
+(tests/test_vllm_connector.py:2437-2549) into a (2, 16, 8) layer, and payloads the
+reference connector itself wrote or accepts (tests/golden/torchop_payloads.npz)
+decoded to the words the reference restored."""
 
 import numpy as np
 import pytest
@@ -167,3 +169,49 @@ def test_connector_restores_every_torchop_mode_in_one_call(sz):
     layer = u16(target).reshape(2, pool, bw)
     for ids, words in expect:
         assert np.array_equal(layer[:, ids].reshape(-1), words)
+
+
+def _golden_cases():
+    import json
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    index = json.loads((golden / "torchop_cases.json").read_text())["cases"]
+    with np.load(golden / "torchop_payloads.npz") as z:
+        arrays = {k: z[k] for k in z.files}
+    return [dict(c, payload=arrays.get(c["key"] + "_payload"), out=arrays.get(c["key"] + "_out"))
+            for c in index if c["kind"] in ("encode", "decode")
+            and arrays.get(c["key"] + "_payload") is not None]
+
+
+def test_reference_produced_payloads(sz):
+    """Payloads the reference connector wrote (its torch-op encoders and
+    hand-made ones its restore decoders accept or refuse; tests/golden/
+    make_torchop_golden.py) decode to the words the reference restored, one launch
+    per block geometry; refused payloads leave their blocks unapplied."""
+    groups = {}
+    for c in _golden_cases():
+        groups.setdefault(c["block_words"], []).append(c)
+    for bw, cases in sorted(groups.items()):
+        say("torchop golden", bw, len(cases))
+        requests = [c["blocks"] for c in cases]
+        items = [(c["payload"], None if c["declined"] else c["out"]) for c in cases]
+        got, expected = run_batch(sz, bw, sum(requests) + 5, requests, items)
+        assert np.array_equal(got, expected), bw
+
+
+def test_connector_restores_reference_produced_payloads(sz):
+    """The encoder fixtures through the connector's restore (host validation, one
+    pinned staging copy, the torch-op launch) into their own block spans."""
+    cases = [c for c in _golden_cases() if c["kind"] == "encode" and not c["declined"]]
+    say("torchop golden connector", len(cases))
+    for c in cases:
+        bw, nblk, start = c["block_words"], c["blocks"], c["start"]
+        codec = SplitzipLayerCodec(CodecConfig(), trace=RecordingTrace())
+        target = torch.zeros((2, start + nblk + 2, bw), dtype=torch.bfloat16, device="cuda")
+        meta = {"raw_bytes": 2 * c["n"], "encoded_bytes": int(c["payload"].size)}
+        ids = list(range(start, start + nblk))
+        got = codec.load_kv_layer_batch(0, target, [(ids, bytes(c["payload"]), meta)])
+        torch.cuda.synchronize()
+        assert got == [(nblk, 2 * c["n"])], c["name"]
+        assert np.array_equal(u16(target)[:, start:start + nblk].reshape(-1), c["out"]), c["name"]

@@ -64,6 +64,9 @@ class PinnedPool:
                 slot.leased = True
                 return slot
             size = -(-nbytes // GRANULE) * GRANULE
+            if self.cap_bytes and size > self.cap_bytes:
+                # no eviction could make room: keep the idle buffers for later layers
+                return None
 
             def over() -> bool:
                 return ((self.cap_buffers and len(self._slots) >= self.cap_buffers)
@@ -74,8 +77,6 @@ class PinnedPool:
                 if not idle:
                     return None
                 self._slots.remove(max(idle, key=lambda s: s.capacity))
-            if self.cap_bytes and size > self.cap_bytes:
-                return None
             slot = PinnedSlot(torch.empty(size, dtype=torch.uint8, pin_memory=True), leased=True)
             self._slots.append(slot)
             self.allocations += 1
