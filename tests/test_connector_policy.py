@@ -361,3 +361,60 @@ def test_batches_are_reused_for_recurring_block_tables():
     assert len(built) == before + 1
     c._batch([[100 + c.BATCH_CACHE - 1]], 2048, "cuda:0")  # still held
     assert len(built) == before + 1
+
+
+class _FakeEvent:
+    """A completed GPU event whose timestamp is ``ms``."""
+
+    def __init__(self, ms):
+        self.ms = ms
+
+    def synchronize(self):
+        pass
+
+    def query(self):
+        return True
+
+    def elapsed_time(self, end):
+        return end.ms - self.ms
+
+
+def test_payload_ready_carries_gpu_timing_under_trace_cuda():
+    """UNCHAIN_KV_TRACE_CUDA=1 adds the GPU time of the layer's encodes and copies
+    to the splitzip_payload_ready event (vllm_connector.py:473, 4634-4664): the sums
+    of the recorded (start, end) event pairs in seconds, each payload's bits and
+    fallback flag, and the time since the save hook began. Without it the event
+    carries the byte counts only."""
+    import numpy as np
+
+    from unchainkv_amd.connector import LayerPayload, PendingLayer
+
+    assert CodecConfig.from_env({"UNCHAIN_KV_TRACE_CUDA": "1"}).trace_cuda
+    assert not CodecConfig.from_env({}).trace_cuda
+    for traced in (True, False):
+        c, trace = codec(top16=True, trace_cuda=traced)
+        host = np.zeros(64, np.uint8)
+        host[0], host[32] = codec_format.MODE_TOP16, codec_format.MODE_FIXED6
+        payloads = [LayerPayload(0, [1], 2 * MIB, BITS_TOP16, BITS_TOP16, epoch=0,
+                                 encoded_bytes=20, _group=0, _offset=0),
+                    LayerPayload(1, [2], 2 * MIB, BITS_FIXED6, BITS_FIXED6,
+                                 encoded_bytes=24, _group=0, _offset=32)]
+        pending = PendingLayer(3, None, 16384, payloads, started=0.0)
+        pending.groups.append((host, _FakeEvent(9.0), None, None))
+        pending.timing += [("encode", _FakeEvent(1.0), _FakeEvent(1.25)),
+                           ("d2h", _FakeEvent(1.5), _FakeEvent(3.5)),
+                           ("encode", _FakeEvent(4.0), _FakeEvent(4.5)),
+                           ("d2h", _FakeEvent(5.0), _FakeEvent(5.5))]
+        got = c.ready(pending)
+        assert [bytes(p.view)[:1] for p in got] == [bytes([5]), bytes([3])]
+        row = next(f for name, f in trace.rows if name == "splitzip_payload_ready")
+        assert row["raw_bytes"] == 4 * MIB and row["encoded_bytes"] == 44
+        if traced:
+            assert row["encode_gpu_s"] == pytest.approx(0.00075)
+            assert row["d2h_gpu_s"] == pytest.approx(0.0025)
+            assert row["bits"] == [BITS_TOP16, BITS_FIXED6]
+            assert row["fallback"] == [False, False]
+            assert row["payload_elapsed_s"] > 0
+        else:
+            assert set(row) == {"layer", "raw_bytes", "encoded_bytes"}
+        assert not pending.timing

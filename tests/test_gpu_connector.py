@@ -160,6 +160,8 @@ def test_probe_after_an_overflow_reencodes_from_presence_masks(sz, codebooks):
         assert (p.probe, p.bits) == (probe, bits), step
         assert (pending.presence is not None) == probe, step
         assert (p._mask_first == 0) == probe, step
+        # the probe's payload is not copied before its mode byte is known
+        assert (not pending.groups and len(pending.deferred) == 1) == probe, step
         payloads = codec.ready(pending)
         assert pending.presence is None
         assert payloads[0].bits == BITS_FIXED6 and payloads[0].fallback == fallback, step
@@ -329,51 +331,61 @@ def test_sender_splits_fixed6_requests_into_two_kvc2_chunks(sz, codebooks):
 # ---------------------------------------------------------------------------
 # payload staging: copy stream and pinned pool (vllm_connector.py:3406-3458)
 
+SLEEP_CYCLES = 200_000_000  # about 0.1 s of GPU clock
+
+
+def _timed_event(stream):
+    event = torch.cuda.Event(enable_timing=True)
+    event.record(stream)
+    return event
+
+
 def _independent_stream(copy, candidates):
     """A candidate stream whose work is not held back by work on `copy`. HIP
     multiplexes a process's streams over a few hardware queues
-    (GPU_MAX_HW_QUEUES), and two streams on one queue run in submission order; a
-    spin on `copy` that outlasts a marker on the candidate shows separate queues."""
+    (GPU_MAX_HW_QUEUES), and two streams on one queue run in submission order. A
+    marker on the candidate, queued right after a long spin on `copy`, whose GPU
+    timestamp comes before the spin's end shows separate queues (event times, no
+    polling)."""
     for s in candidates:
         with torch.cuda.stream(copy):
-            torch.cuda._sleep(50_000_000)  # tens of milliseconds
-        marker = torch.cuda.Event()
-        marker.record(s)
-        while not marker.query():
-            pass
-        free = not copy.query()
-        copy.synchronize()
-        if free:
+            torch.cuda._sleep(SLEEP_CYCLES)
+            spin_end = _timed_event(copy)
+        marker = _timed_event(s)
+        torch.cuda.synchronize()
+        if marker.elapsed_time(spin_end) > 0:
             return s
     return None
 
 
 def test_payload_copy_runs_beside_the_forward_stream(sz, codebooks):
-    """A kernel queued on the forward stream right after save_kv_layer finishes
-    while the layer's device-to-host copy is still running: the copy is on its own
-    stream, which waits for the forward stream but holds nothing queued on it
-    later. The payloads still arrive whole."""
+    """Forward work queued after save_kv_layer does not wait for the layer's
+    device-to-host copy: the copy stream is held back by a long spin queued on it
+    first, and the GPU timestamps show a marker queued on the forward stream after
+    the save hook running before any copy of the layer starts (the copy waits for
+    the forward stream's work up to the save, nothing later). The payloads still
+    arrive whole."""
     say("connector staging overlap")
     books = codebooks[3 * 32:4 * 32]
     rng = np.random.default_rng(12)
     pool = 1100
     kv = layer_from_words(words_with_books(rng, books, pool, 0.0005), pool)
     tables = disjoint_tables(rng, pool, [256, 256, 256, 256])  # ~50 MB of payloads
-    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False))
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False, trace_cuda=True))
     copy = codec.copy_streams.get(kv.device, torch)
     forward = _independent_stream(copy, [torch.cuda.Stream() for _ in range(4)])
     assert forward is not None, "every candidate stream shares the copy stream's queue"
     torch.cuda.synchronize()
+    with torch.cuda.stream(copy):
+        torch.cuda._sleep(SLEEP_CYCLES)
     with torch.cuda.stream(forward):
         pending = codec.save_kv_layer(3, kv, tables)
-        marker = torch.cuda.Event()
-        marker.record(forward)                    # forward work after the save hook
-    # poll without sleeping: a blocking synchronize may wake the host late
-    while not marker.query():
-        pass
-    copies = [event for _, event, _, _ in pending.groups]
-    assert copies and not all(event.query() for event in copies)
+        marker = _timed_event(forward)            # forward work after the save hook
+    starts = [start for kind, start, _ in pending.timing if kind == "d2h"]
+    assert starts
     payloads = codec.ready(pending)
+    torch.cuda.synchronize()
+    assert all(marker.elapsed_time(start) > 0 for start in starts)
     tab = oracle.top16_tables(books)
     src = u16(kv).reshape(2, pool, BW)
     for t, p in zip(tables[:2], payloads[:2]):
@@ -478,3 +490,118 @@ def test_restore_streams_large_batches_and_resends_sorted_escape_lists(sz, codeb
     src, dst = u16(kv).reshape(2, pool, BW), u16(target).reshape(2, pool, BW)
     for t, rt in zip(tables, recv):
         assert np.array_equal(dst[:, rt], src[:, t])
+
+
+def _in_pool(codec, view):
+    """The pinned pool buffer that holds a payload's bytes, or None."""
+    addr = np.frombuffer(view, np.uint8).ctypes.data
+    for slot in codec.pinned._slots:
+        base = slot.tensor.data_ptr()
+        if base <= addr and addr + len(view) <= base + slot.capacity:
+            return slot
+    return None
+
+
+def _spy_copies(codec, monkeypatch):
+    """Records the stream of every staging copy the codec queues."""
+    used = []
+    begin = codec._begin_copies
+
+    def spy(device, torch_):
+        stream = begin(device, torch_)
+        used.append(stream)
+        return stream
+
+    monkeypatch.setattr(codec, "_begin_copies", spy)
+    return used
+
+
+def test_fallback_payloads_are_staged_on_the_copy_stream(sz, codebooks, monkeypatch):
+    """An overflowed Top-16 payload's fixed6 re-encode, and a fixed6 overflow's raw
+    mode-6 payload, reach the host like every other payload: copies queued on the
+    copy stream into pinned pool buffers (no blocking pageable copy), with the
+    bytes of the oracle."""
+    say("connector fallback staging")
+    books = codebooks[2 * 32:3 * 32]
+    rng = np.random.default_rng(31)
+    pool = 56
+    words = words_with_books(rng, books, pool, 0.0)
+    kv_host = words.reshape(2, pool, BW)
+    tables = disjoint_tables(rng, pool, [16, 16, 3])
+    outside = np.array(sorted(set(range(256)) - set(books))[:16], np.uint16)
+    for b in tables[1]:                            # 1.2% escapes: Top-16 overflows
+        hit = rng.random((2, BW)) < 0.012
+        block = kv_host[:, b]
+        block[hit] = (block[hit] & 0x807F) | (outside[rng.integers(0, 16, int(hit.sum()))] << 7)
+        kv_host[:, b] = block
+    for b in tables[2]:                            # every high byte: fixed6 overflows
+        kv_host[:, b] = rng.integers(0, 1 << 16, (2, BW))
+    kv = layer_from_words(kv_host.reshape(-1), pool)
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False), trace=RecordingTrace())
+    copy = codec.copy_streams.get(kv.device, torch)
+    used = _spy_copies(codec, monkeypatch)
+    pending = codec.save_kv_layer(2, kv, tables)
+    at_save = len(used)
+    payloads = codec.ready(pending)
+    assert [p.bits for p in payloads] == [BITS_TOP16, BITS_FIXED6, BITS_RAW]
+    # ready staged the fixed6 re-encode and the raw payload: two more copies
+    assert len(used) == at_save + 2 and all(s is copy for s in used)
+    assert copy is not torch.cuda.current_stream(kv.device)
+    for p in payloads:
+        slot = _in_pool(codec, p.view)
+        assert slot is not None and slot.tensor.is_pinned()
+    assert bytes(payloads[1].view) == bytes(oracle.fixed6_encode(kv_host[:, tables[1]].reshape(-1)))
+    assert payloads[2].view[0] == codec_format.MODE_RAW
+    assert bytes(payloads[2].view[1:]) == kv_host[:, tables[2]].tobytes()
+    codec.release(pending)
+
+
+def test_probe_that_fits_copies_its_payload_after_the_mode_byte(sz, codebooks):
+    """A probe of a layer that overflowed before stages only the mode byte at save;
+    when it fits, ready copies the Top-16 payload (the oracle's bytes) and the
+    layer's backoff reopens."""
+    say("connector deferred probe that fits")
+    books = codebooks[4 * 32:5 * 32]
+    rng = np.random.default_rng(33)
+    pool = 40
+    table = rng.permutation(pool)[:16].tolist()
+    normal = words_with_books(rng, books, pool, 0.001)
+    over = normal.copy()
+    outside = np.array(sorted(set(range(256)) - set(books))[:16], np.uint16)
+    hit = rng.random(over.size) < 0.012
+    over[hit] = (over[hit] & 0x807F) | (outside[rng.integers(0, 16, int(hit.sum()))] << 7)
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True), trace=trace)
+    for words in (over, normal):                   # overflow, then the window's skip
+        codec.ready(codec.save_kv_layer(4, layer_from_words(words, pool), [table]))
+    pending = codec.save_kv_layer(4, layer_from_words(normal, pool), [table])
+    assert pending.payloads[0].probe and not pending.groups and len(pending.deferred) == 1
+    payload = codec.ready(pending)[0]
+    assert payload.bits == BITS_TOP16 and not payload.fallback
+    expect = oracle.top16_encode(normal.reshape(2, pool, BW)[:, table].reshape(-1),
+                                 oracle.top16_tables(books))
+    assert bytes(payload.view) == bytes(expect)
+    assert _in_pool(codec, payload.view) is not None
+    assert "splitzip_top16_probe_success" in trace.names()
+    assert codec.top16_gate.window(4) == 0
+
+
+def test_pinned_pool_stays_flat_without_release(sz, codebooks):
+    """A caller that never calls release(): each layer's pinned buffer goes back to
+    the pool once its payloads' memoryviews are gone, so 12 save -> ready cycles
+    allocate no more than two buffers."""
+    say("connector pool without release")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(35)
+    pool = 48
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.001), pool)
+    tables = disjoint_tables(rng, pool, [16, 20])
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False))
+    first = None
+    for _ in range(12):
+        payloads = codec.ready(codec.save_kv_layer(5, kv, tables))
+        data = [bytes(p.view) for p in payloads]
+        first = first or data
+        assert data == first
+        del payloads
+    assert codec.pinned.allocations <= 2

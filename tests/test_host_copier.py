@@ -79,3 +79,40 @@ def test_streamed_copy_of_a_small_total_reports_one_range():
     dst = np.zeros(end, np.uint8)
     HostCopier(threads=4).copy_streamed(dst, pieces, lambda lo, hi: got.append((lo, hi)))
     assert got == [(0, pieces[-1][0] + 2000)]
+
+
+class _FakeTensor:
+    def __init__(self, n):
+        self.n = n
+
+    def numel(self):
+        return self.n
+
+
+class _FakeTorch:
+    uint8 = "uint8"
+
+    def __init__(self):
+        self.allocated = 0
+
+    def empty(self, n, dtype=None, pin_memory=False):
+        self.allocated += 1
+        return _FakeTensor(n)
+
+
+def test_pinned_pool_keeps_idle_slots_when_a_request_exceeds_the_cap():
+    from unchainkv_amd.staging import GRANULE, PinnedPool
+
+    torch = _FakeTorch()
+    pool = PinnedPool(cap_bytes=8 * GRANULE)
+    a = pool.acquire(3 * GRANULE, torch)
+    b = pool.acquire(3 * GRANULE, torch)
+    pool.release(a)
+    pool.release(b)
+    assert len(pool._slots) == 2
+    assert pool.acquire(9 * GRANULE, torch) is None     # larger than the cap itself
+    assert len(pool._slots) == 2 and torch.allocated == 2
+    # a request that fits after evicting one idle slot still gets one
+    c = pool.acquire(5 * GRANULE, torch)
+    assert c is not None and c.capacity == 5 * GRANULE
+    assert pool.committed_bytes <= 8 * GRANULE

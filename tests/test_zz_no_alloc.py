@@ -40,11 +40,24 @@ def test_noalloc_refuses_batches_beyond_its_scratch():
     offsets = _u64s(range(0, 257 * 256, 256))
     need = int(lib.kvq_splitzip_top16_paged_workspace_bytes(block_words, offsets, 256))
     assert need > cap
+    # every device pointer 0: were the size check not first, the call would decline
+    # with 0 before any launch
     rc = lib.kvq_splitzip_bf16_encode_top16_paged_noalloc(
-        16, 1 << 30, 1 << 14, block_words, 16, offsets, 256, 16, _u64s([0] * 256), 1 << 40, 16, 0, 0)
+        0, 1 << 30, 1 << 14, block_words, 0, offsets, 256, 0, _u64s([0] * 256), 1 << 40, 0, 0, 0)
     assert rc == -1
     message = lib.kvq_splitzip_last_error().decode()
     assert "scratch" in message and str(need) in message and str(cap) in message
+
+
+def test_noalloc_declines_decreasing_offsets_before_the_size_check():
+    """Decreasing block offsets decline with 0, as the workspace entry point does,
+    instead of a scratch-size error computed from a wrapped difference."""
+    lib = _lib()
+    offsets = _u64s([0, 256, 128, 384])
+    assert int(lib.kvq_splitzip_top16_paged_workspace_bytes(16384, offsets, 3)) == 0
+    rc = lib.kvq_splitzip_bf16_encode_top16_paged_noalloc(
+        0, 1 << 30, 1 << 14, 16384, 0, offsets, 3, 0, _u64s([0] * 3), 1 << 40, 0, 0, 0)
+    assert rc == 0
 
 
 def _encode_both(lib, kv, batch, tables):

@@ -42,6 +42,7 @@ prefill may reuse them (``preserve_source``).
 from __future__ import annotations
 
 import os
+import weakref
 from dataclasses import dataclass, field
 
 from . import codec_format, frames
@@ -81,6 +82,9 @@ class CodecConfig:
     # 2: fixed6 layers send a contiguous request as two half-payloads in KVC2
     # frames (vllm_connector.py:446-447, 2718-2799); anything else: one payload
     chunks: int = 1                       # UNCHAIN_KV_SPLITZIP_CHUNKS
+    # GPU event timing of each layer's encodes and copies in the
+    # splitzip_payload_ready trace event (vllm_connector.py:473, 4634-4664)
+    trace_cuda: bool = False              # UNCHAIN_KV_TRACE_CUDA
 
     @classmethod
     def from_env(cls, env=None) -> "CodecConfig":
@@ -96,6 +100,7 @@ class CodecConfig:
             host_mirror_layers=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_LAYERS", 0)),
             host_mirror_bytes=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_BYTES", 0)),
             chunks=2 if _env_int(env, "UNCHAIN_KV_SPLITZIP_CHUNKS", 1) == 2 else 1,
+            trace_cuda=_env_int(env, "UNCHAIN_KV_TRACE_CUDA", 0) > 0,
         )
 
 
@@ -141,6 +146,7 @@ class LayerPayload:
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
     _mask_first: int = -1            # first high-byte presence mask in the layer's masks
+    _overflow: bool = False          # overflowed, found from its mode byte alone (deferred copy)
     chunk_index: int = 0             # which half of the request's blocks (two-chunk frames)
     chunks_in_layer: int = 1
     request_blocks: int = 0          # blocks of the whole request, for a chunk's frame
@@ -158,10 +164,14 @@ class PendingLayer:
     kv_layer: object
     block_words: int
     payloads: list
-    groups: list = field(default_factory=list)  # (host tensor, event, device buffer, status)
-    slots: list = field(default_factory=list)   # pinned pool buffers behind the host tensors
+    groups: list = field(default_factory=list)  # (host array, event, device buffer, status)
+    slots: list = field(default_factory=list)   # (pinned pool buffer, lease) behind the arrays
     started: float = 0.0
     presence: object = None  # high-byte presence masks of the Top-16 group (probe encodes)
+    # Top-16 groups whose payload copy waits for their mode bytes:
+    # (members, encode result, host array of the mode bytes, its copy event)
+    deferred: list = field(default_factory=list)
+    timing: list = field(default_factory=list)  # ("encode" | "d2h", start, end) GPU events
 
 
 class SplitzipLayerCodec:
@@ -362,6 +372,16 @@ class SplitzipLayerCodec:
             return torch.empty(nbytes, dtype=torch.uint8, pin_memory=True), None
         return slot.view(nbytes), slot
 
+    def _host_array(self, host, slot):
+        """The numpy array over a staging tensor that the payloads' memoryviews are
+        taken from. A pool buffer's lease ends at ``release()`` or, for a caller
+        that never calls it, once this array and every memoryview of it are gone;
+        the pool reuses the buffer only after its last copy has completed."""
+        arr = host.numpy()
+        if slot is not None:
+            weakref.finalize(arr, self.pinned.release, slot, slot.lease)
+        return arr
+
     def _begin_copies(self, device, torch):
         """The copy stream, after it has waited for everything queued so far on the
         current (forward) stream: later forward kernels do not wait for the copies
@@ -370,33 +390,77 @@ class SplitzipLayerCodec:
         copy.wait_stream(torch.cuda.current_stream(device))
         return copy
 
-    def _stage(self, pending: PendingLayer, device_buffer, torch) -> int:
-        """Asynchronous copy of a payload buffer into pinned host memory, on the copy
-        stream."""
-        host, slot = self._host_buffer(device_buffer.numel(), torch)
+    def _gpu_mark(self, stream, torch):
+        """A timing event recorded on ``stream`` when GPU timing is traced, else None."""
+        if not self.config.trace_cuda:
+            return None
+        event = torch.cuda.Event(enable_timing=True)
+        event.record(stream)
+        return event
+
+    def _gpu_span(self, pending: PendingLayer, kind: str, start, stream, torch) -> None:
+        if start is not None:
+            pending.timing.append((kind, start, self._gpu_mark(stream, torch)))
+
+    def _stage_ranges(self, pending: PendingLayer, device_buffer, ranges, torch):
+        """Asynchronous copies of the (offset, length) ranges of a device buffer into
+        the same offsets of a pinned host buffer, on the copy stream; returns (host
+        array, completion event)."""
+        host, slot = self._host_buffer(max(1, device_buffer.numel()), torch)
+        arr = self._host_array(host, slot)
         copy = self._begin_copies(device_buffer.device, torch)
         with torch.cuda.stream(copy):
-            host.copy_(device_buffer, non_blocking=True)
-            event = torch.cuda.Event()
+            start = self._gpu_mark(copy, torch)
+            for off, length in ranges:
+                host[off:off + length].copy_(device_buffer[off:off + length], non_blocking=True)
+            event = torch.cuda.Event(enable_timing=start is not None)
             event.record(copy)
+        if start is not None:
+            pending.timing.append(("d2h", start, event))
         # the caching allocator must not hand the buffer out again before the copy
         device_buffer.record_stream(copy)
         self._keep_slot(pending, slot, event)
-        pending.groups.append((host, event, device_buffer, None))
+        return arr, event
+
+    def _stage(self, pending: PendingLayer, device_buffer, torch) -> int:
+        """Asynchronous copy of a payload buffer into pinned host memory, on the copy
+        stream."""
+        arr, event = self._stage_ranges(pending, device_buffer, [(0, device_buffer.numel())], torch)
+        pending.groups.append((arr, event, device_buffer, None))
         return len(pending.groups) - 1
+
+    def _stage_now(self, pending: PendingLayer, device_buffer, ranges, torch):
+        """_stage_ranges, waited for: the fallback payloads ``ready`` makes."""
+        arr, event = self._stage_ranges(pending, device_buffer, ranges, torch)
+        event.synchronize()
+        return arr
+
+    def _defer_top16(self, pending: PendingLayer, members: list, result, torch) -> None:
+        """Queue only the group's mode bytes for the host (one gather launch and a
+        small copy); ``ready`` copies the payloads that did not overflow and
+        re-encodes the others, so no overflowed Top-16 payload crosses PCIe."""
+        out, offsets, _, batch = result
+        index = getattr(batch, "_mode_index", None)
+        if index is None:
+            index = torch.tensor([int(o) for o in offsets], dtype=torch.int64).pin_memory()
+            index = batch._mode_index = index.to(out.device, non_blocking=True)
+        modes = out.index_select(0, index)
+        arr, event = self._stage_ranges(pending, modes, [(0, modes.numel())], torch)
+        pending.deferred.append((members, result, arr, event))
 
     @staticmethod
     def _keep_slot(pending: PendingLayer, slot, event) -> None:
         # the pool reuses the buffer only after release() and the copy's end
         if slot is not None:
             slot.event = event
-            pending.slots.append(slot)
+            pending.slots.append((slot, slot.lease))
 
     def release(self, pending: PendingLayer) -> None:
         """Returns the layer's pinned buffers to the pool once its payloads have been
-        consumed (sent); their memory views must not be used afterwards."""
-        for slot in pending.slots:
-            self.pinned.release(slot)
+        consumed (sent); their memory views must not be used afterwards. Without
+        this call the buffers go back once the payloads' memoryviews are gone."""
+        for slot, lease in pending.slots:
+            self.pinned.release(slot, lease)
         pending.slots.clear()
 
     def _writeback_members(self, members: list, layer_index: int,
@@ -450,12 +514,14 @@ class SplitzipLayerCodec:
                 self.trace.event("codec_writeback_skip", layer=layer, reason="alias")
             return False
         host, slot = self._host_buffer(out.numel(), torch)
+        arr = self._host_array(host, slot)
         status_host = torch.empty(len(picks), dtype=torch.uint8, pin_memory=True)
         flat = kv_layer.view(-1).view(torch.uint8)
         plane = 2 * kv_layer.stride(0)
         picked = set(picks)
         copy = self._begin_copies(kv_layer.device, torch)
         with torch.cuda.stream(copy):
+            start = self._gpu_mark(copy, torch)
             for i, p in enumerate(members):
                 off, size = int(offsets[i]), int(sizes[i])
                 if i not in picked:
@@ -470,14 +536,16 @@ class SplitzipLayerCodec:
                     host[off + seg:off + size].copy_(flat[plane + k:plane + k + size - seg],
                                                      non_blocking=True)
             status_host.copy_(status[:len(picks)], non_blocking=True)
-            event = torch.cuda.Event()
+            event = torch.cuda.Event(enable_timing=start is not None)
             event.record(copy)
+        if start is not None:
+            pending.timing.append(("d2h", start, event))
         out.record_stream(copy)
         status.record_stream(copy)
         self._keep_slot(pending, slot, event)
         # the codec buffer is released now unless an unmoved payload is still read from it
         keep = out if len(picks) < len(members) else None
-        pending.groups.append((host, event, keep, status_host))
+        pending.groups.append((arr, event, keep, status_host))
         group = len(pending.groups) - 1
         for j, i in enumerate(picks):
             p = members[i]
@@ -491,8 +559,11 @@ class SplitzipLayerCodec:
     def save_kv_layer(self, layer_index: int, kv_layer, block_tables) -> PendingLayer:
         """Encode every request's blocks of one layer (the save hook's codec step) and
         start the copies to host. ``ready`` returns the payloads."""
+        import time
+
         import torch
 
+        started = time.perf_counter()
         block_words = self._layer_geometry(kv_layer, torch)
         payloads = []
         for r, ids in enumerate(block_tables):
@@ -511,15 +582,18 @@ class SplitzipLayerCodec:
                 continue
             bits, epoch, probe = self._choose_bits(layer_index, raw)
             payloads.append(LayerPayload(r, ids, raw, bits, bits, epoch, probe))
-        pending = PendingLayer(layer_index, kv_layer, block_words, payloads)
+        pending = PendingLayer(layer_index, kv_layer, block_words, payloads, started=started)
+        stream = torch.cuda.current_stream(kv_layer.device)
 
         # every group is encoded before the Top-16 writeback overwrites any block
         top_result = None
         top = [p for p in payloads if p.bits == BITS_TOP16]
         if top:
             try:
+                mark = self._gpu_mark(stream, torch)
                 result = self._encode_group(BITS_TOP16, kv_layer, top, block_words, layer_index,
                                             pending)
+                self._gpu_span(pending, "encode", mark, stream, torch)
             except Exception:
                 for p in top:
                     self._cancel_splitzip_top16_probe(layer_index, p.epoch, p.probe)
@@ -535,7 +609,9 @@ class SplitzipLayerCodec:
                 top_result = result
         five = [p for p in payloads if p.bits == BITS_FIXED5]
         if five:
+            mark = self._gpu_mark(stream, torch)
             result = self._encode_group(BITS_FIXED5, kv_layer, five, block_words, layer_index)
+            self._gpu_span(pending, "encode", mark, stream, torch)
             if result is None:
                 self._splitzip_fixed6_layers.add(layer_index)
                 for p in five:
@@ -545,15 +621,21 @@ class SplitzipLayerCodec:
                 self._assign(pending, five, result, torch)
         six = [p for p in payloads if p.bits == BITS_FIXED6]
         if six:
+            mark = self._gpu_mark(stream, torch)
             result = self._encode_group(BITS_FIXED6, kv_layer, six, block_words, layer_index)
+            self._gpu_span(pending, "encode", mark, stream, torch)
             if result is None:
                 for p in six:
                     p.bits = BITS_RAW
             else:
                 self._assign(pending, six, result, torch)
         if top_result is not None:
-            if not (self.codec_writeback_overwrite
-                    and self._stage_writeback(pending, top, top_result, torch)):
+            if pending.presence is not None:
+                # a probe of a layer that overflowed before: its payloads cross PCIe
+                # only once their mode bytes show that they fit
+                self._defer_top16(pending, top, top_result, torch)
+            elif not (self.codec_writeback_overwrite
+                      and self._stage_writeback(pending, top, top_result, torch)):
                 self._assign(pending, top, top_result, torch)
         self.trace.event("codec_encode_submitted", layer=layer_index, requests=len(payloads),
                          raw_bytes=sum(p.raw_bytes for p in payloads))
@@ -569,6 +651,13 @@ class SplitzipLayerCodec:
     # ready: overflow fallback chain (vllm_connector.py:4526-4665)
 
     def ready(self, pending: PendingLayer) -> list:
+        """The layer's payloads once on the host (vllm_connector.py:4526-4665): the
+        copies are waited for; Top-16 (and fixed5) payloads that overflowed are
+        re-encoded as fixed6 with one launch, and fixed6 overflow falls back to raw
+        mode 6. The fallback payloads are staged like the others: pinned pool
+        buffers, copies on the copy stream."""
+        import time
+
         import torch
 
         for host, event, _, _ in pending.groups:
@@ -587,42 +676,102 @@ class SplitzipLayerCodec:
                     self.trace.event("codec_writeback_done", layer=layer, bytes=p.encoded_bytes,
                                      raw_bytes=p.raw_bytes, segments=p.writeback_segments,
                                      overflow=overflow)
-                p.view = memoryview(host.numpy())[p._offset:p._offset + p.encoded_bytes]
+                p.view = memoryview(host)[p._offset:p._offset + p.encoded_bytes]
+        for members, result, modes, event in pending.deferred:
+            # only the payloads that fit go to the host; the others are re-encoded below
+            event.synchronize()
+            out, offsets, sizes, _ = result
+            fit = [i for i in range(len(members)) if modes[i] == codec_format.MODE_TOP16]
+            for i in range(len(members)):
+                members[i]._overflow = i not in fit
+            if fit:
+                ranges = [(int(offsets[i]), int(sizes[i])) for i in fit]
+                host = self._stage_now(pending, out, ranges, torch)
+                for i, (off, size) in zip(fit, ranges):
+                    members[i].view = memoryview(host)[off:off + size]
+        pending.deferred.clear()
+
+        def overflowed_payload(p) -> bool:
+            return p._overflow or (p.view is not None and p.view[0] == codec_format.MODE_OVERFLOW)
+
         for p in pending.payloads:
             if p.bits == BITS_TOP16:
-                self._finish_splitzip_top16_attempt(layer, p.epoch, p.probe,
-                                                    p.view[0] == codec_format.MODE_OVERFLOW)
+                self._finish_splitzip_top16_attempt(layer, p.epoch, p.probe, overflowed_payload(p))
         overflowed = [p for p in pending.payloads
-                      if p.view is not None and p.view[0] == codec_format.MODE_OVERFLOW
-                      and p.bits in {BITS_TOP16, BITS_FIXED5}]
+                      if overflowed_payload(p) and p.bits in {BITS_TOP16, BITS_FIXED5}]
         if any(p.bits == BITS_FIXED5 for p in overflowed):
             self._splitzip_fixed6_layers.add(layer)
             self.trace.event("splitzip_fixed5_overflow", layer=layer)
         if overflowed:
+            stream = torch.cuda.current_stream(pending.kv_layer.device)
+            mark = self._gpu_mark(stream, torch)
             result = self._encode_group(BITS_FIXED6, pending.kv_layer, overflowed,
                                         pending.block_words, layer, pending)
+            self._gpu_span(pending, "encode", mark, stream, torch)
+            for p in overflowed:
+                p.view = None
             if result is not None:
                 out, offsets, sizes, _ = result
-                host = out.cpu()
+                host = self._stage_now(pending, out, [(0, out.numel())], torch)
                 for p, off, size in zip(overflowed, offsets, sizes):
-                    p.view = memoryview(host.numpy())[off:off + size]
+                    p.view = memoryview(host)[off:off + size]
                     p.encoded_bytes = int(size)
             for p in overflowed:
-                p.bits, p.fallback = BITS_FIXED6, True
-        for p in pending.payloads:
-            if p.bits == BITS_RAW or (p.view is not None and p.view[0] == codec_format.MODE_OVERFLOW):
-                ids = torch.as_tensor(p.block_ids, dtype=torch.long, device=pending.kv_layer.device)
-                raw = pending.kv_layer.index_select(1, ids).contiguous().view(torch.int16).cpu()
-                payload = bytearray(p.raw_bytes + 1)
-                payload[0] = codec_format.MODE_RAW
-                payload[1:] = memoryview(raw.numpy()).cast("B")
-                p.view, p.bits, p.encoded_bytes = memoryview(payload), BITS_RAW, len(payload)
+                p.bits, p.fallback, p._overflow = BITS_FIXED6, True, False
+        raws = [p for p in pending.payloads
+                if p.bits == BITS_RAW or p.view is None or p.view[0] == codec_format.MODE_OVERFLOW]
+        if raws:
+            self._stage_raw(pending, raws, torch)
+            for _ in raws:
                 self.trace.event("splitzip_fixed6_overflow", layer=layer)
         pending.presence = None
+        fields = {}
+        if self.config.trace_cuda:
+            # the events have completed: every copy above was waited for
+            fields = {
+                "bits": [p.bits for p in pending.payloads],
+                "fallback": [p.fallback for p in pending.payloads],
+                "encode_gpu_s": sum(a.elapsed_time(b) for k, a, b in pending.timing
+                                    if k == "encode") / 1000.0,
+                "d2h_gpu_s": sum(a.elapsed_time(b) for k, a, b in pending.timing
+                                 if k == "d2h") / 1000.0,
+                "payload_elapsed_s": time.perf_counter() - pending.started,
+            }
+        pending.timing.clear()
         self.trace.event("splitzip_payload_ready", layer=layer,
                          raw_bytes=sum(p.raw_bytes for p in pending.payloads),
-                         encoded_bytes=sum(p.encoded_bytes for p in pending.payloads))
+                         encoded_bytes=sum(p.encoded_bytes for p in pending.payloads), **fields)
         return pending.payloads
+
+    def _stage_raw(self, pending: PendingLayer, raws: list, torch) -> None:
+        """Raw mode-6 payloads (``[6]`` + the request's words in block order,
+        vllm_connector.py:4606-4625): the blocks are gathered on the GPU into one
+        buffer behind each payload's mode byte and copied to the host like the
+        others."""
+        kv_layer = pending.kv_layer
+        batch = self._batch([p.block_ids for p in raws], pending.block_words, kv_layer.device)
+        layout, end = [], 0
+        for p in raws:
+            at = -(-(end + 1) // 256) * 256 - 1       # the words start 256-byte aligned
+            layout.append(at)
+            end = at + 1 + p.raw_bytes
+        buf = torch.empty(end, dtype=torch.uint8, device=kv_layer.device)
+        stream = torch.cuda.current_stream(kv_layer.device)
+        mark = self._gpu_mark(stream, torch)
+        first = 0
+        for p, at in zip(raws, layout):
+            count = len(p.block_ids)
+            buf[at:at + 1].fill_(codec_format.MODE_RAW)
+            words = buf[at + 1:at + 1 + p.raw_bytes].view(torch.bfloat16)
+            torch.index_select(kv_layer, 1, batch.ids[first:first + count],
+                               out=words.view((2, count) + tuple(kv_layer.shape[2:])))
+            first += count
+        self._gpu_span(pending, "encode", mark, stream, torch)
+        host = self._stage_now(pending, buf, [(at, 1 + p.raw_bytes) for p, at in zip(raws, layout)],
+                               torch)
+        for p, at in zip(raws, layout):
+            p.view = memoryview(host)[at:at + 1 + p.raw_bytes]
+            p.bits, p.encoded_bytes = BITS_RAW, 1 + p.raw_bytes
 
     # ------------------------------------------------------------------
     # load: restore validation and dispatch (vllm_connector.py:5098-5313)

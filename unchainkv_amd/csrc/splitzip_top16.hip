@@ -1656,6 +1656,7 @@ extern "C" unsigned long long kvq_splitzip_top16_paged_workspace_bytes(
   if (block_offsets == nullptr) return 0;
   unsigned long long tiles = 0;
   for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;  // refused by the encode too
     const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
     // the smallest tile of any plan bounds the tile count
     tiles += host_payload_tiles(n, true, kMinTileShift);
@@ -1911,7 +1912,14 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged_noalloc(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long directory_ptr, unsigned long long stream_ptr) {
-  if (block_offsets != nullptr && payload_count != 0) {
+  // the workspace entry point's checks of the host arrays first, so that a bad
+  // batch declines with 0 as it does there (the device pointers are checked there)
+  if (block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 ||
+      block_words == 0 || block_words > 0xFFFFFFFFULL)
+    return 0;
+  for (unsigned long long r = 0; r < payload_count; ++r)
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+  {
     const unsigned long long need =
         kvq_splitzip_top16_paged_workspace_bytes(block_words, block_offsets, payload_count);
     if (need > kStaticScratchBytes)

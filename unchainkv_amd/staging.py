@@ -11,7 +11,9 @@ no buffer the caller copies synchronously instead.
 
 Here buffers are plain pinned byte tensors sized in 2 MiB steps, handed out
 smallest-fit; a released buffer returns to the pool at once and is reused only
-after its last copy's event has completed.
+after its last copy's event has completed. Each lease has a number, so a late
+release of an earlier lease (a view's finaliser after an explicit release) leaves
+the buffer's current lease alone.
 """
 
 from __future__ import annotations
@@ -27,6 +29,7 @@ class PinnedSlot:
     tensor: object            # pinned uint8 CPU tensor
     event: object = None      # last copy into or out of it (torch.cuda.Event)
     leased: bool = False
+    lease: int = 0            # number of the current (or last) lease
 
     @property
     def capacity(self) -> int:
@@ -62,6 +65,7 @@ class PinnedPool:
             if fits:
                 slot = min(fits, key=lambda s: s.capacity)
                 slot.leased = True
+                slot.lease += 1
                 return slot
             size = -(-nbytes // GRANULE) * GRANULE
             if self.cap_bytes and size > self.cap_bytes:
@@ -77,14 +81,17 @@ class PinnedPool:
                 if not idle:
                     return None
                 self._slots.remove(max(idle, key=lambda s: s.capacity))
-            slot = PinnedSlot(torch.empty(size, dtype=torch.uint8, pin_memory=True), leased=True)
+            slot = PinnedSlot(torch.empty(size, dtype=torch.uint8, pin_memory=True), leased=True,
+                              lease=1)
             self._slots.append(slot)
             self.allocations += 1
             return slot
 
-    def release(self, slot: PinnedSlot) -> None:
+    def release(self, slot: PinnedSlot, lease: int | None = None) -> None:
+        """Ends the slot's lease (only lease number ``lease``, when given)."""
         with self._lock:
-            slot.leased = False
+            if lease is None or slot.lease == lease:
+                slot.leased = False
 
 
 class CopyStreams:
