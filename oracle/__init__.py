@@ -337,14 +337,23 @@ def fit_top16_py(histogram) -> list[int] | None:
     return selected if len(selected) == 16 else None
 
 
-def default_threads() -> int:
-    """Threads for the oracle's multi-threaded calls: the cores this process may
-    run on, at most 16 (one GPU's share of an 8-GPU node's cores)."""
+def visible_cores() -> int:
+    """Cores this process may run on (its CPU affinity)."""
     try:
-        cores = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    return max(1, min(cores, 16))
+        return os.cpu_count() or 1
+
+
+def default_threads() -> int:
+    """Threads for the oracle's multi-threaded calls: the host's CPU share for one
+    GPU, ``OMP_NUM_THREADS`` when it is set (16 on a one-GPU share of an 8-GPU
+    node), else at most 16, and never more than the visible cores."""
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "") or 16)
+    except ValueError:
+        share = 16
+    return max(1, min(visible_cores(), share))
 
 
 # ---------------------------------------------------------------------------

@@ -172,6 +172,7 @@ class PendingLayer:
     # (members, encode result, host array of the mode bytes, its copy event)
     deferred: list = field(default_factory=list)
     timing: list = field(default_factory=list)  # ("encode" | "d2h", start, end) GPU events
+    d2h_bytes: int = 0       # bytes queued for the host so far (the layer's PCIe traffic)
 
 
 class SplitzipLayerCodec:
@@ -413,6 +414,7 @@ class SplitzipLayerCodec:
             start = self._gpu_mark(copy, torch)
             for off, length in ranges:
                 host[off:off + length].copy_(device_buffer[off:off + length], non_blocking=True)
+                pending.d2h_bytes += int(length)
             event = torch.cuda.Event(enable_timing=start is not None)
             event.record(copy)
         if start is not None:
@@ -526,12 +528,14 @@ class SplitzipLayerCodec:
                 off, size = int(offsets[i]), int(sizes[i])
                 if i not in picked:
                     host[off:off + size].copy_(out[off:off + size], non_blocking=True)
+                    pending.d2h_bytes += size
                     continue
                 start, count = _contiguous_runs(p.block_ids)[0]
                 seg = 2 * count * pending.block_words
                 k = 2 * start * kv_layer.stride(1)
                 head = min(size, seg)
                 host[off:off + head].copy_(flat[k:k + head], non_blocking=True)
+                pending.d2h_bytes += size
                 if size > seg:
                     host[off + seg:off + size].copy_(flat[plane + k:plane + k + size - seg],
                                                      non_blocking=True)
