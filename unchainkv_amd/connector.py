@@ -329,14 +329,14 @@ class SplitzipLayerCodec:
                 presence = batch.new_presence()
             got = None
             if presence is not None:
-                got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(),
+                got = sz.encode_top16_paged(kv_layer, batch, out, batch.workspace(),
                                             tables=tables, presence=presence)
                 if got:
                     pending.presence = presence
                     for p, first in zip(members, batch.presence_first(range(len(members)))):
                         p._mask_first = first
             if not got:
-                got = sz.encode_top16_paged(kv_layer, batch, out, batch.new_workspace(),
+                got = sz.encode_top16_paged(kv_layer, batch, out, batch.workspace(),
                                             tables=tables)
             return (out, batch.out_offsets, batch.encoded_bytes, batch) if got else None
         offsets, sizes, _ = batch.palette_layout(kind)

@@ -471,6 +471,7 @@ class PagedBatch:
         self.max_block = max(flat)
         self.unique_blocks = len(set(flat)) == len(flat)
         self._palette = {}
+        self._workspace = None
         self._runs = None
         self._writeback = {}
 
@@ -528,6 +529,15 @@ class PagedBatch:
             import torch
         return torch.empty(max(self.workspace_bytes(), 16), dtype=torch.uint8,
                            device=self.device)
+
+    def workspace(self, torch=None):
+        """This batch's own encode workspace, made by new_workspace on first use and
+        kept, so that recurring batches allocate it once: calls with the same batch
+        on one stream reuse it (calls that may overlap on different streams need
+        workspaces of their own)."""
+        if self._workspace is None:
+            self._workspace = self.new_workspace(torch)
+        return self._workspace
 
     def directory_bytes(self) -> int:
         """Bytes of the batch's escape directory (0 when its block geometry has none:
