@@ -291,12 +291,16 @@ def plan_fallbacks(torch, sz, w):
                                "presence_first": send.presence_first(over)}
             entry.update(cache[over])
             entry["buffer"] = entry["send"].new_palette_buffer(6)
-            # a layer that overflows is encoded with the presence-mask variant (the
-            # connector's choice for a layer whose Top-16 attempt is a probe after
-            # an overflow), so its fallback needs no presence pass
+            # a layer that overflows is encoded as a probe (the connector's choice
+            # for a Top-16 attempt after an overflow): presence masks and palette
+            # records in the same launches, no escape placement in an overflowed
+            # payload, so its fixed6 fallback is one pass
             if "presence" not in w:
                 w["presence"] = send.new_presence()
+                w["palette_info"] = send.new_palette_info()
             entry["presence"] = w["presence"]
+            entry["palette_info"] = w["palette_info"]
+            entry["info_first"] = list(over)
         if keep and over:
             key = ("keep", keep)
             if key not in cache:
@@ -306,10 +310,10 @@ def plan_fallbacks(torch, sz, w):
         w["plan"].append(entry)
 
 
-def encode_top16(sz, w, layer, presence=None):
+def encode_top16(sz, w, layer, presence=None, palette_info=None):
     got = sz.encode_top16_paged(w["kv"][layer], w["send"], w["payloads"][layer], w["workspace"],
                                 tables=w["tables"][layer], directory=w["dirs"][layer],
-                                presence=presence)
+                                presence=presence, palette_info=palette_info)
     if got != w["send"].total_encoded_bytes:
         raise RuntimeError(f"layer {layer}: paged encode declined ({got})")
 
@@ -317,11 +321,11 @@ def encode_top16(sz, w, layer, presence=None):
 def encode_layer(sz, w, layer):
     """Top-16 for every request; fixed6 for the requests whose Top-16 payload overflows."""
     plan = w["plan"][layer]
-    encode_top16(sz, w, layer, plan.get("presence"))
+    encode_top16(sz, w, layer, plan.get("presence"), plan.get("palette_info"))
     if plan["over"]:
         got = sz.encode_bf16_paged(w["kv"][layer], plan["send"], plan["buffer"],
-                                   plan["workspace"], bits=6, presence=plan["presence"],
-                                   presence_first=plan["presence_first"])
+                                   plan["workspace"], bits=6, palette_info=plan["palette_info"],
+                                   info_first=plan["info_first"])
         if got != sum(plan["sizes"]):
             raise RuntimeError(f"layer {layer}: fixed6 fallback encode declined ({got})")
 
@@ -1374,7 +1378,7 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
     kernels = {"encode": "top16_encode_tile+top16_encode_finalize",
                "decode": "top16_decode_tile_dir (escape directory)"}
     if overflowed:
-        kernels = {"encode": "top16 encode (presence masks) + palette_reduce/encode_tile (fixed6)",
+        kernels = {"encode": "top16 probe encode (presence masks, palette records in its finalize launch) + palette_encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
     traffic, traffic_source = (None, None) if overflowed else measured_traffic(name,

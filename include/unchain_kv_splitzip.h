@@ -202,6 +202,30 @@ long long kvq_splitzip_bf16_encode_top16_paged_presence(
     unsigned long long directory_ptr, unsigned long long presence_ptr,
     unsigned long long stream_ptr);
 
+/* kvq_splitzip_bf16_encode_top16_paged_presence for a probe of a layer that
+ * overflowed before (no counterpart in the reference; it replaces the Top-16 attempt
+ * of the reference connector's probe, vllm_connector.py:3078-3123, whose overflowed
+ * payload is re-encoded as fixed6, :4557-4633). In the same launch as its finalize it
+ * also writes each payload's palette record (512 bytes: 256-bit presence mask,
+ * distinct count, rank table, ascending palette) to palette_info_ptr + 512 r
+ * (16-byte aligned, payload_count records), which
+ * kvq_splitzip_bf16_encode_mode_paged_info takes instead of a presence and reduce
+ * pass; and a payload found to overflow gets its header (255, count clamped to the
+ * capacity), body and codes but no escape placement: its escape section stays zero
+ * (the reference's holds escapes in atomic order, and both are discarded for the
+ * fixed6 re-encode). Payloads that fit are byte-identical to the plain encode's.
+ * Declined (0) when presence_ptr or palette_info_ptr is 0, and as the presence
+ * variant. */
+long long kvq_splitzip_bf16_encode_top16_paged_probe(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long directory_ptr, unsigned long long presence_ptr,
+    unsigned long long palette_info_ptr, unsigned long long stream_ptr);
+
 /* No counterpart in the reference: kvq_splitzip_bf16_encode_top16_paged for callers
  * that cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same arguments, results and preconditions,
@@ -290,6 +314,21 @@ long long kvq_splitzip_bf16_encode_mode_paged_presence(
     unsigned long long out_capacity, unsigned long long workspace_ptr,
     unsigned long long workspace_bytes, unsigned long long presence_ptr,
     const unsigned long long* presence_first, unsigned long long stream_ptr, int bits);
+
+/* kvq_splitzip_bf16_encode_mode_paged from the palette records of a Top-16 probe
+ * encode (no counterpart in the reference): payload r's palette is record
+ * info_first[r] (a HOST array, each < info_count) of info_ptr (written by
+ * kvq_splitzip_bf16_encode_top16_paged_probe over the same blocks; 16-byte aligned);
+ * no workspace, presence or reduce pass. Same results and other preconditions;
+ * declined (0) for block geometries the tile kernels do not take. */
+long long kvq_splitzip_bf16_encode_mode_paged_info(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long info_ptr,
+    const unsigned long long* info_first, unsigned long long info_count,
+    unsigned long long stream_ptr, int bits);
 
 /* Palette decode + scatter of a batch (no counterpart in the reference; it replaces
  * one kvq_splitzip_bf16_decode_fixed6_blocks call per request, and decodes fixed5 on

@@ -146,6 +146,7 @@ class LayerPayload:
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
     _mask_first: int = -1            # first high-byte presence mask in the layer's masks
+    _info_index: int = -1            # its palette record in the layer's probe records
     _overflow: bool = False          # overflowed, found from its mode byte alone (deferred copy)
     chunk_index: int = 0             # which half of the request's blocks (two-chunk frames)
     chunks_in_layer: int = 1
@@ -168,6 +169,7 @@ class PendingLayer:
     slots: list = field(default_factory=list)   # (pinned pool buffer, lease) behind the arrays
     started: float = 0.0
     presence: object = None  # high-byte presence masks of the Top-16 group (probe encodes)
+    palette_info: object = None  # the probe encode's palette record per Top-16 member
     # Top-16 groups whose payload copy waits for their mode bytes:
     # (members, encode result, host array of the mode bytes, its copy event)
     deferred: list = field(default_factory=list)
@@ -314,9 +316,13 @@ class SplitzipLayerCodec:
         offsets, sizes, batch) or None when the library declines.
 
         With `pending`: a Top-16 group that holds a probe (the layer overflowed
-        before, so it may again) also records every tile's high-byte presence
-        mask in ``pending.presence``; a palette group whose members all have masks
-        there starts from them instead of reading the blocks once more."""
+        before, so it may again) is encoded as a probe: it also records every
+        tile's high-byte presence mask in ``pending.presence`` and every member's
+        fixed6/fixed5 palette in ``pending.palette_info``, and leaves an overflowed
+        payload's escape slots unplaced (it is re-encoded anyway); a palette group
+        whose members all have palettes there is encoded in one pass from them (or
+        from their masks, without reading the blocks once more for a presence
+        pass)."""
         sz = self._lib()
         batch = self._batch([p.block_ids for p in members], block_words, kv_layer.device)
         if kind == BITS_TOP16:
@@ -324,30 +330,39 @@ class SplitzipLayerCodec:
             if tables is None:
                 return None
             out = batch.new_payload_buffer()
-            presence = None
+            presence = info = None
             if pending is not None and any(p.probe for p in members):
                 presence = batch.new_presence()
+                info = batch.new_palette_info() if presence is not None else None
             got = None
             if presence is not None:
                 got = sz.encode_top16_paged(kv_layer, batch, out, batch.workspace(),
-                                            tables=tables, presence=presence)
+                                            tables=tables, presence=presence, palette_info=info)
                 if got:
-                    pending.presence = presence
-                    for p, first in zip(members, batch.presence_first(range(len(members)))):
-                        p._mask_first = first
+                    pending.presence, pending.palette_info = presence, info
+                    for k, (p, first) in enumerate(
+                            zip(members, batch.presence_first(range(len(members))))):
+                        p._mask_first, p._info_index = first, k
             if not got:
                 got = sz.encode_top16_paged(kv_layer, batch, out, batch.workspace(),
                                             tables=tables)
             return (out, batch.out_offsets, batch.encoded_bytes, batch) if got else None
         offsets, sizes, _ = batch.palette_layout(kind)
         out = batch.new_palette_buffer(kind)
-        masks = {}
-        if pending is not None and pending.presence is not None and \
-                all(p._mask_first >= 0 for p in members):
-            masks = {"presence": pending.presence,
-                     "presence_first": [p._mask_first for p in members]}
-        got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(), bits=kind,
-                                   **masks)
+        got = None
+        if pending is not None and pending.palette_info is not None and \
+                all(p._info_index >= 0 for p in members):
+            got = sz.encode_bf16_paged(kv_layer, batch, out, None, bits=kind,
+                                       palette_info=pending.palette_info,
+                                       info_first=[p._info_index for p in members])
+        if not got:
+            masks = {}
+            if pending is not None and pending.presence is not None and \
+                    all(p._mask_first >= 0 for p in members):
+                masks = {"presence": pending.presence,
+                         "presence_first": [p._mask_first for p in members]}
+            got = sz.encode_bf16_paged(kv_layer, batch, out, batch.new_palette_workspace(),
+                                       bits=kind, **masks)
         return (out, offsets, sizes, batch) if got else None
 
     BATCH_CACHE = 16
@@ -728,7 +743,7 @@ class SplitzipLayerCodec:
             self._stage_raw(pending, raws, torch)
             for _ in raws:
                 self.trace.event("splitzip_fixed6_overflow", layer=layer)
-        pending.presence = None
+        pending.presence = pending.palette_info = None
         fields = {}
         if self.config.trace_cuda:
             # the events have completed: every copy above was waited for

@@ -32,6 +32,18 @@ constexpr unsigned int kInBodySlots = kStageSlots - 1;
 // Payload descriptors passed by value in the kernel arguments.
 constexpr int kMaxPayloads = 64;
 
+// Per-payload palette of the fixed6 / fixed5 codecs, from the OR of the payload's
+// high-byte presence masks (palette_info_from_masks).
+struct PaletteInfo {
+  unsigned int mask[8];     // presence of each high byte
+  unsigned int distinct;    // number of distinct high bytes
+  unsigned int pad0[7];
+  unsigned char rank[256];  // high byte -> code (0 for absent bytes)
+  unsigned char palette[64];
+  unsigned char pad1[128];
+};
+static_assert(sizeof(PaletteInfo) == 512, "palette info");
+
 struct PayloadDesc {
   unsigned long long buf_offset;  // byte offset of the payload inside the payload buffer
   unsigned long long ids_offset;  // first block id of this payload inside `ids`
@@ -83,6 +95,10 @@ struct LaunchArgs {
   // fallback encode of an overflowed payload then starts from these masks instead
   // of reading the words again.
   uint32_t* presence;
+  // Palette of each payload of the launch, computed from its presence masks by the
+  // Top-16 probe encode's finalize launch (null otherwise); the fixed6 / fixed5
+  // re-encode of an overflowed payload then starts from it.
+  PaletteInfo* palette_info;
   PayloadDesc p[kMaxPayloads];
 };
 
@@ -470,6 +486,62 @@ __device__ __forceinline__ u32x4 decode_run8(u32x2 body, uint32_t cd, const uint
                assemble_pair(__builtin_amdgcn_perm(ea, body.x, 0x07030602u)),
                assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x05010400u)),
                assemble_pair(__builtin_amdgcn_perm(eb, body.y, 0x07030602u))};
+}
+
+// Workgroup-cooperative: OR of `count` 32-byte presence masks at `masks` -> the
+// palette record `out` (ascending palette, rank table, distinct count). Thread tid
+// ORs whole masks tid, tid + 256, ... (four loads in flight), then the wave by
+// shuffles and the workgroup through LDS (s_mask, 8 dwords).
+__device__ __forceinline__ void palette_info_from_masks(const unsigned int* masks,
+                                                        unsigned long long count,
+                                                        PaletteInfo& out, unsigned int* s_mask) {
+  const unsigned int tid = threadIdx.x;
+  if (tid < 8) s_mask[tid] = 0;
+  __syncthreads();
+  u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+  const u32x4* m4 = reinterpret_cast<const u32x4*>(masks);
+  for (unsigned long long s = tid; s < count; s += 4 * kThreads) {
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const unsigned long long slot = s + (unsigned long long)k * kThreads;
+      a[k] = slot < count ? m4[2 * slot] : u32x4{0, 0, 0, 0};
+      b[k] = slot < count ? m4[2 * slot + 1] : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo |= a[k];
+      hi |= b[k];
+    }
+  }
+  // one LDS atomic per wave and dword (an atomic from every lane compiles to a loop
+  // over the active lanes)
+  unsigned int part[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) part[k] |= __shfl_xor(part[k], off, kWave);
+  if ((tid & (kWave - 1)) == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (part[k]) atomicOr(&s_mask[k], part[k]);
+  }
+  __syncthreads();
+  unsigned int distinct = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) distinct += __popc(s_mask[k]);
+  if (tid < 8) out.mask[tid] = s_mask[tid];
+  if (tid == 0) out.distinct = distinct;
+  // code of high byte h = number of present bytes below h (ascending palette)
+  const unsigned int h = tid;
+  unsigned int rank = __popc(s_mask[h >> 5] & ((1u << (h & 31)) - 1u));
+  for (unsigned int k = 0; k < (h >> 5); ++k) rank += __popc(s_mask[k]);
+  const bool present = (s_mask[h >> 5] >> (h & 31)) & 1u;
+  out.rank[h] = (unsigned char)(present ? rank : 0);
+  if (tid < 64) out.palette[tid] = 0;
+  __syncthreads();
+  // (a palette of more than 32 entries is an overflow for fixed5, which reads 32)
+  if (present && rank < 64) out.palette[rank] = (unsigned char)h;
 }
 
 }  // namespace unchainkv

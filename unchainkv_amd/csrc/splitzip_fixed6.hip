@@ -48,17 +48,6 @@ inline unsigned long long palette_encoded_size(unsigned long long n, int bits) {
   return bits == 6 ? 65 + n + ((n + 3) / 4) * 3 : 33 + n + ((n + 7) / 8) * 5;
 }
 
-// Per-payload palette state written by palette_reduce.
-struct PaletteInfo {
-  unsigned int mask[8];     // presence of each high byte
-  unsigned int distinct;    // number of distinct high bytes
-  unsigned int pad0[7];
-  unsigned char rank[256];  // high byte -> code (0 for absent bytes)
-  unsigned char palette[64];
-  unsigned char pad1[128];
-};
-static_assert(sizeof(PaletteInfo) == 512, "palette info");
-
 constexpr unsigned int kGenericGroups = 64;  // workgroups per payload, generic kernels
 
 // ---------------------------------------------------------------------------
@@ -131,59 +120,12 @@ __global__ __launch_bounds__(kThreads) void palette_reduce(LaunchArgs a, unsigne
                                                            const unsigned int* masks,
                                                            PaletteInfo* info) {
   __shared__ unsigned int s_mask[8];
-  const unsigned int tid = threadIdx.x, r = blockIdx.x;
+  const unsigned int r = blockIdx.x;
   const PayloadDesc d = a.p[r];
   const unsigned long long n = payload_words(a, d);
   const unsigned long long first = groups ? (unsigned long long)r * groups : d.mask_begin;
   const unsigned long long count = groups ? groups : payload_tiles(a, n);
-  if (tid < 8) s_mask[tid] = 0;
-  __syncthreads();
-  // thread tid ORs whole 32-byte masks of slots tid, tid + 256, ... (loads of four
-  // slots are issued together)
-  u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
-  const u32x4* m4 = reinterpret_cast<const u32x4*>(masks + first * 8);
-  for (unsigned long long s = tid; s < count; s += 4 * kThreads) {
-    u32x4 a[4], b[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const unsigned long long slot = s + (unsigned long long)k * kThreads;
-      a[k] = slot < count ? m4[2 * slot] : u32x4{0, 0, 0, 0};
-      b[k] = slot < count ? m4[2 * slot + 1] : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      lo |= a[k];
-      hi |= b[k];
-    }
-  }
-  // OR over the wave by shuffles, then one LDS atomic per wave and dword (an
-  // atomic from every lane compiles to a loop over the active lanes)
-  unsigned int part[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) part[k] |= __shfl_xor(part[k], off, kWave);
-  if ((tid & (kWave - 1)) == 0) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (part[k]) atomicOr(&s_mask[k], part[k]);
-  }
-  __syncthreads();
-  PaletteInfo& out = info[r];
-  unsigned int distinct = 0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) distinct += __popc(s_mask[k]);
-  if (tid < 8) out.mask[tid] = s_mask[tid];
-  if (tid == 0) out.distinct = distinct;
-  // code of high byte h = number of present bytes below h (ascending palette)
-  const unsigned int h = tid;
-  unsigned int rank = __popc(s_mask[h >> 5] & ((1u << (h & 31)) - 1u));
-  for (unsigned int k = 0; k < (h >> 5); ++k) rank += __popc(s_mask[k]);
-  const bool present = (s_mask[h >> 5] >> (h & 31)) & 1u;
-  out.rank[h] = (unsigned char)(present ? rank : 0);
-  if (tid < 64) out.palette[tid] = 0;
-  __syncthreads();
-  if (present && rank < (unsigned int)Palette<kBits>::kLimit) out.palette[rank] = (unsigned char)h;
+  palette_info_from_masks(masks + first * 8, count, info[r], s_mask);
 }
 
 // ---------------------------------------------------------------------------
@@ -250,7 +192,9 @@ __device__ __forceinline__ unsigned long long unstage_run(const unsigned char* s
   return bits;
 }
 
-template <bool kIds, int kBits>
+// kIndexed: payload r's palette is info[a.p[r].mask_begin] (palettes computed by a
+// Top-16 probe encode for a larger batch), else info[r].
+template <bool kIds, int kBits, bool kIndexed = false>
 __global__ __launch_bounds__(kThreads) void palette_encode_tile(LaunchArgs a, EncodeGeom geo,
                                                                 const PaletteInfo* info) {
   using P = Palette<kBits>;
@@ -261,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void palette_encode_tile(LaunchArgs a, En
   const unsigned int lane = tid & (kWave - 1);
   const unsigned int wave = uniform(tid >> 6);
   const PlaneTile t = plane_tile<kTileShift>(a, group_index());
-  const PaletteInfo& pi = info[t.payload_index];
+  const PaletteInfo& pi = info[kIndexed ? a.p[t.payload_index].mask_begin : t.payload_index];
   const unsigned int in_plane = t.in_plane0 + wave * 1024;
   const unsigned long long wstart = t.plane * (t.n >> 1) + in_plane;  // payload word
   const bool active = wave * 1024 < t.words;
@@ -519,6 +463,22 @@ long long launch_palette_decode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
   return check("palette_decode");
 }
 
+// Encodes with the palettes a Top-16 probe encode computed: payload r's is
+// info[a.p[r].mask_begin]; the presence and reduce passes are skipped (tile
+// geometry only).
+template <int kBits>
+long long launch_palette_encode_info(LaunchArgs& a, const EncodeGeom& g, const PaletteInfo* info,
+                                     hipStream_t stream) {
+  const dim3 block(kThreads);
+  if (a.ids)
+    hipLaunchKernelGGL((palette_encode_tile<true, kBits, true>), dim3(a.total_tiles), block, 0,
+                       stream, a, g, info);
+  else
+    hipLaunchKernelGGL((palette_encode_tile<false, kBits, true>), dim3(a.total_tiles), block, 0,
+                       stream, a, g, info);
+  return check("palette_encode (probe palettes)");
+}
+
 long long palette_encode(LaunchArgs& a, const EncodeGeom& g, bool tiles,
                          unsigned int presence_groups, PaletteInfo* info, unsigned int* masks,
                          hipStream_t stream, int bits, bool masks_given = false) {
@@ -739,16 +699,24 @@ long long encode_mode_paged_impl(
     unsigned long long out_ptr, const unsigned long long* out_offsets,
     unsigned long long out_capacity, unsigned long long workspace_ptr,
     unsigned long long workspace_bytes, unsigned long long stream_ptr, int bits,
-    unsigned long long presence_ptr, const unsigned long long* presence_first) {
-  if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || workspace_ptr == 0 ||
+    unsigned long long presence_ptr, const unsigned long long* presence_first,
+    unsigned long long info_ptr = 0, const unsigned long long* info_first = nullptr,
+    unsigned long long info_count = 0) {
+  // info mode (palettes from a Top-16 probe encode): no workspace and no masks
+  const bool with_info = info_ptr != 0;
+  if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || (workspace_ptr == 0 && !with_info) ||
       block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 ||
       block_words == 0 || block_words > 0xFFFFFFFFULL || (bits != 5 && bits != 6) ||
       workspace_ptr % 16 != 0 || presence_ptr % 16 != 0 ||
-      (presence_ptr != 0 && presence_first == nullptr))
+      (presence_ptr != 0 && presence_first == nullptr) ||
+      (with_info && (info_ptr % 16 != 0 || info_first == nullptr || presence_ptr != 0)))
     return 0;
   if (presence_ptr != 0)
     for (unsigned long long r = 0; r < payload_count; ++r)
       if (presence_first[r] > 0xFFFFFFFFULL) return 0;
+  if (with_info)
+    for (unsigned long long r = 0; r < payload_count; ++r)
+      if (info_first[r] >= info_count) return 0;
   unsigned long long total = 0, max_plane = 0;
   bool sections = true;
   std::vector<std::pair<unsigned long long, unsigned long long>> spans;
@@ -765,9 +733,12 @@ long long encode_mode_paged_impl(
   std::sort(spans.begin(), spans.end());
   for (size_t k = 1; k < spans.size(); ++k)
     if (spans[k].first < spans[k - 1].second) return 0;  // overlapping payloads
-  if (batch_workspace_bytes(block_offsets, payload_count, block_words) > workspace_bytes) return 0;
+  if (!with_info && batch_workspace_bytes(block_offsets, payload_count, block_words) >
+                        workspace_bytes)
+    return 0;
   const bool tiles =
       sections && tile_geometry(kv_ptr, plane_stride, block_stride, block_words, max_plane);
+  if (with_info && !tiles) return 0;  // the probe palettes come with the tile geometry
   const EncodeGeom g = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace_ptr);
@@ -782,6 +753,14 @@ long long encode_mode_paged_impl(
     const unsigned int count =
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
     fill_batch(a, block_offsets, out_offsets, first, count, block_words);
+    if (with_info) {
+      for (unsigned int k = 0; k < count; ++k) a.p[k].mask_begin = (unsigned int)info_first[first + k];
+      const PaletteInfo* probe = reinterpret_cast<const PaletteInfo*>(info_ptr);
+      const long long rc = bits == 6 ? launch_palette_encode_info<6>(a, g, probe, stream)
+                                     : launch_palette_encode_info<5>(a, g, probe, stream);
+      if (rc < 0) return rc;
+      continue;
+    }
     PaletteInfo* info = reinterpret_cast<PaletteInfo*>(ws);
     unsigned int* masks = reinterpret_cast<unsigned int*>(info + count);
     if (presence_ptr != 0) {
@@ -824,6 +803,21 @@ extern "C" long long kvq_splitzip_bf16_encode_mode_paged_presence(
                                 block_offsets, payload_count, out_ptr, out_offsets, out_capacity,
                                 workspace_ptr, workspace_bytes, stream_ptr, bits, presence_ptr,
                                 presence_first);
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_mode_paged_info(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long info_ptr,
+    const unsigned long long* info_first, unsigned long long info_count,
+    unsigned long long stream_ptr, int bits) {
+  if (info_ptr == 0) return 0;
+  return encode_mode_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                block_offsets, payload_count, out_ptr, out_offsets, out_capacity,
+                                0, 0, stream_ptr, bits, 0, nullptr, info_ptr, info_first,
+                                info_count);
 }
 
 extern "C" long long kvq_splitzip_bf16_decode_mode_paged(

@@ -963,10 +963,25 @@ __device__ void rescan_tile(const LaunchArgs& a, const PayloadDesc& d, unsigned 
   }
 }
 
-template <int kFinGroups, bool kInBody, int kDenseItems>
+// kProbe (a probe encode of a layer that overflowed before, whose caller re-encodes
+// an overflowed payload as fixed6 / fixed5): a payload found to overflow gets its
+// header but no escape placement (its escape section is left zeroed; the
+// reference's is in atomic order and discarded the same way), and
+// a.payload_count more workgroups after the finalize groups compute each payload's
+// palette from the presence masks the tile kernel wrote (a.palette_info).
+template <int kFinGroups, bool kInBody, int kDenseItems, bool kProbe = false>
 __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) {
   constexpr int kFinPerThread = kFinGroups;             // tile counts per thread per pass
   constexpr int kFinChunk = kThreads * kFinPerThread;   // tiles scanned per pass
+  if (kProbe && blockIdx.x >= a.payload_count * kFinGroups) {
+    __shared__ unsigned int s_mask[8];
+    const unsigned int r = blockIdx.x - a.payload_count * kFinGroups;
+    const PayloadDesc d = a.p[r];
+    const unsigned long long n = 2ull * d.block_count * a.block_words;
+    palette_info_from_masks(a.presence + 8ull * d.tile_begin,
+                            payload_tiles(a, n), a.palette_info[r], s_mask);
+    return;
+  }
   __shared__ unsigned int s_over_tile[kFinChunk / kFinGroups];
   __shared__ unsigned int s_over_base[kFinChunk / kFinGroups];
   __shared__ unsigned int s_over_count;
@@ -1060,6 +1075,11 @@ __global__ __launch_bounds__(kThreads) void top16_encode_finalize(LaunchArgs a) 
     for (int q = 0; q < kFinPreload; ++q) pre[q] = staged_at(q);
     unsigned int chunk_total;
     unsigned int prefix = block_exclusive_sum(sum, s_wave, chunk_total);
+    if (kProbe && chunk0 == 0 && m == tiles && chunk_total > cap) {
+      // the whole payload in one pass and over its capacity: header only
+      running = chunk_total;
+      break;
+    }
 
     // staged escapes of this group's tile go straight to their slots
     unsigned int c = 0;
@@ -1386,7 +1406,8 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   // everywhere) spreads its placement over 32 groups per payload: 1 % outlier
   // layer encode call 109.2 -> 105.8 us (16 groups: 106.5 us)
   const dim3 fin_grid(a.payload_count *
-                      (a.presence && !a.inbody_slots ? kFinPresenceGroups : large ? 16 : 8));
+                          (a.presence && !a.inbody_slots ? kFinPresenceGroups : large ? 16 : 8) +
+                      (a.palette_info ? a.payload_count : 0));
   if (a.inbody_slots) {
     if (large)
       hipLaunchKernelGGL((top16_encode_finalize<16, true, kDenseItemsSparse>), fin_grid, block, 0,
@@ -1394,6 +1415,9 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
     else
       hipLaunchKernelGGL((top16_encode_finalize<8, true, kDenseItemsSparse>), fin_grid, block, 0,
                          stream, a);
+  } else if (a.presence && a.palette_info) {
+    hipLaunchKernelGGL((top16_encode_finalize<kFinPresenceGroups, false, kDenseItemsDense, true>),
+                       fin_grid, block, 0, stream, a);
   } else if (a.presence) {
     hipLaunchKernelGGL((top16_encode_finalize<kFinPresenceGroups, false, kDenseItemsDense>),
                        fin_grid, block, 0, stream, a);
@@ -1750,7 +1774,8 @@ long long encode_top16_paged_impl(
     unsigned long long out_capacity, unsigned long long tables_ptr,
     unsigned long long workspace_ptr, unsigned long long workspace_bytes,
     unsigned long long directory_ptr, unsigned long long presence_ptr,
-    unsigned long long stream_ptr) {
+    unsigned long long stream_ptr, unsigned long long info_ptr = 0) {
+  if (info_ptr != 0 && (presence_ptr == 0 || info_ptr % 16 != 0)) return 0;
   if (kv_ptr == 0 || block_ids_ptr == 0 || out_ptr == 0 || tables_ptr == 0 || workspace_ptr == 0 ||
       block_offsets == nullptr || out_offsets == nullptr || payload_count == 0 || block_words == 0 ||
       block_words > 0xFFFFFFFFULL)
@@ -1805,6 +1830,7 @@ long long encode_top16_paged_impl(
     a.workspace = ws;
     set_directory(a, directory_ptr, dir_tiles, tile_offset);
     if (presence_ptr) a.presence = reinterpret_cast<uint32_t*>(presence_ptr) + 8 * tile_offset;
+    if (info_ptr) a.palette_info = reinterpret_cast<PaletteInfo*>(info_ptr) + first;
     long long rc = launch_encode(a, g, plan, stream);
     if (rc < 0) return rc;
     ws += workspace_words(tiles);
@@ -1899,6 +1925,22 @@ extern "C" long long kvq_splitzip_bf16_encode_top16_paged_presence(
                                  block_offsets, payload_count, out_ptr, out_offsets,
                                  out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
                                  directory_ptr, presence_ptr, stream_ptr);
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_top16_paged_probe(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long out_ptr, const unsigned long long* out_offsets,
+    unsigned long long out_capacity, unsigned long long tables_ptr,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long directory_ptr, unsigned long long presence_ptr,
+    unsigned long long palette_info_ptr, unsigned long long stream_ptr) {
+  if (presence_ptr == 0 || palette_info_ptr == 0) return 0;
+  return encode_top16_paged_impl(kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                                 block_offsets, payload_count, out_ptr, out_offsets,
+                                 out_capacity, tables_ptr, workspace_ptr, workspace_bytes,
+                                 directory_ptr, presence_ptr, stream_ptr, palette_info_ptr);
 }
 
 extern "C" unsigned long long kvq_splitzip_top16_noalloc_scratch_bytes() {

@@ -78,6 +78,13 @@ _SIGNATURES = (
         False,
     ),
     (
+        "kvq_splitzip_bf16_encode_top16_paged_probe",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64,
+         _U64, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
         "kvq_splitzip_bf16_decode_top16_paged",
         [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64],
         ctypes.c_longlong,
@@ -118,6 +125,13 @@ _SIGNATURES = (
         "kvq_splitzip_bf16_encode_mode_paged_presence",
         [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64P,
          _U64, ctypes.c_int],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_encode_mode_paged_info",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64, _U64P, _U64, _U64,
+         ctypes.c_int],
         ctypes.c_longlong,
         False,
     ),
@@ -571,6 +585,16 @@ class PagedBatch:
         size = self.presence_bytes()
         return torch.empty(size, dtype=torch.uint8, device=self.device) if size else None
 
+    PALETTE_INFO_BYTES = 512
+
+    def new_palette_info(self, torch=None):
+        """Device buffer for one 512-byte palette record per request (written by a
+        probe encode: ``encode_top16_paged(presence=..., palette_info=...)``)."""
+        if torch is None:
+            import torch
+        return torch.empty(self.PALETTE_INFO_BYTES * self.payload_count, dtype=torch.uint8,
+                           device=self.device)
+
     def presence_first(self, members) -> list[int]:
         """Index of the first presence mask of each request in ``members`` (masks
         of request r follow those of requests 0 .. r-1, one per 4096-word tile of
@@ -652,17 +676,25 @@ def _directory_ptr(directory, batch: PagedBatch, torch) -> int | None:
 
 def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index: int = -1, *,
                        codebooks: bytes | None = None, tables=None,
-                       directory=None, presence=None) -> int | None:
+                       directory=None, presence=None, palette_info=None) -> int | None:
     """Gather + Top-16 encode every request of ``batch`` from one paged layer
     ``(2, num_blocks, ...)`` into ``out`` (a ``batch.out_bytes`` uint8 buffer).
     With ``directory`` (``batch.new_directory()``) the encoder also writes the
     escape directory that lets ``decode_top16_paged`` apply escapes without a
     second pass; with ``presence`` (``batch.new_presence()``) it writes the
     high-byte presence masks that let ``encode_bf16_paged`` re-encode an
-    overflowed request without a presence pass. Returns the total encoded bytes
-    or ``None`` when the codec declines."""
+    overflowed request without a presence pass. ``palette_info``
+    (``batch.new_palette_info()``, with ``presence``): a probe encode of a layer
+    that overflowed before; it also writes every request's fixed6/fixed5 palette
+    record (``encode_bf16_paged(palette_info=...)`` then needs no presence or
+    reduce pass) and leaves an overflowed payload's escape slots unplaced (its
+    header, body and codes are written; it is re-encoded anyway). Returns the total
+    encoded bytes or ``None`` when the codec declines."""
+    if palette_info is not None and presence is None:
+        raise ValueError("palette_info needs presence")
     lib = _load()
-    name = "kvq_splitzip_bf16_encode_top16_paged" + ("_presence" if presence is not None else "")
+    name = "kvq_splitzip_bf16_encode_top16_paged" + (
+        "_probe" if palette_info is not None else "_presence" if presence is not None else "")
     encode = getattr(lib, name, None) if lib else None
     if encode is None:
         return None
@@ -684,6 +716,12 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
                 or batch.presence_bytes() == 0:
             return None
         extra = (int(presence.data_ptr()),)
+    if palette_info is not None:
+        if palette_info.dtype != torch.uint8 or not palette_info.is_contiguous() or \
+                palette_info.device != kv_layer.device or \
+                palette_info.numel() < PagedBatch.PALETTE_INFO_BYTES * batch.payload_count:
+            return None
+        extra += (int(palette_info.data_ptr()),)
     stream = _stream_handle(kv_layer.device, torch)
     encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
                      batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
@@ -808,18 +846,26 @@ def build_directory(host_payloads, src_offsets, encoded_bytes, batch: PagedBatch
 # batched paged fixed6 / fixed5 (the Top-16 overflow fallback, one launch per layer)
 
 def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6, *,
-                      presence=None, presence_first=None) -> int | None:
+                      presence=None, presence_first=None, palette_info=None,
+                      info_first=None) -> int | None:
     """Gather + fixed6 (bits 6) or fixed5 (bits 5) encode of every request of
     ``batch``; payload r goes to ``batch.palette_layout(bits)[0][r]`` of ``out``.
     ``presence`` / ``presence_first``: the high-byte presence masks a Top-16
     encode of the same blocks wrote (``encode_top16_paged(presence=...)``) and the
     index of request r's first mask there (``PagedBatch.presence_first`` of that
-    batch); the encode then skips its own presence pass. Returns the total
-    encoded bytes or ``None`` when the codec declines."""
+    batch); the encode then skips its own presence pass. ``palette_info`` /
+    ``info_first``: the palette records a probe encode of the same blocks wrote
+    (``encode_top16_paged(presence=..., palette_info=...)``) and the index of
+    request r's record there; the encode is then one pass (``workspace`` unused).
+    Returns the total encoded bytes or ``None`` when the codec declines."""
     if bits not in {5, 6}:
         raise ValueError("splitzip bf16 bits must be 5 or 6")
     if (presence is None) != (presence_first is None):
         raise ValueError("presence and presence_first go together")
+    if (palette_info is None) != (info_first is None):
+        raise ValueError("palette_info and info_first go together")
+    if palette_info is not None:
+        return _encode_bf16_paged_info(kv_layer, batch, out, bits, palette_info, info_first)
     lib = _load()
     name = "kvq_splitzip_bf16_encode_mode_paged" + ("_presence" if presence is not None else "")
     encode = getattr(lib, name, None) if lib else None
@@ -852,6 +898,34 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
                      int(bits))
     if encoded < 0:
         _raise_last(lib, "splitzip palette paged encode failed")
+    return int(encoded) or None
+
+
+def _encode_bf16_paged_info(kv_layer, batch, out, bits, palette_info, info_first):
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_mode_paged_info", None) if lib else None
+    if encode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    if palette_info.dtype != torch.uint8 or not palette_info.is_contiguous() or \
+            palette_info.device != kv_layer.device or len(info_first) != batch.payload_count:
+        return None
+    records = palette_info.numel() // PagedBatch.PALETTE_INFO_BYTES
+    batch.palette_layout(bits)
+    offs = batch._palette[bits][3]
+    firsts = (ctypes.c_ulonglong * batch.payload_count)(*map(int, info_first))
+    stream = _stream_handle(kv_layer.device, torch)
+    encoded = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                     batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                     batch.payload_count, int(out.data_ptr()), offs, int(out.numel()),
+                     int(palette_info.data_ptr()), firsts, records, int(stream), int(bits))
+    if encoded < 0:
+        _raise_last(lib, "splitzip palette paged encode (probe palettes) failed")
     return int(encoded) or None
 
 
