@@ -1378,7 +1378,8 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
     kernels = {"encode": "top16_encode_tile+top16_encode_finalize",
                "decode": "top16_decode_tile_dir (escape directory)"}
     if overflowed:
-        kernels = {"encode": "top16 probe encode (presence masks, palette records in its finalize launch) + palette_encode_tile (fixed6)",
+        kernels = {"encode": "top16 probe encode (presence masks; palettes in its finalize "
+                             "launch) + palette_encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
     traffic, traffic_source = (None, None) if overflowed else measured_traffic(name,
