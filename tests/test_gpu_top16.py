@@ -279,6 +279,42 @@ def test_decode_accepts_shuffled_escapes_and_garbage_padding(sz, codebooks):
     assert np.array_equal(got, words)
 
 
+def test_decode_of_reference_cpu_decoder_fixtures(sz):
+    """Payloads with shuffled escape lists and random unused slots, decoded by the
+    reference's CPU decoder into the fixture words (tests/golden/
+    make_top16_cpu_golden.py): the GPU decode + scatter writes the same words, at
+    tile geometry (1024-word blocks) and at block sizes the tile kernels do not
+    take. Repeated positions are left out: the GPU patches escapes in parallel, and
+    the reference's CUDA decode has no order among them either."""
+    import json
+    from pathlib import Path
+
+    golden = Path(__file__).resolve().parent / "golden"
+    index = json.loads((golden / "top16_cpu_cases.json").read_text())
+    blocks_for = {256: 2, 1000: 4, 4096: 2, 16384: 8, 10004: 82}
+    rng = np.random.default_rng(5)
+    done = 0
+    with np.load(golden / "top16_cpu_payloads.npz") as data:
+        for case in index["cases"]:
+            if not (case["decoded"] and case["distinct"]):
+                continue
+            key, n = case["key"], case["raw_bytes"] // 2
+            blocks = blocks_for[n]
+            bw = n // (2 * blocks)
+            say("reference cpu decoder fixture", case["name"], "blocks", blocks, "bw", bw)
+            pool = blocks + 5
+            ids = rng.permutation(pool)[:blocks].tolist()
+            target = torch.zeros((2, pool, bw), dtype=torch.bfloat16, device="cuda")
+            comp = torch.from_numpy(data[key + "_payload"].copy()).cuda()
+            books = data[key + "_books"].tobytes()
+            assert sz.decode_top16(comp, target, ids, 2 * n, -1, codebooks=books) == 2 * n
+            torch.cuda.synchronize()
+            got = u16(target).reshape(2, pool, bw)[:, ids].reshape(-1)
+            assert np.array_equal(got, data[key + "_words"]), case["name"]
+            done += 1
+    assert done == 15
+
+
 def test_decode_leaves_overflowed_payload_unapplied(sz, codebooks):
     say("decode mode 255")
     n = 2 * 4 * 512
