@@ -151,25 +151,32 @@ __device__ __forceinline__ RawShare load_share(const PlaneBases& pb, unsigned in
   return r;
 }
 
-// First index in [0, count) whose position is >= target (entries ascending);
-// wave-cooperative 64-way search, result uniform across the wave.
-__device__ unsigned int lower_bound_escapes(const unsigned char* entries, unsigned int count,
-                                            unsigned int target) {
-  const unsigned int lane = __lane_id();
-  unsigned int lo = 0, hi = count;
-  while (hi - lo > 64) {
-    const unsigned int step = (hi - lo + 63) / 64;
-    const unsigned int idx = lo + lane * step;
+// First indices in [0, count) whose positions are >= target_k and >= target_v
+// (entries ascending): lanes 0-31 search for target_k and lanes 32-63 for target_v
+// at once, 32 ways per round, so that both searches share each memory round trip.
+// Results uniform across the wave.
+__device__ uint2 lower_bound_escapes2(const unsigned char* entries, unsigned int count,
+                                      unsigned int target_k, unsigned int target_v) {
+  const unsigned int lane = __lane_id(), half = lane >> 5, sub = lane & 31;
+  const unsigned int target = half ? target_v : target_k;
+  unsigned int lo = 0, hi = count;  // uniform within each half
+  for (;;) {
+    const unsigned int span_k = __builtin_amdgcn_readlane(hi - lo, 0);
+    const unsigned int span_v = __builtin_amdgcn_readlane(hi - lo, 32);
+    if (span_k <= 32 && span_v <= 32) break;
+    const unsigned int step = (hi - lo + 31) / 32;
+    const unsigned int idx = lo + sub * step;
     const bool below = idx < hi && entry_pos(entries, idx) < target;
-    const unsigned int k = (unsigned int)__popcll(__ballot(below));
+    const unsigned int k = (unsigned int)__popcll((__ballot(below) >> (32 * half)) & 0xFFFFFFFFull);
     const unsigned int new_lo = k ? lo + (k - 1) * step + 1 : lo;
     const unsigned int new_hi = min(hi, lo + k * step);
     lo = new_lo;
     hi = max(new_hi, new_lo);
   }
-  const unsigned int idx = lo + lane;
+  const unsigned int idx = lo + sub;
   const bool below = idx < hi && entry_pos(entries, idx) < target;
-  return __builtin_amdgcn_readfirstlane(lo + (unsigned int)__popcll(__ballot(below)));
+  const unsigned int r = lo + (unsigned int)__popcll((__ballot(below) >> (32 * half)) & 0xFFFFFFFFull);
+  return uint2{__builtin_amdgcn_readlane(r, 0), __builtin_amdgcn_readlane(r, 32)};
 }
 
 // One 64-entry window of a plane's escape list (entry base + lane); positions past
@@ -302,14 +309,23 @@ __device__ __forceinline__ void attend_step(const RawShare& cur, unsigned int ts
       dstk[1] = u32x4{o[4], o[5], o[6], o[7]};
       decode8(cur.vb[i].x, cur.vb[i].y, cur.vc[i].x, c.tab_v, o);
       decode8(cur.vb[i].z, cur.vb[i].w, cur.vc[i].y, c.tab_v, o + 4);
-      if (tail && ts + tt >= c.we) {
-        // a token past the range: zero V so that p = 0 cannot meet an Inf or NaN
-#pragma unroll
-        for (int r = 0; r < 8; ++r) o[r] = 0u;
-      }
       u32x4* dstv = reinterpret_cast<u32x4*>(c.sV + tt * kKStride + part * 16);
       dstv[0] = u32x4{o[0], o[1], o[2], o[3]};
       dstv[1] = u32x4{o[4], o[5], o[6], o[7]};
+    }
+  }
+  if (tail) {
+    // tokens past the range (their lanes decoded a clamped, in-range token without
+    // its escapes): zero their V rows so that p = 0 cannot meet an Inf or NaN. The
+    // stores sit behind the wave-uniform branch, so full steps skip them.
+    const unsigned int tt0 = lane / 8, part = lane % 8;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const unsigned int tt = tt0 + 8 * i;
+      if (ts + tt >= c.we) {
+        u32x4* dstv = reinterpret_cast<u32x4*>(c.sV + tt * kKStride + part * 16);
+        dstv[0] = dstv[1] = u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
 
@@ -505,12 +521,6 @@ top16_attention_split(AttnArgs a) {
   };
   if (wb < c.we) {
     const unsigned int we = c.we;
-    w.ptr_k = lower_bound_escapes(entries, c.count, wb * row_words);
-    w.ptr_v = lower_bound_escapes(entries, c.count, c.half + wb * row_words);
-    w.base_k = w.ptr_k;
-    w.base_v = w.ptr_v;
-    w.wk = load_window(entries, c.count, w.ptr_k + lane);
-    w.wv = load_window(entries, c.count, w.ptr_v + lane);
     const unsigned int share = h * kHeadDim + (lane % 8) * 16;
     // two register sets of raw bytes alternate: one is decoded while the next
     // step's loads are in flight
@@ -520,7 +530,15 @@ top16_attention_split(AttnArgs a) {
                         min(t0 + 8, we - 1) * row_words + share);
     };
     auto step = [&](const RawShare& r, unsigned int ts) { attend_step(r, ts, c, qb, w); };
+    // the first step's loads go out before the escape searches, whose round trips
+    // they then overlap
     RawShare r0 = load_step(wb);
+    const uint2 first = lower_bound_escapes2(entries, c.count, wb * row_words,
+                                             c.half + wb * row_words);
+    w.ptr_k = w.base_k = first.x;
+    w.ptr_v = w.base_v = first.y;
+    w.wk = load_window(entries, c.count, w.ptr_k + lane);
+    w.wv = load_window(entries, c.count, w.ptr_v + lane);
     check_order();
     RawShare r1;
     unsigned int ts = wb;
