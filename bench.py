@@ -89,6 +89,9 @@ def parse_args():
     p.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="summarise two rocprofv3 --pmc runs of --profile-steps (FETCH_SIZE, "
                         "then WRITE_SIZE) into HBM bytes per dispatch, print JSON and exit")
+    p.add_argument("--counter-summary", metavar="PMC_DIR",
+                   help="mean value per dispatch of every counter of a rocprofv3 --pmc run, "
+                        "per kernel; print JSON and exit")
     return p.parse_args()
 
 
@@ -101,6 +104,11 @@ CALL_KERNELS = {
     "encode": ("top16_encode_tile", "top16_encode_finalize"),
     "decode": ("top16_decode_tile_dir",),
     "attention": ("top16_attention_split", "top16_attention_combine"),
+}
+# a layer whose Top-16 payloads overflow: the probe encode, then fixed6
+CALL_KERNELS_OVERFLOW = {
+    "encode": ("top16_encode_tile", "top16_encode_finalize", "palette_encode_tile"),
+    "decode": ("palette_decode_tile",),
 }
 
 
@@ -205,7 +213,21 @@ def pmc_summary(fetch_dir, write_dir) -> dict:
             "kernels": kernels}
 
 
-def measured_traffic(workload: str, direction: str):
+def counter_summary(directory) -> dict:
+    """Mean value per dispatch of every counter of one rocprofv3 --pmc run, per kernel
+    (the SQ counters of a pass, for instance)."""
+    sums, dispatches = {}, {}
+    for row in _counter_rows(directory):
+        name = _short_name(row["Kernel_Name"])
+        counter = row["Counter_Name"]
+        sums.setdefault(name, {}).setdefault(counter, 0.0)
+        sums[name][counter] += float(row["Counter_Value"])
+        dispatches.setdefault(name, {}).setdefault(counter, set()).add(row["Dispatch_Id"])
+    return {name: {c: round(v / len(dispatches[name][c]), 1) for c, v in counters.items()}
+            for name, counters in sums.items()}
+
+
+def measured_traffic(workload: str, direction: str, overflowed: bool = False):
     """HBM bytes of one call (its kernels' counter bytes) from the committed summary
     profiles/pmc_<workload>.json, or None when there is none."""
     path = PROFILES / f"pmc_{workload}.json"
@@ -213,7 +235,7 @@ def measured_traffic(workload: str, direction: str):
         return None, None
     summary = json.loads(path.read_text())
     kernels = summary.get("kernels", {})
-    names = CALL_KERNELS[direction]
+    names = (CALL_KERNELS_OVERFLOW if overflowed else CALL_KERNELS)[direction]
     if not all(n in kernels for n in names):
         return None, path.name
     return sum(kernels[n]["hbm_bytes"] for n in names), path.name
@@ -1382,8 +1404,7 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
                              "launch) + palette_encode_tile (fixed6)",
                    "decode": "palette_decode_tile (fixed6)"}
 
-    traffic, traffic_source = (None, None) if overflowed else measured_traffic(name,
-                                                                                 dominant[0])
+    traffic, traffic_source = measured_traffic(name, dominant[0], bool(overflowed))
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -1457,6 +1478,13 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
             result["cpu_baseline"] = base
     elif name in SUB_CPU_BASELINE and not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, w, 1, SUB_CPU_SECONDS)
+    if not headline and name == "llama32-1b-contiguous":
+        # launch-bound layers: the same step replayed from a HIP graph, per layer too
+        replay = time_graph_replay(torch, step, w, steps, raw_bytes=raw_layer * layers)
+        if "ms_per_step" in replay:
+            replay["us_per_layer_encode_plus_decode"] = round(replay["ms_per_step"] * 1e3 / layers,
+                                                              2)
+        result["graph_replay"] = replay
     if w["plan"][0]["over"]:
         result["dropin_fixed6_per_request"] = time_dropin_fixed6(torch, sz, w)
         if not headline:
@@ -1473,7 +1501,8 @@ def _sub_summary(result: dict) -> dict:
             "compression_ratio", "escapes_per_layer", "overflowed_payloads", "roofline",
             "verified", "ms_per_layer_call", "escape_fraction",
             "max_rel_error_vs_decode_then_attend", "decode_only_ms_per_layer", "mfma_TFLOPs",
-            "dtype", "data", "dropin_fixed6_per_request", "connector_layer", "cpu_baseline")
+            "dtype", "data", "dropin_fixed6_per_request", "connector_layer", "cpu_baseline",
+            "graph_replay")
     return {k: result[k] for k in keep if k in result}
 
 
@@ -1489,6 +1518,9 @@ def main() -> int:
     args = parse_args()
     if args.pmc_summary:
         print(json.dumps(pmc_summary(*args.pmc_summary), indent=1))
+        return 0
+    if args.counter_summary:
+        print(json.dumps(counter_summary(args.counter_summary), indent=1))
         return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
