@@ -605,3 +605,39 @@ def test_pinned_pool_stays_flat_without_release(sz, codebooks):
         assert data == first
         del payloads
     assert codec.pinned.allocations <= 2
+
+
+def test_restore_returns_its_pinned_buffer_when_staging_raises(sz, codebooks, monkeypatch):
+    """A restore whose host staging raises (here the copier) hands its pinned buffer
+    back to the pool: the next restore of the same layer reuses it and decodes
+    exactly."""
+    say("connector restore slot on error")
+    books = codebooks[5 * 32:6 * 32]
+    rng = np.random.default_rng(36)
+    pool = 48
+    kv = layer_from_words(words_with_books(rng, books, pool, 0.001), pool)
+    tables = disjoint_tables(rng, pool, [16, 20])
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=False))
+    pending = codec.save_kv_layer(5, kv, tables)
+    payloads = codec.ready(pending)
+    requests = [(t, p.view, p.metadata(5, kv[0, 0].numel())) for t, p in zip(tables, payloads)]
+    receiver = torch.zeros_like(kv)
+
+    def broken(*args, **kwargs):
+        raise RuntimeError("staging failed")
+
+    leased = sum(s.leased for s in codec.pinned._slots)  # the saved payloads' buffer
+    monkeypatch.setattr(codec.host_copier, "copy_streamed", broken)
+    with pytest.raises(RuntimeError, match="staging failed"):
+        codec.load_kv_layer_batch(5, receiver, requests)
+    torch.cuda.synchronize()
+    assert sum(s.leased for s in codec.pinned._slots) == leased
+    allocations = codec.pinned.allocations
+    monkeypatch.undo()
+    got = codec.load_kv_layer_batch(5, receiver, requests)
+    torch.cuda.synchronize()
+    assert got == [(len(t), 4 * len(t) * kv[0, 0].numel()) for t in tables]
+    assert codec.pinned.allocations == allocations
+    for t in tables:
+        assert torch.equal(receiver[:, t].view(torch.int16), kv[:, t].view(torch.int16))
+    codec.release(pending)

@@ -951,43 +951,47 @@ class SplitzipLayerCodec:
                 dir_at = -(-end // 256) * 256
                 end = dir_at + dir_bytes
         host, slot = self._host_buffer(max(end, 1), torch)
-        host_np = host.numpy()
-        device = torch.empty(max(end, 1), dtype=torch.uint8, device=kv_layer.device)
+        try:
+            host_np = host.numpy()
+            device = torch.empty(max(end, 1), dtype=torch.uint8, device=kv_layer.device)
 
-        def upload(lo: int, hi: int) -> None:
-            device[lo:hi].copy_(host[lo:hi], non_blocking=True)
+            def upload(lo: int, hi: int) -> None:
+                device[lo:hi].copy_(host[lo:hi], non_blocking=True)
 
-        # each range of the staging buffer goes to the GPU as soon as its payload
-        # bytes are in place, while the host threads copy the next ones
-        payload_end = max((start + len(member[3]) for _, member, start in layout), default=0)
-        self.host_copier.copy_streamed(host_np, [(start, member[3]) for _, member, start in layout],
-                                       upload, end=payload_end)
-        if dir_bytes:
-            tops = [start for m, _, start in layout if m == codec_format.MODE_TOP16]
-            # the builder sorts each escape list in place (a reference sender's is in
-            # atomic order): a list it reordered goes to the GPU again
-            lists = []
-            for start, member in zip(tops, top):
-                n = member[2] // 2
-                lo = start + codec_format.top16_sections(n)["escapes"][0]
-                count = min(int.from_bytes(bytes(host_np[start + 1:start + 5]), "little"),
-                            codec_format.top16_escape_capacity(n))
-                lists.append((lo, lo + 5 * count, host_np[lo:lo + 5 * count].copy()))
-            built = sz.build_directory(host_np, tops, [len(m[3]) for m in top],
-                                       batches[codec_format.MODE_TOP16])
-            if built is None:
-                dir_bytes = 0
-            else:
-                host_np[dir_at:dir_at + dir_bytes] = built
-                upload(dir_at, dir_at + dir_bytes)
-            for lo, hi, before in lists:
-                if (before != host_np[lo:hi]).any():
-                    upload(lo, hi)
-        if slot is not None:
-            # back to the pool at once: reused after the host-to-device copy ends
-            slot.event = torch.cuda.Event()
-            slot.event.record(torch.cuda.current_stream(kv_layer.device))
-            self.pinned.release(slot)
+            # each range of the staging buffer goes to the GPU as soon as its payload
+            # bytes are in place, while the host threads copy the next ones
+            payload_end = max((start + len(member[3]) for _, member, start in layout), default=0)
+            self.host_copier.copy_streamed(host_np,
+                                           [(start, member[3]) for _, member, start in layout],
+                                           upload, end=payload_end)
+            if dir_bytes:
+                tops = [start for m, _, start in layout if m == codec_format.MODE_TOP16]
+                # the builder sorts each escape list in place (a reference sender's is in
+                # atomic order): a list it reordered goes to the GPU again
+                lists = []
+                for start, member in zip(tops, top):
+                    n = member[2] // 2
+                    lo = start + codec_format.top16_sections(n)["escapes"][0]
+                    count = min(int.from_bytes(bytes(host_np[start + 1:start + 5]), "little"),
+                                codec_format.top16_escape_capacity(n))
+                    lists.append((lo, lo + 5 * count, host_np[lo:lo + 5 * count].copy()))
+                built = sz.build_directory(host_np, tops, [len(m[3]) for m in top],
+                                           batches[codec_format.MODE_TOP16])
+                if built is None:
+                    dir_bytes = 0
+                else:
+                    host_np[dir_at:dir_at + dir_bytes] = built
+                    upload(dir_at, dir_at + dir_bytes)
+                for lo, hi, before in lists:
+                    if (before != host_np[lo:hi]).any():
+                        upload(lo, hi)
+        finally:
+            if slot is not None:
+                # back to the pool at once (also when staging raised): reused after
+                # the host-to-device copies queued so far end
+                slot.event = torch.cuda.Event()
+                slot.event.record(torch.cuda.current_stream(kv_layer.device))
+                self.pinned.release(slot)
         for mode, members in groups.items():
             starts = [start for m, _, start in layout if m == mode]
             batch = batches[mode]
