@@ -59,10 +59,19 @@ constexpr int kHeadDim = 128;
 constexpr int kGroup = 4;                   // query heads per kv head
 constexpr int kStep = 16;                   // tokens per wave step
 // u16 per row of sK and sV: 288-byte rows (16-byte aligned for the b128 accesses).
-// The padding spreads the rows' LDS banks: on the Llama-3-8B decode step 288-byte
-// rows ran 3 us faster than 272-byte ones and 14 us faster than unpadded 256-byte
-// rows; longer rows would not leave room for 4 workgroups per CU.
+// The padding spreads the LDS banks of the 16 rows one MFMA operand read spans: on
+// the Llama-3-8B decode step, unpadded 256-byte rows ran 10 us slower; with the
+// chunk order below, 272- and 288-byte rows run alike (before it, 288 was 3 us
+// ahead). Longer rows would not leave room for 4 workgroups per CU.
 constexpr int kKStride = kHeadDim + 16;
+
+// Position in an LDS row of dim d: the row's 8-dim (16-byte) chunks are stored even
+// chunks first, then odd ones (chunk c in slot (c >> 1) | (c & 1) << 3), so that the
+// 8 lanes of one decode store, which hold chunks 2p (then 2p + 1), write 128
+// contiguous bytes. Reads take whole chunks, or 4 dims inside one.
+__device__ __forceinline__ constexpr unsigned int row_pos(unsigned int d) {
+  return ((((d >> 3) >> 1) | (((d >> 3) & 1u) << 3)) << 3) | (d & 7u);
+}
 constexpr int kWaveLds = 2 * kStep * kKStride;  // u16 per wave: K and V of a step, token-major
 constexpr int kMaxSeqs = 64;                // sequences per launch (kernel arguments)
 constexpr int kPartial = kHeadDim + 2;      // m, l, acc[128] per (split, query head)
@@ -259,7 +268,7 @@ __device__ __forceinline__ void apply_escapes(Window& win, unsigned int& ptr, un
       const unsigned int x = r >> 7;  // step token * kv_heads + head
       const unsigned int tt = (x * c.head_magic) >> 24;
       if (x - tt * c.kv_heads == c.head) {
-        const unsigned int word = tt * kKStride + (r & (kHeadDim - 1));
+        const unsigned int word = tt * kKStride + row_pos(r & (kHeadDim - 1));
         const unsigned int shift = (word & 1u) * 16u;
         uint32_t* dw = reinterpret_cast<uint32_t*>(dst) + (word >> 1);
         __hip_atomic_fetch_and(dw, ~(0x7F80u << shift), __ATOMIC_RELAXED,
@@ -283,11 +292,12 @@ __device__ __forceinline__ void apply_escapes(Window& win, unsigned int& ptr, un
 template <int G>
 __device__ __forceinline__ void pv_group(i16x4 pa, const uint16_t* sV, f32x4 (&acc)[2 * kPvChains]) {
   const unsigned int lane = __lane_id(), col = lane % 16, grp = lane / 16;
-  const uint16_t* vsrc = sV + (4 * G + col / 4) * kKStride + 16 * grp + 4 * (col % 4);
+  const uint16_t* vrow = sV + (4 * G + col / 4) * kKStride;
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
+    const uint16_t* vsrc = vrow + row_pos(64 * half + 16 * grp + 4 * (col % 4));
     const i16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) i16x4*)(vsrc + 64 * half));
+        (__attribute__((address_space(3))) i16x4*)(vsrc));
     f32x4& o = acc[half + 2 * (G % kPvChains)];
     o = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(pa, vb, o, 4, 4 * G, 0);
   }
@@ -308,14 +318,15 @@ __device__ __forceinline__ void attend_step(const RawShare& cur, unsigned int ts
       uint32_t o[8];
       decode8(cur.kb[i].x, cur.kb[i].y, cur.kc[i].x, c.tab_k, o);
       decode8(cur.kb[i].z, cur.kb[i].w, cur.kc[i].y, c.tab_k, o + 4);
-      u32x4* dstk = reinterpret_cast<u32x4*>(c.sK + tt * kKStride + part * 16);
-      dstk[0] = u32x4{o[0], o[1], o[2], o[3]};
-      dstk[1] = u32x4{o[4], o[5], o[6], o[7]};
+      // dims 16p .. 16p + 7 and 16p + 8 .. 16p + 15: chunks 2p and 2p + 1
+      uint16_t* rowk = c.sK + tt * kKStride;
+      *reinterpret_cast<u32x4*>(rowk + row_pos(part * 16)) = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4*>(rowk + row_pos(part * 16 + 8)) = u32x4{o[4], o[5], o[6], o[7]};
       decode8(cur.vb[i].x, cur.vb[i].y, cur.vc[i].x, c.tab_v, o);
       decode8(cur.vb[i].z, cur.vb[i].w, cur.vc[i].y, c.tab_v, o + 4);
-      u32x4* dstv = reinterpret_cast<u32x4*>(c.sV + tt * kKStride + part * 16);
-      dstv[0] = u32x4{o[0], o[1], o[2], o[3]};
-      dstv[1] = u32x4{o[4], o[5], o[6], o[7]};
+      uint16_t* rowv = c.sV + tt * kKStride;
+      *reinterpret_cast<u32x4*>(rowv + row_pos(part * 16)) = u32x4{o[0], o[1], o[2], o[3]};
+      *reinterpret_cast<u32x4*>(rowv + row_pos(part * 16 + 8)) = u32x4{o[4], o[5], o[6], o[7]};
     }
   }
   if (tail) {
@@ -327,8 +338,9 @@ __device__ __forceinline__ void attend_step(const RawShare& cur, unsigned int ts
     for (int i = 0; i < 2; ++i) {
       const unsigned int tt = tt0 + 8 * i;
       if (ts + tt >= c.we) {
-        u32x4* dstv = reinterpret_cast<u32x4*>(c.sV + tt * kKStride + part * 16);
-        dstv[0] = dstv[1] = u32x4{0u, 0u, 0u, 0u};
+        uint16_t* rowv = c.sV + tt * kKStride;
+        *reinterpret_cast<u32x4*>(rowv + row_pos(part * 16)) = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(rowv + row_pos(part * 16 + 8)) = u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -352,10 +364,11 @@ __device__ __forceinline__ void attend_step(const RawShare& cur, unsigned int ts
   // ---- S^T = K Q^T: lane l gets tokens 4*(l/16)+j of head l%16 ----
   f32x4 st = {0, 0, 0, 0};
   {
-    const uint16_t* krow = c.sK + col * kKStride + grp * 32;
+    const uint16_t* krow = c.sK + col * kKStride;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 ka = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(krow + 8 * ks));
+      const bf16x8 ka = __builtin_bit_cast(
+          bf16x8, *reinterpret_cast<const u32x4*>(krow + row_pos(grp * 32 + 8 * ks)));
       st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], st, 0, 0, 0);
     }
   }
