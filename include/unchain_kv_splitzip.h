@@ -358,6 +358,49 @@ long long kvq_splitzip_bf16_decode_torchop_paged(
     unsigned long long block_words, unsigned long long block_ids_ptr,
     const unsigned long long* block_offsets, unsigned long long stream_ptr);
 
+/* Torch-op encode of a batch, in two calls with a host read between them (no
+ * counterpart in the reference library: it replaces the torch ops of
+ * _splitzip_bf16_native_blocks, src/unchain_kv/vllm_connector.py:3204-3343, which a
+ * sender takes for a request below 1 MiB without Top-16 native decode, :3043-3046).
+ *
+ * kvq_splitzip_bf16_plan_torchop_paged writes one 64-byte plan record per payload
+ * to plans (device, 8-byte aligned):
+ *   bytes  0-31  256-bit presence mask of the words' high bytes
+ *   bytes 32-35  presence of the values of bits 0-3 (bits 0-15) and bits 4-7
+ *                (bits 16-31)
+ *   byte  36     mode the reference picks: 2 (sign/magnitude) when the magnitudes
+ *                span fewer than 7 bits and the payload is smaller than the raw
+ *                words, else 0 (high-byte palette) when it has at most 128 entries
+ *                and is smaller, else 1 (nibble planes) when smaller, else 255
+ *   bytes 37-40  widths (modes 2, 0: byte 37; mode 1: one per nibble plane)
+ *   byte  41     smallest magnitude (mode 2)
+ *   bytes 48-55  encoded bytes (u64; 0 when declined), bytes 56-63 words n
+ * workspace: kvq_splitzip_torchop_workspace_bytes() bytes of device memory.
+ * Returns payload_count, or 0 on a failed precondition.
+ *
+ * kvq_splitzip_bf16_encode_torchop_paged then writes payload r, as the reference's
+ * encoder writes it, to out + out_offsets[r]; encoded_bytes[r] is its plan's size
+ * (0: declined, nothing written). A payload whose plan in device memory does not
+ * give that size is not written. Returns the total encoded bytes, 0 on a failed
+ * precondition, -1 on a launch error. Block tables as in the batched decode. */
+unsigned long long kvq_splitzip_torchop_plan_bytes(void);
+unsigned long long kvq_splitzip_torchop_workspace_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count);
+long long kvq_splitzip_bf16_plan_torchop_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long plans_ptr, unsigned long long stream_ptr);
+long long kvq_splitzip_bf16_encode_torchop_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long plans_ptr, unsigned long long out_ptr,
+    const unsigned long long* out_offsets, const unsigned long long* encoded_bytes,
+    unsigned long long out_capacity, unsigned long long stream_ptr);
+
 /* ------------------------------------------------------------------------------
  * bf16 exponent histograms of a paged layer: the statistics Top-16 codebooks are
  * fit from (no counterpart in the reference as a native call: it runs

@@ -12,6 +12,17 @@
 // A payload whose header does not give exactly its encoded size (the reference's
 // restore checks) is left unapplied.
 //
+// Encode (the sender's choice for a request below 1 MiB without the native codec,
+// :3043-3046, 3204-3343): a presence pass records which high-byte and low-nibble
+// values occur in each 4096-word tile, a plan pass ORs a payload's tiles and picks
+// the format in the reference's order -- sign/magnitude if the magnitudes span
+// fewer than 7 bits and the payload is smaller than the raw words, else the
+// high-byte palette if it has at most 128 entries and is smaller, else the nibble
+// planes if smaller, else none -- with its widths and encoded size, and the encode
+// pass writes the chosen format (palettes ascending, unused palette bytes zero,
+// codes LSB-first with zero padding bits). The host reads the plans' sizes between
+// the plan and the encode to lay the payloads out.
+//
 // Workgroup (x, y): payload y of the launch, words [4096 x, 4096 x + 4096); a thread
 // decodes 16 consecutive words. Byte-granular reads (these are fallback formats),
 // 16-byte stores when a thread's words lie in one block.
@@ -147,6 +158,349 @@ __global__ __launch_bounds__(kThreads) void torchop_decode(LaunchArgs a, Torchop
     a.kv[word_offset(a, d, i0 + k)] = (uint16_t)(out[k >> 1] >> (16 * (k & 1)));
 }
 
+
+// ---------------------------------------------------------------------------
+// encode
+
+// Presence of word values in one 4096-word tile (workspace record, 16 u32):
+// [0..8) 256-bit mask of the high bytes, [8] bits 0-15: values of bits 0-3 of the
+// words, bits 16-31: values of bits 4-7.
+constexpr unsigned int kTorchopRecordWords = 16;
+
+// Plan of one payload's torch-op encode (64 bytes, device memory; the host reads
+// encoded_bytes).
+struct TorchopPlan {
+  unsigned int high[8];              // presence of each high byte value
+  unsigned int nibbles;              // presence of bits 0-3 values | bits 4-7 values << 16
+  unsigned char mode;                // 2, 0 or 1; kTorchopNone when none is smaller
+  unsigned char width[4];            // modes 2 and 0: width[0]; mode 1: per nibble plane
+  unsigned char mag_min;             // mode 2: smallest magnitude (high byte & 0x7F)
+  unsigned char pad0[6];
+  unsigned long long encoded_bytes;  // 0 when declined
+  unsigned long long words;          // n
+};
+static_assert(sizeof(TorchopPlan) == 64, "torch-op plan record");
+constexpr unsigned char kTorchopNone = 255;
+
+// Up to 16 consecutive words i0 .. of payload d (count of them valid) into w (two
+// bf16 per dword): two 16-byte loads when they lie in one block and are 16-byte
+// aligned, else word by word.
+__device__ __forceinline__ unsigned int load_words16(const LaunchArgs& a, const PayloadDesc& d,
+                                                     unsigned long long n, unsigned long long i0,
+                                                     uint32_t (&w)[8]) {
+  const unsigned int count = (unsigned int)std::min<unsigned long long>(kWordsPerLane, n - i0);
+  const unsigned long long half = n >> 1;
+  const unsigned int plane = i0 >= half ? 1u : 0u;
+  const unsigned long long in_plane = i0 - plane * half;
+  const unsigned long long j = in_plane / a.block_words;
+  const unsigned long long within = in_plane - j * a.block_words;
+  if (count == kWordsPerLane && within + kWordsPerLane <= a.block_words &&
+      i0 + kWordsPerLane <= (plane + 1ull) * half) {
+    const unsigned long long blk = a.ids ? (unsigned long long)a.ids[d.ids_offset + j] : j;
+    const uint16_t* src = a.kv + plane * a.plane_stride + blk * a.block_stride + within;
+    if (((uintptr_t)src & 15) == 0) {
+      const u32x4 v0 = load_stream16(src), v1 = load_stream16(src + 8);
+      w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+      w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+      return count;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) w[k] = 0;
+  for (unsigned int k = 0; k < count; ++k)
+    w[k >> 1] |= (uint32_t)a.kv[word_offset(a, d, i0 + k)] << (16 * (k & 1));
+  return count;
+}
+
+__device__ __forceinline__ unsigned int word_at(const uint32_t (&w)[8], unsigned int k) {
+  return (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+}
+
+// Workgroup (x, y): tile x of payload y; each thread marks the values of its 16
+// words in LDS byte maps, one ballot per wave turns them into mask bits.
+__global__ __launch_bounds__(kThreads) void torchop_presence(LaunchArgs a) {
+  __shared__ unsigned char s_high[256];
+  __shared__ unsigned char s_nib[64];
+  const unsigned int tid = threadIdx.x;
+  const PayloadDesc d = a.p[blockIdx.y];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long tile0 = (unsigned long long)blockIdx.x * kTorchopTile;
+  if (tile0 >= n) return;  // the whole workgroup
+  s_high[tid] = 0;
+  if (tid < 64) s_nib[tid] = 0;
+  __syncthreads();
+  const unsigned long long i0 = tile0 + (unsigned long long)tid * kWordsPerLane;
+  if (i0 < n) {
+    uint32_t w[8];
+    const unsigned int count = load_words16(a, d, n, i0, w);
+    for (unsigned int k = 0; k < count; ++k) {
+      const unsigned int v = word_at(w, k);
+      s_high[v >> 8] = 1;
+      s_nib[v & 15] = 1;
+      s_nib[16 + ((v >> 4) & 15)] = 1;
+    }
+  }
+  __syncthreads();
+  const unsigned int lane = tid & (kWave - 1), wave = tid >> 6;
+  unsigned int* rec = a.workspace + kTorchopRecordWords * (d.tile_begin + blockIdx.x);
+  const unsigned long long high = __ballot(s_high[tid] != 0);
+  if (lane == 0) {
+    rec[2 * wave] = (unsigned int)high;
+    rec[2 * wave + 1] = (unsigned int)(high >> 32);
+  }
+  if (wave == 0) {
+    const unsigned long long nib = __ballot(lane < 32 && s_nib[lane] != 0);
+    if (lane == 0) rec[8] = (unsigned int)nib;
+  }
+}
+
+__device__ __forceinline__ unsigned int bit_length(unsigned int x) {
+  return x ? 32u - (unsigned int)__clz((int)x) : 0u;
+}
+
+// Width of a nibble plane with k distinct values (vllm_connector.py:3287).
+__device__ __forceinline__ unsigned int nibble_width(unsigned int mask) {
+  const unsigned int k = (unsigned int)__popc(mask);
+  return k <= 2 ? 1u : k <= 4 ? 2u : 4u;
+}
+
+// The four nibble planes' value masks (bits 0-3, 4-7, 8-11, 12-15 of the words)
+// from a plan's presence masks.
+__device__ __forceinline__ void nibble_masks(const unsigned int (&high)[8], unsigned int nibbles,
+                                             unsigned int (&m)[4]) {
+  m[0] = nibbles & 0xFFFFu;
+  m[1] = nibbles >> 16;
+  unsigned int lo = 0, hi = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    lo |= (high[k] & 0xFFFFu) | (high[k] >> 16);        // high byte & 15 (bits 8-11)
+    hi |= ((high[k] & 0xFFFFu) != 0 ? 1u : 0u) << (2 * k);  // high byte >> 4 (bits 12-15)
+    hi |= ((high[k] >> 16) != 0 ? 1u : 0u) << (2 * k + 1);
+  }
+  m[2] = lo;
+  m[3] = hi;
+}
+
+// One workgroup per payload: OR of its tile records, then the reference's format
+// choice (vllm_connector.py:3210-3213, 3219-3222, 3250-3253, 3279-3290, 3310-3311).
+__global__ __launch_bounds__(kThreads) void torchop_plan(LaunchArgs a, TorchopPlan* plans) {
+  __shared__ unsigned int s_or[9];
+  const unsigned int tid = threadIdx.x;
+  const PayloadDesc d = a.p[blockIdx.x];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned int tiles = (unsigned int)((n + kTorchopTile - 1) / kTorchopTile);
+  if (tid < 9) s_or[tid] = 0;
+  __syncthreads();
+  unsigned int part[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (unsigned int t = tid; t < tiles; t += kThreads) {
+    const unsigned int* rec = a.workspace + kTorchopRecordWords * (d.tile_begin + t);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) part[k] |= rec[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 9; ++k)
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) part[k] |= __shfl_xor(part[k], off, kWave);
+  if ((tid & (kWave - 1)) == 0) {
+#pragma unroll
+    for (int k = 0; k < 9; ++k)
+      if (part[k]) atomicOr(&s_or[k], part[k]);
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  TorchopPlan p{};
+  for (int k = 0; k < 8; ++k) p.high[k] = s_or[k];
+  p.nibbles = s_or[8];
+  p.words = n;
+  p.mode = kTorchopNone;
+  const unsigned long long raw = 2 * n;
+  // sign / magnitude: magnitudes present = high bytes with the sign bit dropped
+  unsigned int mags[4];
+  for (int k = 0; k < 4; ++k) mags[k] = p.high[k] | p.high[k + 4];
+  unsigned int mag_min = 0, mag_max = 0;
+  bool seen = false;
+  for (int k = 0; k < 4; ++k) {
+    if (!mags[k]) continue;
+    if (!seen) mag_min = 32 * k + (unsigned int)__ffs((int)mags[k]) - 1;
+    mag_max = 32 * k + 31 - (unsigned int)__clz((int)mags[k]);
+    seen = true;
+  }
+  const unsigned int mag_width = max(1u, bit_length(mag_max - mag_min));
+  if (mag_width < 7) {
+    const unsigned long long size = 3 + n + (n + 7) / 8 + (n * mag_width + 7) / 8;
+    if (size < raw) {
+      p.mode = 2;
+      p.width[0] = (unsigned char)mag_width;
+      p.mag_min = (unsigned char)mag_min;
+      p.encoded_bytes = size;
+    }
+  }
+  if (p.mode == kTorchopNone) {
+    unsigned int distinct = 0;
+    for (int k = 0; k < 8; ++k) distinct += (unsigned int)__popc(p.high[k]);
+    const unsigned int width = max(1u, bit_length(distinct - 1));
+    if (width < 8) {
+      const unsigned long long size = 258 + n + (n * width + 7) / 8;
+      if (size < raw) {
+        p.mode = 0;
+        p.width[0] = (unsigned char)width;
+        p.encoded_bytes = size;
+      }
+    }
+  }
+  if (p.mode == kTorchopNone) {
+    unsigned int m[4];
+    nibble_masks(p.high, p.nibbles, m);
+    unsigned long long size = 69;
+    for (int q = 0; q < 4; ++q) {
+      const unsigned int w = nibble_width(m[q]);
+      p.width[q] = (unsigned char)w;
+      size += (n * w + 7) / 8;
+    }
+    if (size < raw) {
+      p.mode = 1;
+      p.encoded_bytes = size;
+    } else {
+      for (int q = 0; q < 4; ++q) p.width[q] = 0;
+    }
+  }
+  plans[blockIdx.x] = p;
+}
+
+// Code section write of one thread: 16 codes (count of them valid, the others 0)
+// of `width` bits each, LSB-first, at bit 16 * width * (i0 / 16) of the section:
+// whole bytes, ceil(count * width / 8) of them.
+__device__ __forceinline__ void put_codes(unsigned char* sec, unsigned long long i0,
+                                          const unsigned int (&code)[16], unsigned int count,
+                                          unsigned int width) {
+  unsigned long long lo = 0, hi = 0;
+#pragma unroll
+  for (unsigned int k = 0; k < 16; ++k) {
+    const unsigned long long c = k < count ? code[k] : 0u;
+    const unsigned int b = k * width;
+    if (b < 64) {
+      lo |= c << b;
+      if (b + width > 64) hi |= c >> (64 - b);
+    } else {
+      hi |= c << (b - 64);
+    }
+  }
+  unsigned char* dst = sec + (i0 * width) / 8;
+  const unsigned int bytes = (count * width + 7) / 8;
+  for (unsigned int j = 0; j < bytes; ++j)
+    dst[j] = (unsigned char)(j < 8 ? lo >> (8 * j) : hi >> (8 * (j - 8)));
+}
+
+// Workgroup (x, y): words [4096 x, 4096 x + 4096) of payload y, 16 per thread;
+// workgroup x == 0 also writes the header. Payloads whose plan declined, or whose
+// plan size is not the size the host laid out, are skipped.
+__global__ __launch_bounds__(kThreads) void torchop_encode(LaunchArgs a, const TorchopPlan* plans,
+                                                           TorchopSizes sizes) {
+  __shared__ unsigned char s_rank[256];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int r = blockIdx.y;
+  const PayloadDesc d = a.p[r];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long tile0 = (unsigned long long)blockIdx.x * kTorchopTile;
+  const TorchopPlan& plan = plans[r];
+  const unsigned int mode = plan.mode;
+  if (tile0 >= n || mode == kTorchopNone || plan.encoded_bytes != sizes.encoded[r] ||
+      plan.words != n)
+    return;  // the whole workgroup
+  unsigned int high[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) high[k] = plan.high[k];
+  unsigned int width[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) width[q] = plan.width[q];
+  const unsigned int mag_min = plan.mag_min;
+  unsigned char* out = a.buf + d.buf_offset;
+
+  // rank tables: mode 0, high byte -> palette index; mode 1, entry 16q + v -> index
+  // of nibble value v in plane q's palette
+  unsigned int nib[4];
+  nibble_masks(high, plan.nibbles, nib);
+  {
+    unsigned int rank = 0, present = 0;
+    if (mode == 0) {
+      // (mask words read from the plan in memory: a per-thread index into a
+      // register array would go through scratch)
+      const unsigned int h = tid;
+      const unsigned int word = plan.high[h >> 5];
+      rank = (unsigned int)__popc(word & ((1u << (h & 31)) - 1u));
+#pragma unroll
+      for (unsigned int k = 0; k < 8; ++k) rank += k < (h >> 5) ? (unsigned int)__popc(high[k]) : 0u;
+      present = (word >> (h & 31)) & 1u;
+    } else if (mode == 1 && tid < 64) {
+      const unsigned int q = tid >> 4, v = tid & 15;
+      rank = (unsigned int)__popc(nib[q] & ((1u << v) - 1u));
+      present = (nib[q] >> v) & 1u;
+    }
+    s_rank[tid] = (unsigned char)rank;
+    if (blockIdx.x == 0) {
+      // header (vllm_connector.py:3226-3228, 3259-3261, 3300-3307)
+      if (mode == 2) {
+        if (tid == 0) out[0] = 2;
+        if (tid == 1) out[1] = (unsigned char)width[0];
+        if (tid == 2) out[2] = (unsigned char)mag_min;
+      } else if (mode == 0) {
+        unsigned int distinct = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) distinct += (unsigned int)__popc(high[k]);
+        if (tid == 0) {
+          out[0] = 0;
+          out[1] = (unsigned char)width[0];
+        }
+        if (present) out[2 + rank] = (unsigned char)tid;
+        if (tid >= distinct) out[2 + tid] = 0;
+      } else if (tid < 64) {
+        const unsigned int q = tid >> 4, v = tid & 15;
+        if (present) out[5 + 16 * q + rank] = (unsigned char)v;
+        if (v >= (unsigned int)__popc(nib[q])) out[5 + 16 * q + v] = 0;
+        if (tid == 0) out[0] = 1;
+        if (tid < 4) out[1 + tid] = (unsigned char)width[tid];
+      }
+    }
+  }
+  __syncthreads();
+  const unsigned long long i0 = tile0 + (unsigned long long)tid * kWordsPerLane;
+  if (i0 >= n) return;
+  uint32_t w[8];
+  const unsigned int count = load_words16(a, d, n, i0, w);
+  unsigned int code[16];
+  if (mode == 2 || mode == 0) {
+    // low bytes, then (mode 2) sign bits and magnitudes, (mode 0) palette indices
+    const unsigned long long low_at = mode == 2 ? 3 : 258;
+    for (unsigned int k = 0; k < count; ++k) out[low_at + i0 + k] = (unsigned char)word_at(w, k);
+    if (mode == 2) {
+      unsigned int signs = 0;
+#pragma unroll
+      for (unsigned int k = 0; k < 16; ++k) {
+        const unsigned int v = word_at(w, k);
+        signs |= (k < count ? (v >> 15) : 0u) << k;
+        code[k] = ((v >> 8) & 0x7Fu) - mag_min;
+      }
+      unsigned char* sign_sec = out + 3 + n;
+      sign_sec[i0 / 8] = (unsigned char)signs;
+      if (count > 8) sign_sec[i0 / 8 + 1] = (unsigned char)(signs >> 8);
+      put_codes(out + 3 + n + (n + 7) / 8, i0, code, count, width[0]);
+    } else {
+#pragma unroll
+      for (unsigned int k = 0; k < 16; ++k) code[k] = s_rank[word_at(w, k) >> 8];
+      put_codes(out + 258 + n, i0, code, count, width[0]);
+    }
+    return;
+  }
+  unsigned long long at = 69;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (unsigned int k = 0; k < 16; ++k) code[k] = s_rank[16 * q + ((word_at(w, k) >> (4 * q)) & 15)];
+    put_codes(out + at, i0, code, count, width[q]);
+    at += (n * width[q] + 7) / 8;
+  }
+}
+
 }  // namespace
 }  // namespace unchainkv
 
@@ -200,6 +554,155 @@ extern "C" long long kvq_splitzip_bf16_decode_torchop_paged(
     hipLaunchKernelGGL(torchop_decode, grid, dim3(kThreads), 0, stream, a, sizes);
     const hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_decode", st);
+  }
+  return (long long)total;
+}
+
+namespace {
+
+// Tile records of a launch's payloads (first, first + count) start at their
+// payloads' tile prefix over the whole call.
+unsigned long long torchop_tiles(unsigned long long n) {
+  return (n + kTorchopTile - 1) / kTorchopTile;
+}
+
+// Fills the launch arguments of payloads [first, first + count); false when a
+// payload's word count is past the kernels' limit.
+bool torchop_args(LaunchArgs& a, unsigned long long kv_ptr, unsigned long long plane_stride,
+                  unsigned long long block_stride, unsigned long long block_words,
+                  unsigned long long block_ids_ptr, const unsigned long long* block_offsets,
+                  unsigned long long first, unsigned int count, unsigned long long tile_prefix,
+                  unsigned long long& max_n) {
+  a = LaunchArgs{};
+  a.kv = reinterpret_cast<uint16_t*>(kv_ptr);
+  a.ids = reinterpret_cast<const long long*>(block_ids_ptr);
+  a.plane_stride = plane_stride;
+  a.block_stride = block_stride;
+  a.block_words = block_words;
+  a.payload_count = count;
+  max_n = 0;
+  unsigned long long tile = tile_prefix;
+  for (unsigned int k = 0; k < count; ++k) {
+    const unsigned long long r = first + k;
+    const unsigned long long blocks = block_offsets[r + 1] - block_offsets[r];
+    const unsigned long long n = 2 * blocks * block_words;
+    if (n > 0x7FFFFFFFULL || tile > 0xFFFFFFFFULL) return false;
+    a.p[k].ids_offset = block_offsets[r];
+    a.p[k].block_count = (unsigned int)blocks;
+    a.p[k].tile_begin = (unsigned int)tile;
+    tile += torchop_tiles(n);
+    max_n = std::max(max_n, n);
+  }
+  return true;
+}
+
+bool torchop_tables_ok(unsigned long long kv_ptr, unsigned long long block_words,
+                       unsigned long long block_ids_ptr, const unsigned long long* block_offsets,
+                       unsigned long long payload_count) {
+  if (kv_ptr == 0 || block_ids_ptr == 0 || block_offsets == nullptr || payload_count == 0 ||
+      block_words == 0 || block_words > 0xFFFFFFFFULL || kv_ptr % 2 != 0)
+    return false;
+  for (unsigned long long r = 0; r < payload_count; ++r)
+    if (block_offsets[r + 1] <= block_offsets[r]) return false;
+  return true;
+}
+
+}  // namespace
+
+// Plan records are 64 bytes per payload.
+extern "C" unsigned long long kvq_splitzip_torchop_plan_bytes() { return sizeof(TorchopPlan); }
+
+// Workspace of kvq_splitzip_bf16_plan_torchop_paged: 64 bytes per 4096-word tile of
+// every payload; 0 when the block offsets do not increase.
+extern "C" unsigned long long kvq_splitzip_torchop_workspace_bytes(
+    unsigned long long block_words, const unsigned long long* block_offsets,
+    unsigned long long payload_count) {
+  if (block_offsets == nullptr || payload_count == 0 || block_words == 0) return 0;
+  unsigned long long tiles = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    if (block_offsets[r + 1] <= block_offsets[r]) return 0;
+    tiles += torchop_tiles(2 * (block_offsets[r + 1] - block_offsets[r]) * block_words);
+  }
+  return tiles * kTorchopRecordWords * 4;
+}
+
+extern "C" long long kvq_splitzip_bf16_plan_torchop_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long workspace_ptr, unsigned long long workspace_bytes,
+    unsigned long long plans_ptr, unsigned long long stream_ptr) {
+  if (!torchop_tables_ok(kv_ptr, block_words, block_ids_ptr, block_offsets, payload_count) ||
+      workspace_ptr == 0 || plans_ptr == 0 || workspace_ptr % 4 != 0 || plans_ptr % 8 != 0)
+    return 0;
+  const unsigned long long need =
+      kvq_splitzip_torchop_workspace_bytes(block_words, block_offsets, payload_count);
+  if (need == 0 || workspace_bytes < need) return 0;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  unsigned long long tile_prefix = 0;
+  for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
+    const unsigned int count =
+        (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
+    LaunchArgs a;
+    unsigned long long max_n = 0;
+    if (!torchop_args(a, kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                      block_offsets, first, count, tile_prefix, max_n))
+      return 0;
+    a.workspace = reinterpret_cast<unsigned int*>(workspace_ptr);
+    hipLaunchKernelGGL(torchop_presence, dim3((unsigned int)torchop_tiles(max_n), count),
+                       dim3(kThreads), 0, stream, a);
+    hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return fail("torchop_presence", st);
+    hipLaunchKernelGGL(torchop_plan, dim3(count), dim3(kThreads), 0, stream, a,
+                       reinterpret_cast<TorchopPlan*>(plans_ptr) + first);
+    st = hipGetLastError();
+    if (st != hipSuccess) return fail("torchop_plan", st);
+    for (unsigned int k = 0; k < count; ++k)
+      tile_prefix += torchop_tiles(2ull * a.p[k].block_count * block_words);
+  }
+  return (long long)payload_count;
+}
+
+extern "C" long long kvq_splitzip_bf16_encode_torchop_paged(
+    unsigned long long kv_ptr, unsigned long long plane_stride, unsigned long long block_stride,
+    unsigned long long block_words, unsigned long long block_ids_ptr,
+    const unsigned long long* block_offsets, unsigned long long payload_count,
+    unsigned long long plans_ptr, unsigned long long out_ptr,
+    const unsigned long long* out_offsets, const unsigned long long* encoded_bytes,
+    unsigned long long out_capacity, unsigned long long stream_ptr) {
+  if (!torchop_tables_ok(kv_ptr, block_words, block_ids_ptr, block_offsets, payload_count) ||
+      plans_ptr == 0 || plans_ptr % 8 != 0 || out_ptr == 0 || out_offsets == nullptr ||
+      encoded_bytes == nullptr)
+    return 0;
+  unsigned long long total = 0;
+  for (unsigned long long r = 0; r < payload_count; ++r) {
+    const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
+    const unsigned long long size = encoded_bytes[r];
+    if (size == 0) continue;  // declined by its plan: nothing to write
+    if (size >= 2 * n || out_offsets[r] > out_capacity || size > out_capacity - out_offsets[r])
+      return 0;
+    total += size;
+  }
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
+    const unsigned int count =
+        (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
+    LaunchArgs a;
+    unsigned long long max_n = 0;
+    if (!torchop_args(a, kv_ptr, plane_stride, block_stride, block_words, block_ids_ptr,
+                      block_offsets, first, count, 0, max_n))
+      return 0;
+    a.buf = reinterpret_cast<unsigned char*>(out_ptr);
+    TorchopSizes sizes{};
+    for (unsigned int k = 0; k < count; ++k) {
+      a.p[k].buf_offset = out_offsets[first + k];
+      sizes.encoded[k] = encoded_bytes[first + k];
+    }
+    hipLaunchKernelGGL(torchop_encode, dim3((unsigned int)torchop_tiles(max_n), count),
+                       dim3(kThreads), 0, stream, a,
+                       reinterpret_cast<const TorchopPlan*>(plans_ptr) + first, sizes);
+    const hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return fail("torchop_encode", st);
   }
   return (long long)total;
 }

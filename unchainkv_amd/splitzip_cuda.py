@@ -141,6 +141,20 @@ _SIGNATURES = (
         ctypes.c_longlong,
         False,
     ),
+    ("kvq_splitzip_torchop_plan_bytes", [], _U64, False),
+    ("kvq_splitzip_torchop_workspace_bytes", [_U64, _U64P, _U64], _U64, False),
+    (
+        "kvq_splitzip_bf16_plan_torchop_paged",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
+    (
+        "kvq_splitzip_bf16_encode_torchop_paged",
+        [_U64, _U64, _U64, _U64, _U64, _U64P, _U64, _U64, _U64, _U64P, _U64P, _U64, _U64],
+        ctypes.c_longlong,
+        False,
+    ),
     (
         "kvq_splitzip_bf16_decode_mode_paged",
         [_U64, _U64P, _U64P, _U64, _U64, _U64, _U64, _U64, _U64, _U64P, _U64, ctypes.c_int],
@@ -993,6 +1007,93 @@ def decode_torchop_paged(source, src_offsets, encoded_bytes, kv_layer,
     if copied < 0:
         _raise_last(lib, "splitzip torch-op paged decode failed")
     return int(copied) or None
+
+
+# ---------------------------------------------------------------------------
+# torch-op encode (the sender's formats for small requests)
+
+TORCHOP_PLAN_BYTES = 64
+
+
+def plan_torchop_paged(kv_layer, batch: PagedBatch, plans=None):
+    """Queue the plan of the reference connector's torch-op encode of every request
+    of ``batch`` (src/unchain_kv/vllm_connector.py:3204-3343: sign/magnitude, else
+    the high-byte palette, else the nibble planes, else none). Returns the device
+    tensor of 64-byte plan records (``plans`` when given), or ``None`` when the
+    library declines; ``read_torchop_plans`` turns a host copy into sizes."""
+    lib = _load()
+    plan = getattr(lib, "kvq_splitzip_bf16_plan_torchop_paged", None) if lib else None
+    if plan is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    size = int(lib.kvq_splitzip_torchop_workspace_bytes(batch.block_words, batch._block_offsets,
+                                                        batch.payload_count))
+    if size == 0:
+        return None
+    if plans is None:
+        plans = torch.empty(TORCHOP_PLAN_BYTES * batch.payload_count, dtype=torch.uint8,
+                            device=kv_layer.device)
+    elif plans.dtype != torch.uint8 or plans.numel() < TORCHOP_PLAN_BYTES * batch.payload_count \
+            or not plans.is_contiguous() or plans.device != kv_layer.device:
+        return None
+    workspace = torch.empty(size, dtype=torch.uint8, device=kv_layer.device)
+    stream = _stream_handle(kv_layer.device, torch)
+    got = plan(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+               batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+               batch.payload_count, int(workspace.data_ptr()), size, int(plans.data_ptr()),
+               int(stream))
+    if got < 0:
+        _raise_last(lib, "splitzip torch-op plan failed")
+    if not got:
+        return None
+    # the workspace must outlive the queued kernels
+    workspace.record_stream(torch.cuda.current_stream(kv_layer.device))
+    return plans
+
+
+def read_torchop_plans(host_plans) -> list[tuple[int, int]]:
+    """(mode, encoded bytes) per request from a host copy of the plan records; mode
+    255 and 0 bytes for a request no torch-op format compresses."""
+    import numpy as np
+
+    raw = np.asarray(host_plans, dtype=np.uint8).reshape(-1, TORCHOP_PLAN_BYTES)
+    sizes = raw[:, 48:56].copy().view(np.uint64).reshape(-1)
+    return [(int(raw[r, 36]), int(sizes[r])) for r in range(raw.shape[0])]
+
+
+def encode_torchop_paged(kv_layer, batch: PagedBatch, plans, out, out_offsets,
+                         encoded_bytes) -> int | None:
+    """Write request r's torch-op payload, as the reference's encoder writes it, to
+    ``out[out_offsets[r]:][:encoded_bytes[r]]`` per its plan (``encoded_bytes[r]``
+    from ``read_torchop_plans``; 0 skips the request). Returns the total encoded
+    bytes, or ``None`` when the library declines."""
+    lib = _load()
+    encode = getattr(lib, "kvq_splitzip_bf16_encode_torchop_paged", None) if lib else None
+    if encode is None:
+        return None
+    import torch
+
+    if not _paged_layout_ok(kv_layer, batch, torch):
+        return None
+    if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    if plans.numel() < TORCHOP_PLAN_BYTES * batch.payload_count or plans.device != out.device:
+        return None
+    if len(out_offsets) != batch.payload_count or len(encoded_bytes) != batch.payload_count:
+        return None
+    offs = batch._c_array(out_offsets, None, None)
+    encs = batch._c_array(encoded_bytes, None, None)
+    stream = _stream_handle(kv_layer.device, torch)
+    got = encode(int(kv_layer.data_ptr()), int(kv_layer.stride(0)), int(kv_layer.stride(1)),
+                 batch.block_words, int(batch.ids.data_ptr()), batch._block_offsets,
+                 batch.payload_count, int(plans.data_ptr()), int(out.data_ptr()), offs, encs,
+                 int(out.numel()), int(stream))
+    if got < 0:
+        _raise_last(lib, "splitzip torch-op encode failed")
+    return int(got) if got or not any(encoded_bytes) else None
 
 
 # ---------------------------------------------------------------------------
