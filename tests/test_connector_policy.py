@@ -99,6 +99,96 @@ def test_codec_choice_top16_large_fixed6_small_and_fixed5_rules():
     assert both._choose_bits(0, MIB)[0] == BITS_FIXED6
 
 
+def test_native_codec_from_1_mib_or_with_top16_native_decode():
+    """prefer_native (vllm_connector.py:3043-3046): the native codec for 1 MiB or
+    more, or for every size while Top-16 with native decode is on; below that the
+    torch-op formats."""
+    plain, _ = codec()
+    assert plain._prefer_native(MIB) and not plain._prefer_native(MIB - 2)
+    assert codec(top16=True)[0]._prefer_native(4096)
+    no_native = codec(top16=True, native_decode=False)[0]
+    assert not no_native._prefer_native(4096) and no_native._prefer_native(MIB)
+    assert not codec(fixed5=True)[0]._prefer_native(4096)
+
+
+def test_torchop_declines_go_raw_and_a_declined_first_half_sends_the_request_whole():
+    """A request that no torch-op format compresses is sent as raw words
+    (raw_passthrough, vllm_connector.py:2685-2711); a two-chunk request whose first
+    half is declined is sent whole with the codec choice for its full size
+    (:2741-2747, here a torch-op payload again, or fixed6 from 1 MiB); a declined
+    second half alone fails (:2745-2746)."""
+    from unchainkv_amd.connector import (BITS_PASSTHROUGH, BITS_TORCHOP, LayerPayload,
+                                         PendingLayer)
+
+    bw = 8
+
+    def pending_for(c, tables):
+        payloads = []
+        for r, ids in enumerate(tables):
+            raw = 2 * len(ids) * bw * 2
+            if c._two_chunks(ids):
+                half = len(ids) // 2
+                for k in range(2):
+                    payloads.append(LayerPayload(r, ids[k * half:(k + 1) * half], raw // 2,
+                                                 BITS_TORCHOP, BITS_TORCHOP, chunk_index=k,
+                                                 chunks_in_layer=2, request_blocks=len(ids)))
+            else:
+                payloads.append(LayerPayload(r, ids, raw, BITS_TORCHOP, BITS_TORCHOP))
+        return PendingLayer(3, None, bw, payloads)
+
+    def run(c, pending, declines):
+        calls, raw = [], []
+
+        def group(pending_, members, torch):
+            calls.append([(p.request, p.chunk_index, p.chunks_in_layer, tuple(p.block_ids))
+                          for p in members])
+            return [p for p in members if declines(p)]
+
+        def stage(pending_, members, torch):
+            raw.extend(members)
+            for p in members:
+                p.bits = BITS_PASSTHROUGH
+
+        c._torchop_group, c._stage_passthrough = group, stage
+        c._torchop_payloads(pending, torch=None)
+        return calls, raw
+
+    c, _ = codec(chunks=2)
+    pending = pending_for(c, [[1], [10, 11, 12, 13], [20, 21], [30, 31, 32, 33]])
+    # request 0 incompressible; request 1's first half declined, its whole request
+    # then accepted; request 2's halves accepted; request 3's first half declined and
+    # the whole request declined again
+    calls, raw = run(c, pending, lambda p: p.request == 0 or
+                     (p.request in (1, 3) and p.chunks_in_layer == 2 and p.chunk_index == 0) or
+                     (p.request == 3 and p.chunks_in_layer == 1))
+    assert calls[0] == [(0, 0, 1, (1,)), (1, 0, 2, (10, 11)), (1, 1, 2, (12, 13)),
+                        (2, 0, 2, (20,)), (2, 1, 2, (21,)), (3, 0, 2, (30, 31)),
+                        (3, 1, 2, (32, 33))]
+    assert calls[1] == [(1, 0, 1, (10, 11, 12, 13)), (3, 0, 1, (30, 31, 32, 33))]
+    assert [(p.request, p.chunks_in_layer, p.bits) for p in pending.payloads] == [
+        (0, 1, BITS_PASSTHROUGH), (1, 1, BITS_TORCHOP), (2, 2, BITS_TORCHOP),
+        (2, 2, BITS_TORCHOP), (3, 1, BITS_PASSTHROUGH)]
+    assert [p.request for p in raw] == [0, 3]
+    assert pending.payloads[0].metadata(3, bw)["codec"] == "raw_passthrough"
+    assert pending.payloads[1].metadata(3, bw)["codec"] == "splitzip_bf16"
+
+    # a whole request of 1 MiB or more goes to the native codec (fixed6)
+    big = 1 << 14   # 16 blocks of 64 KiB
+    c2, _ = codec(chunks=2)
+    bw = big
+    pending = pending_for(c2, [list(range(16))])
+    calls, raw = run(c2, pending, lambda p: p.chunk_index == 0)
+    assert len(calls) == 1 and not raw
+    assert [(p.chunks_in_layer, p.bits, p.raw_bytes) for p in pending.payloads] == \
+        [(1, BITS_FIXED6, 16 * 4 * big)]
+
+    c3, _ = codec(chunks=2)
+    bw = 8
+    pending = pending_for(c3, [[5, 6]])
+    with pytest.raises(RuntimeError, match="second chunk"):
+        run(c3, pending, lambda p: p.chunk_index == 1)
+
+
 def test_config_from_environment():
     cfg = CodecConfig.from_env({
         "UNCHAIN_KV_SPLITZIP_TOP16": "1",

@@ -8,8 +8,8 @@ import pytest
 
 import oracle
 from unchainkv_amd import codec_format
-from unchainkv_amd.connector import (BITS_FIXED5, BITS_FIXED6, BITS_RAW, BITS_TOP16,
-                                     CodecConfig, SplitzipLayerCodec)
+from unchainkv_amd.connector import (BITS_FIXED5, BITS_FIXED6, BITS_PASSTHROUGH, BITS_RAW,
+                                     BITS_TOP16, BITS_TORCHOP, CodecConfig, SplitzipLayerCodec)
 from unchainkv_amd.trace import RecordingTrace
 
 torch = pytest.importorskip("torch")
@@ -288,11 +288,12 @@ def test_layer_travels_in_compressed_native_frames(sz, codebooks):
         assert np.array_equal(dst[:, recv[name]], src[:, t]), name
 
 
-def test_sender_splits_fixed6_requests_into_two_kvc2_chunks(sz, codebooks):
-    """UNCHAIN_KV_SPLITZIP_CHUNKS=2 on a fixed6 layer (vllm_connector.py:2718-2799):
-    a request with an even number of blocks in one run leaves as two fixed6
-    half-payloads in KVC2 frames, the others as one KVC1 frame; every payload equals
-    the oracle's fixed6 of its blocks and the receiver restores all of them."""
+def test_sender_splits_requests_into_two_kvc2_chunks(sz, codebooks):
+    """UNCHAIN_KV_SPLITZIP_CHUNKS=2 without Top-16 (vllm_connector.py:2718-2799): a
+    request with an even number of blocks in one run leaves as two half-payloads in
+    KVC2 frames -- fixed6 for halves of 1 MiB or more, a torch-op format below --
+    the others as one KVC1 frame (torch-op below 1 MiB); every payload equals the
+    oracle's encoding of its blocks and the receiver restores all of them."""
     from unchainkv_amd import frames
 
     say("connector two-chunk frames")
@@ -303,29 +304,99 @@ def test_sender_splits_fixed6_requests_into_two_kvc2_chunks(sz, codebooks):
     words = ((highs[rng.integers(0, 40, n)] << 8) | rng.integers(0, 256, n).astype(np.uint16))
     words = words.astype(np.uint16)
     kv = layer_from_words(words, pool)
-    tables = [list(range(10, 22)), [40, 41, 42], [60, 62, 61, 63]]  # run, odd, not a run
+    # a 32-block run (halves of 1 MiB), a 12-block run (halves below 1 MiB), odd, not a run
+    tables = [list(range(10, 42)), list(range(50, 62)), [66, 67, 68], [70, 72, 71, 73]]
     codec = SplitzipLayerCodec(CodecConfig(chunks=2), trace=RecordingTrace())
     pending = codec.save_kv_layer(3, kv, tables)
     payloads = codec.ready(pending)
-    assert [(p.request, p.chunk_index, p.chunks_in_layer) for p in payloads] == \
-        [(0, 0, 2), (0, 1, 2), (1, 0, 1), (2, 0, 1)]
+    assert [(p.request, p.chunk_index, p.chunks_in_layer, p.bits) for p in payloads] == \
+        [(0, 0, 2, BITS_FIXED6), (0, 1, 2, BITS_FIXED6), (1, 0, 2, BITS_TORCHOP),
+         (1, 1, 2, BITS_TORCHOP), (2, 0, 1, BITS_TORCHOP), (3, 0, 1, BITS_TORCHOP)]
     host = words.reshape(2, pool, BW)
     for p in payloads:
-        assert p.bits == BITS_FIXED6 and p.view[0] == codec_format.MODE_FIXED6
-        assert bytes(p.view) == bytes(oracle.fixed6_encode(host[:, p.block_ids].reshape(-1)))
-    parts = SplitzipLayerCodec.frames(3, payloads, BW, "t2", ["a", "b", "c"])
+        blocks = host[:, p.block_ids].reshape(-1)
+        expected = oracle.fixed6_encode(blocks) if p.bits == BITS_FIXED6 else \
+            oracle.encode_torchop(blocks)
+        assert bytes(p.view) == bytes(expected)
+    assert {p.view[0] for p in payloads if p.bits == BITS_TORCHOP} == {codec_format.MODE_PALETTE}
+    parts = SplitzipLayerCodec.frames(3, payloads, BW, "t2", ["a", "b", "c", "d"])
     parsed = [frames.parse_compressed_native(b"".join(x[1:])) for x in parts]
     assert [(f.request_id, f.chunks_in_layer, f.block_count) for f in parsed] == \
-        [("a", 2, 12), ("a", 2, 12), ("b", 1, 3), ("c", 1, 4)]
-    recv = {"a": list(range(50, 62)), "b": [1, 3, 5], "c": [70, 71, 72, 73]}
+        [("a", 2, 32), ("a", 2, 32), ("b", 2, 12), ("b", 2, 12), ("c", 1, 3), ("d", 1, 4)]
+    perm = rng.permutation(pool).tolist()
+    recv = {"a": perm[:32], "b": perm[32:44], "c": perm[44:47], "d": perm[47:51]}
     target = torch.zeros_like(kv)
     got = codec.restore_frames(target, [b"".join(x[1:]) for x in parts], recv)
     torch.cuda.synchronize()
     codec.release(pending)
     dst = u16(target).reshape(2, pool, BW)
-    for name, t in zip("abc", tables):
+    for name, t in zip("abcd", tables):
         assert got[name] == (len(t), 4 * BW * len(t)), name
         assert np.array_equal(dst[:, recv[name]], host[:, t]), name
+
+
+def test_small_requests_take_the_torchop_formats(sz, codebooks):
+    """Without Top-16 a request below 1 MiB leaves in the reference's torch-op
+    formats (vllm_connector.py:3043-3046, 3204-3343): sign/magnitude, the high-byte
+    palette or the nibble planes, byte for byte the oracle's (which the reference
+    connector's own payloads pin); an incompressible one as raw words with codec
+    raw_passthrough (:2685-2711); a 1 MiB request with the native fixed6. All of
+    them go through KVC1 frames and are restored into the receiver's blocks."""
+    from unchainkv_amd import frames
+
+    say("connector torch-op sender")
+    rng = np.random.default_rng(23)
+    pool = 40
+    host = np.empty((2, pool, BW), np.uint16)
+    low = rng.integers(0, 256, (2, pool, BW)).astype(np.uint16)
+    sign = rng.integers(0, 2, (2, pool, BW)).astype(np.uint16) << 15
+    host[:] = sign | ((0x38 + rng.integers(0, 8, (2, pool, BW)).astype(np.uint16)) << 8) | low
+    palette = np.array([0x00, 0x7F, 0x81, 0x3C, 0xC0], np.uint16)   # 7-bit magnitudes
+    host[:, 4:7] = (palette[rng.integers(0, 5, (2, 3, BW))] << 8) | low[:, 4:7]
+    nib = rng.integers(0, 1 << 16, (2, 2, BW)).astype(np.uint16) & 0xF0F3
+    nib[..., :256] = (np.arange(256, dtype=np.uint16) << 8) | (nib[..., :256] & 0xF3)
+    host[:, 8:10] = nib                                              # 256 high bytes
+    host[:, 12:14] = rng.integers(0, 1 << 16, (2, 2, BW))            # incompressible
+    highs = rng.choice(256, 50, replace=False).astype(np.uint16)
+    host[:, 20:36] = (highs[rng.integers(0, 50, (2, 16, BW))] << 8) | low[:, 20:36]
+    kv = layer_from_words(host.reshape(-1), pool)
+    tables = [[1, 3], [4, 5, 6], [8, 9], [12, 13], list(range(20, 36))]
+    codec = SplitzipLayerCodec(CodecConfig(), trace=RecordingTrace())
+    pending = codec.save_kv_layer(2, kv, tables)
+    payloads = codec.ready(pending)
+    assert [p.bits for p in payloads] == [BITS_TORCHOP] * 3 + [BITS_PASSTHROUGH, BITS_FIXED6]
+    for p, mode in zip(payloads[:3], (codec_format.MODE_SIGNMAG, codec_format.MODE_PALETTE,
+                                      codec_format.MODE_NIBBLES)):
+        blocks = host[:, p.block_ids].reshape(-1)
+        assert p.view[0] == mode
+        assert bytes(p.view) == bytes(oracle.encode_torchop(blocks))
+        assert p.metadata(2, BW)["codec"] == "splitzip_bf16"
+    raw = payloads[3]
+    assert raw.metadata(2, BW)["codec"] == "raw_passthrough"
+    assert raw.encoded_bytes == raw.raw_bytes
+    assert bytes(raw.view) == host[:, [12, 13]].tobytes()
+    assert bytes(payloads[4].view) == bytes(oracle.fixed6_encode(host[:, 20:36].reshape(-1)))
+    names = [f"r{r}" for r in range(len(tables))]
+    parts = SplitzipLayerCodec.frames(2, payloads, BW, "t3", names)
+    perm = rng.permutation(pool).tolist()
+    recv, at = {}, 0
+    for name, t in zip(names, tables):
+        recv[name] = perm[at:at + len(t)]
+        at += len(t)
+    target = torch.zeros_like(kv)
+    got = codec.restore_frames(target, [b"".join(x[1:]) for x in parts], recv)
+    # the same payloads through the per-layer batch restore, metadata as sent
+    target2 = torch.zeros_like(kv)
+    results = codec.load_kv_layer_batch(2, target2, [
+        (recv[name], bytes(p.view), p.metadata(2, BW)) for name, p in zip(names, payloads)])
+    torch.cuda.synchronize()
+    codec.release(pending)
+    for dst_kv in (target, target2):
+        dst = u16(dst_kv).reshape(2, pool, BW)
+        for name, t in zip(names, tables):
+            assert np.array_equal(dst[:, recv[name]], host[:, t]), name
+    assert [got[name] for name in names] == [(len(t), 4 * BW * len(t)) for t in tables]
+    assert results == [(len(t), 4 * BW * len(t)) for t in tables]
 
 
 # ---------------------------------------------------------------------------

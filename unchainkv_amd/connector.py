@@ -27,10 +27,11 @@ This module keeps that codec behaviour and its knobs, batched per layer:
   modes 0-5 (0, 1 and 2, the reference's torch-op codecs, in one launch), raw copy
   of mode 6.
 
-Everything runs on the HIP library; there is no CPU codec path. Modes 0, 1 and 2
-are restored but not produced (the reference sends them only without its native
-codec). Payloads below 1 MiB use fixed6, as the reference does when its codec buffer pool
-is in use. The KV blocks of a saved layer must stay unchanged until ``ready``
+Everything runs on the HIP library; there is no CPU codec path. A request below
+1 MiB is sent in the reference's torch-op formats (modes 2, 0, 1, in the
+reference's order of preference) unless Top-16 with native decode is enabled
+(``prefer_native``, :3043-3046), and as raw words (``raw_passthrough``) when none
+of them is smaller (:2685-2711). The KV blocks of a saved layer must stay unchanged until ``ready``
 returns: the fallback re-encodes read them again (the reference keeps a gathered
 copy instead). The writeback therefore skips an overflowed payload on the GPU (its
 mode byte is checked there), leaving its blocks intact for the fixed6 re-encode;
@@ -110,6 +111,9 @@ TORCHOP = "torchop"
 
 # bits of a payload as the reference's _SplitzipCudaPayload records them
 BITS_TOP16, BITS_FIXED5, BITS_FIXED6, BITS_RAW = 4, 5, 6, 16
+# payloads the reference makes outside _SplitzipCudaPayload, which records no bits:
+# the torch-op formats (modes 0, 1, 2) and raw words sent with codec raw_passthrough
+BITS_TORCHOP, BITS_PASSTHROUGH = 8, 0
 
 
 def _contiguous_runs(values) -> tuple[tuple[int, int], ...]:
@@ -122,10 +126,6 @@ def _contiguous_runs(values) -> tuple[tuple[int, int], ...]:
         else:
             runs.append([value, 1])
     return tuple((start, count) for start, count in runs)
-_MODE_OF_BITS = {BITS_TOP16: codec_format.MODE_TOP16, BITS_FIXED5: codec_format.MODE_FIXED5,
-                 BITS_FIXED6: codec_format.MODE_FIXED6, BITS_RAW: codec_format.MODE_RAW}
-
-
 @dataclass
 class LayerPayload:
     """One request's payload of a layer (the fields of the reference's
@@ -152,10 +152,14 @@ class LayerPayload:
     chunks_in_layer: int = 1
     request_blocks: int = 0          # blocks of the whole request, for a chunk's frame
 
+    @property
+    def codec(self) -> str:
+        return "raw_passthrough" if self.bits == BITS_PASSTHROUGH else "splitzip_bf16"
+
     def metadata(self, layer_index: int, block_words: int) -> dict:
         """Receiver metadata of a compressed-native layer payload."""
         return {"block_count": len(self.block_ids), "raw_block_size": 2 * 2 * block_words,
-                "raw_bytes": self.raw_bytes, "codec": "splitzip_bf16",
+                "raw_bytes": self.raw_bytes, "codec": self.codec,
                 "encoded_bytes": self.encoded_bytes, "_layer_index": layer_index}
 
 
@@ -285,6 +289,12 @@ class SplitzipLayerCodec:
         enabled, and an even number (at least 2) of blocks in one ascending run."""
         return (self.config.chunks == 2 and not self.splitzip_top16 and not self.splitzip_fixed5
                 and len(ids) >= 2 and len(ids) % 2 == 0 and len(_contiguous_runs(ids)) == 1)
+
+    def _prefer_native(self, raw_bytes: int) -> bool:
+        """The native codec for a payload of 1 MiB or more, or for any payload while
+        Top-16 with native decode is enabled; the torch-op formats otherwise
+        (vllm_connector.py:3043-3046)."""
+        return raw_bytes >= TOP16_MIN_BYTES or (self.splitzip_top16 and self.config.native_decode)
 
     def _choose_bits(self, layer_index: int, raw_bytes: int):
         """Codec choice of _splitzip_bf16_native_blocks (vllm_connector.py:3078-3094)."""
@@ -591,18 +601,29 @@ class SplitzipLayerCodec:
                 raise ValueError("every request needs at least one block")
             raw = 2 * len(ids) * block_words * 2
             if self._two_chunks(ids):
-                # each half of the blocks is its own fixed6 payload and frame
+                # each half of the blocks is its own payload and frame (fixed6, or a
+                # torch-op format below 1 MiB)
                 half = len(ids) // 2
+                bits = BITS_FIXED6 if self._prefer_native(raw // 2) else BITS_TORCHOP
                 for chunk in range(2):
                     part = ids[chunk * half:(chunk + 1) * half]
-                    payloads.append(LayerPayload(r, part, raw // 2, BITS_FIXED6, BITS_FIXED6,
+                    payloads.append(LayerPayload(r, part, raw // 2, bits, bits,
                                                  chunk_index=chunk, chunks_in_layer=2,
                                                  request_blocks=len(ids)))
+                continue
+            if not self._prefer_native(raw):
+                payloads.append(LayerPayload(r, ids, raw, BITS_TORCHOP, BITS_TORCHOP))
                 continue
             bits, epoch, probe = self._choose_bits(layer_index, raw)
             payloads.append(LayerPayload(r, ids, raw, bits, bits, epoch, probe))
         pending = PendingLayer(layer_index, kv_layer, block_words, payloads, started=started)
         stream = torch.cuda.current_stream(kv_layer.device)
+
+        if any(p.bits == BITS_TORCHOP for p in payloads):
+            mark = self._gpu_mark(stream, torch)
+            self._torchop_payloads(pending, torch)
+            self._gpu_span(pending, "encode", mark, stream, torch)
+            payloads = pending.payloads
 
         # every group is encoded before the Top-16 writeback overwrites any block
         top_result = None
@@ -659,6 +680,109 @@ class SplitzipLayerCodec:
         self.trace.event("codec_encode_submitted", layer=layer_index, requests=len(payloads),
                          raw_bytes=sum(p.raw_bytes for p in payloads))
         return pending
+
+    # ------------------------------------------------------------------
+    # torch-op formats (vllm_connector.py:3204-3343) and raw passthrough
+
+    def _torchop_group(self, pending: PendingLayer, members: list, torch) -> list:
+        """Plans and encodes ``members`` in the torch-op formats (one plan launch, a
+        host read of the plans' sizes, one encode launch) and stages the payloads;
+        returns the members that no format compresses."""
+        sz = self._lib()
+        kv_layer = pending.kv_layer
+        batch = self._batch([p.block_ids for p in members], pending.block_words, kv_layer.device)
+        plans = sz.plan_torchop_paged(kv_layer, batch)
+        if plans is None:
+            return list(members)
+        # the host waits for the plans, as the reference waits for its magnitude
+        # range (.item()) and palette (torch.unique) before it sizes a payload
+        fields = sz.read_torchop_plans(plans.cpu().numpy())
+        sizes = [size for _, size in fields]
+        offsets, end = [], 0
+        for size in sizes:
+            offsets.append(end)
+            end += size
+        if end:
+            out = torch.empty(end, dtype=torch.uint8, device=kv_layer.device)
+            if sz.encode_torchop_paged(kv_layer, batch, plans, out, offsets, sizes) != end:
+                raise RuntimeError("splitzip torch-op encode declined")
+            group = self._stage(pending, out, torch)
+            for p, off, size in zip(members, offsets, sizes):
+                if size:
+                    p._group, p._offset, p.encoded_bytes = group, off, size
+        return [p for p, size in zip(members, sizes) if not size]
+
+    def _torchop_payloads(self, pending: PendingLayer, torch) -> None:
+        """Encodes the layer's torch-op payloads. A request that no format compresses
+        is sent as its raw words (raw_passthrough, vllm_connector.py:2685-2711). A
+        two-chunk request whose first half is declined is sent whole instead, with
+        the codec choice for its full size (:2741-2747); one whose second half alone
+        is declined fails, as the reference's does (:2745-2746)."""
+        members = [p for p in pending.payloads if p.bits == BITS_TORCHOP]
+        declined = self._torchop_group(pending, members, torch)
+        whole = {p.request for p in declined if p.chunks_in_layer == 2 and p.chunk_index == 0}
+        if any(p.chunks_in_layer == 2 and p.request not in whole for p in declined):
+            raise RuntimeError("splitzip second chunk encode failed")
+        passthrough = [p for p in declined if p.chunks_in_layer == 1]
+        if whole:
+            payloads, again = [], []
+            for p in pending.payloads:
+                if p.request not in whole or p.chunks_in_layer != 2:
+                    payloads.append(p)
+                elif p.chunk_index == 0:
+                    halves = [q for q in pending.payloads
+                              if q.request == p.request and q.chunks_in_layer == 2]
+                    ids = [b for q in sorted(halves, key=lambda q: q.chunk_index)
+                           for b in q.block_ids]
+                    raw = 2 * p.raw_bytes
+                    if self._prefer_native(raw):
+                        bits, epoch, probe = self._choose_bits(pending.layer_index, raw)
+                        payloads.append(LayerPayload(p.request, ids, raw, bits, bits, epoch, probe))
+                    else:
+                        q = LayerPayload(p.request, ids, raw, BITS_TORCHOP, BITS_TORCHOP)
+                        payloads.append(q)
+                        again.append(q)
+            pending.payloads[:] = payloads
+            if again:
+                passthrough += self._torchop_group(pending, again, torch)
+        if passthrough:
+            self._stage_passthrough(pending, passthrough, torch)
+
+    def _gather_raw(self, pending: PendingLayer, members: list, mode_byte: bool, torch):
+        """One device buffer of each member's words in block order (the K blocks,
+        then the V blocks), starting 256-byte aligned, behind a mode byte 6 when
+        ``mode_byte``; returns (buffer, offset of each member's first byte)."""
+        kv_layer = pending.kv_layer
+        batch = self._batch([p.block_ids for p in members], pending.block_words, kv_layer.device)
+        lead = 1 if mode_byte else 0
+        layout, end = [], 0
+        for p in members:
+            at = -(-(end + lead) // 256) * 256 - lead
+            layout.append(at)
+            end = at + lead + p.raw_bytes
+        buf = torch.empty(max(end, 1), dtype=torch.uint8, device=kv_layer.device)
+        first = 0
+        for p, at in zip(members, layout):
+            count = len(p.block_ids)
+            if mode_byte:
+                buf[at:at + 1].fill_(codec_format.MODE_RAW)
+            words = buf[at + lead:at + lead + p.raw_bytes].view(torch.bfloat16)
+            torch.index_select(kv_layer, 1, batch.ids[first:first + count],
+                               out=words.view((2, count) + tuple(kv_layer.shape[2:])))
+            first += count
+        return buf, layout
+
+    def _stage_passthrough(self, pending: PendingLayer, members: list, torch) -> None:
+        """Raw words sent with codec raw_passthrough (no mode byte), gathered on the
+        GPU and staged like the encoded payloads."""
+        stream = torch.cuda.current_stream(pending.kv_layer.device)
+        mark = self._gpu_mark(stream, torch)
+        buf, layout = self._gather_raw(pending, members, False, torch)
+        self._gpu_span(pending, "encode", mark, stream, torch)
+        group = self._stage(pending, buf, torch)
+        for p, at in zip(members, layout):
+            p.bits = BITS_PASSTHROUGH
+            p._group, p._offset, p.encoded_bytes = group, at, p.raw_bytes
 
     def _assign(self, pending, members, result, torch) -> None:
         out, offsets, sizes, _ = result
@@ -737,8 +861,8 @@ class SplitzipLayerCodec:
                     p.encoded_bytes = int(size)
             for p in overflowed:
                 p.bits, p.fallback, p._overflow = BITS_FIXED6, True, False
-        raws = [p for p in pending.payloads
-                if p.bits == BITS_RAW or p.view is None or p.view[0] == codec_format.MODE_OVERFLOW]
+        raws = [p for p in pending.payloads if p.bits != BITS_PASSTHROUGH and (
+            p.bits == BITS_RAW or p.view is None or p.view[0] == codec_format.MODE_OVERFLOW)]
         if raws:
             self._stage_raw(pending, raws, torch)
             for _ in raws:
@@ -767,24 +891,9 @@ class SplitzipLayerCodec:
         vllm_connector.py:4606-4625): the blocks are gathered on the GPU into one
         buffer behind each payload's mode byte and copied to the host like the
         others."""
-        kv_layer = pending.kv_layer
-        batch = self._batch([p.block_ids for p in raws], pending.block_words, kv_layer.device)
-        layout, end = [], 0
-        for p in raws:
-            at = -(-(end + 1) // 256) * 256 - 1       # the words start 256-byte aligned
-            layout.append(at)
-            end = at + 1 + p.raw_bytes
-        buf = torch.empty(end, dtype=torch.uint8, device=kv_layer.device)
-        stream = torch.cuda.current_stream(kv_layer.device)
+        stream = torch.cuda.current_stream(pending.kv_layer.device)
         mark = self._gpu_mark(stream, torch)
-        first = 0
-        for p, at in zip(raws, layout):
-            count = len(p.block_ids)
-            buf[at:at + 1].fill_(codec_format.MODE_RAW)
-            words = buf[at + 1:at + 1 + p.raw_bytes].view(torch.bfloat16)
-            torch.index_select(kv_layer, 1, batch.ids[first:first + count],
-                               out=words.view((2, count) + tuple(kv_layer.shape[2:])))
-            first += count
+        buf, layout = self._gather_raw(pending, raws, True, torch)
         self._gpu_span(pending, "encode", mark, stream, torch)
         host = self._stage_now(pending, buf, [(at, 1 + p.raw_bytes) for p, at in zip(raws, layout)],
                                torch)
@@ -884,10 +993,6 @@ class SplitzipLayerCodec:
                 ids = ids[f.chunk_index * half:(f.chunk_index + 1) * half]
                 meta = dict(meta, raw_bytes=f.raw_block_size * len(ids),
                             encoded_bytes=f.encoded_bytes)
-            if f.codec == "raw_passthrough":
-                # the native words themselves: restored as a mode-6 payload
-                payload = bytes([codec_format.MODE_RAW]) + bytes(payload)
-                meta = dict(meta, encoded_bytes=len(payload))
             requests.append((ids, payload, meta))
             keys.append(f.request_id)
         results = self.load_kv_layer_batch(layer, kv_layer, requests)
@@ -918,6 +1023,10 @@ class SplitzipLayerCodec:
         groups: dict[int, list] = {}
         for k, (block_ids, payload, metadata) in enumerate(requests):
             block_ids = [int(b) for b in block_ids]
+            if metadata.get("codec") == "raw_passthrough":
+                # the native words themselves: restored as a mode-6 payload
+                payload = bytes([codec_format.MODE_RAW]) + bytes(payload)
+                metadata = dict(metadata, encoded_bytes=len(payload))
             checked = self._validate(kv_layer, block_ids, payload, metadata, torch)
             if checked is None:
                 continue
