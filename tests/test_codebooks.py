@@ -95,3 +95,19 @@ def test_fit_rejects_bad_histograms():
         cb.fit_layer_codebook([1] * 10 + [0] * 246, [1] * 256)
     assert cb.fit_layer_codebook([1] * 256, [0] * 100 + [1] * 156) == \
         bytes(range(16)) + bytes(range(100, 116))
+
+
+def test_summary_matches_the_reference_trace_payload(golden_dir):
+    """tests/golden/trace_summary_cases.json holds the reference's own
+    summarize_symbol_counts (src/unchain_kv/trace.py:27-58) on 12 seeded
+    histograms (empty, ties, all 256 exponents, 16 M-word planes, huge counts):
+    every field equal, the entropy to the last bit."""
+    import json
+
+    cases = json.loads((golden_dir / "trace_summary_cases.json").read_text())["cases"]
+    assert len(cases) == 12
+    for case in cases:
+        ours = json.loads(json.dumps(cb.summarize_symbol_counts(case["histogram"]),
+                                     sort_keys=True))
+        assert ours == case["summary"], case["name"]
+        assert ours["entropy_bits"].hex() == case["summary"]["entropy_bits"].hex(), case["name"]

@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import hashlib
 import json
+import math
 from collections.abc import Iterable
 from pathlib import Path
 
@@ -64,11 +65,15 @@ def summarize_symbol_counts(counts: Iterable[int]) -> dict[str, object]:
     h = _histogram(counts)
     words = int(h.sum())
     ranked = rank_exponents(h)
+    # summed bin by bin in exponent order, in double precision, so that the trace
+    # field is the same float as the reference's (a pairwise numpy sum differs in
+    # the last bits)
+    entropy = 0.0
     if words:
-        p = h[h > 0] / words
-        entropy = float(-(p * np.log2(p)).sum())
-    else:
-        entropy = 0.0
+        for count in h.tolist():
+            if count > 0:
+                entropy += (count / words) * math.log2(count / words)
+        entropy = -entropy
     summary: dict[str, object] = {"words": words, "histogram": h.tolist(),
                                   "unique_exponents": int(ranked.size), "entropy_bits": entropy}
     for size in (8, 16):
