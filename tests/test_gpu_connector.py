@@ -712,3 +712,37 @@ def test_restore_returns_its_pinned_buffer_when_staging_raises(sz, codebooks, mo
     for t in tables:
         assert torch.equal(receiver[:, t].view(torch.int16), kv[:, t].view(torch.int16))
     codec.release(pending)
+
+
+def test_payload_ready_carries_gpu_times_on_the_gpu(sz, codebooks):
+    """UNCHAIN_KV_TRACE_CUDA=1 on the GPU (vllm_connector.py:473, 4634-4664): the
+    splitzip_payload_ready event of a Top-16 layer and of a small-request layer
+    (torch-op payloads, whose plan and encode are timed as the layer's encode)
+    carries positive GPU times from the recorded events, each payload's bits and
+    fallback flag, and the wall time since the save hook began."""
+    from unchainkv_amd.connector import BITS_TORCHOP
+
+    say("connector trace_cuda fields")
+    books = codebooks[2 * 32:3 * 32]
+    rng = np.random.default_rng(31)
+    pool = 48
+    # no escapes: the small requests' magnitudes then span few bits (sign/magnitude)
+    words = words_with_books(rng, books, pool, 0.0)
+    kv = layer_from_words(words, pool)
+    for config, tables, bits in (
+            (CodecConfig(top16=True, writeback=False, trace_cuda=True),
+             disjoint_tables(rng, pool, [16, 20]), [BITS_TOP16, BITS_TOP16]),
+            (CodecConfig(trace_cuda=True), disjoint_tables(rng, pool, [3, 5]),
+             [BITS_TORCHOP, BITS_TORCHOP])):
+        trace = RecordingTrace()
+        codec = SplitzipLayerCodec(config, trace=trace, codebooks={2: books})
+        pending = codec.save_kv_layer(2, kv, tables)
+        payloads = codec.ready(pending)
+        rows = [f for name, f in trace.rows if name == "splitzip_payload_ready"]
+        assert len(rows) == 1
+        row = rows[0]
+        assert row["bits"] == bits and row["fallback"] == [False, False]
+        assert row["encode_gpu_s"] > 0 and row["d2h_gpu_s"] > 0
+        assert row["payload_elapsed_s"] > 0
+        assert row["encoded_bytes"] == sum(p.encoded_bytes for p in payloads)
+        codec.release(pending)

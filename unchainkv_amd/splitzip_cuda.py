@@ -1047,11 +1047,9 @@ def plan_torchop_paged(kv_layer, batch: PagedBatch, plans=None):
                int(stream))
     if got < 0:
         _raise_last(lib, "splitzip torch-op plan failed")
-    if not got:
-        return None
-    # the workspace must outlive the queued kernels
-    workspace.record_stream(torch.cuda.current_stream(kv_layer.device))
-    return plans
+    # (the workspace goes back to torch's caching allocator on return: a later
+    # allocation reuses it only for work queued on this stream after the plan's)
+    return plans if got else None
 
 
 def read_torchop_plans(host_plans) -> list[tuple[int, int]]:
