@@ -116,3 +116,43 @@ def test_pinned_pool_keeps_idle_slots_when_a_request_exceeds_the_cap():
     c = pool.acquire(5 * GRANULE, torch)
     assert c is not None and c.capacity == 5 * GRANULE
     assert pool.committed_bytes <= 8 * GRANULE
+
+
+def test_streamed_copy_error_leaves_no_copy_running():
+    """When the range callback raises (as an upload may), copy_streamed re-raises
+    only after every copy job has finished or been cancelled: nothing writes into
+    the destination once the caller sees the error and returns it to a pool."""
+    import threading
+    import time
+
+    import pytest
+
+    rng = np.random.default_rng(8)
+    pieces, end = _pieces(rng, [4 << 20] * 12)
+    dst = np.zeros(end, np.uint8)
+    copier = HostCopier(threads=2)
+    running = []
+    lock = threading.Lock()
+    original = np.copyto
+
+    def slow_copy(out, src):
+        with lock:
+            running.append(1)
+        time.sleep(0.01)
+        original(out, src)
+        with lock:
+            running.pop()
+
+    def fail(lo, hi):
+        raise RuntimeError("upload failed")
+
+    np.copyto = slow_copy
+    try:
+        with pytest.raises(RuntimeError, match="upload failed"):
+            copier.copy_streamed(dst, pieces, fail, window=4 << 20)
+        assert not running
+        snapshot = dst.copy()
+        time.sleep(0.05)
+        assert np.array_equal(dst, snapshot)
+    finally:
+        np.copyto = original

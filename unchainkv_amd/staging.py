@@ -168,15 +168,25 @@ class HostCopier:
             at, arr = job
             np.copyto(dst[at:at + arr.size], arr)
 
+        from concurrent.futures import wait
+
         pool = self._executor()
         futures = [pool.submit(run, job) for job in jobs]
         issued = 0
-        for (at, arr), fut in zip(jobs, futures):
-            fut.result()  # in order: every earlier job has finished too
-            done = at + arr.size
-            if on_ready is not None and done - issued >= window:
-                on_ready(issued, done)
-                issued = done
-        if on_ready is not None and end > issued:
-            on_ready(issued, end)
+        try:
+            for (at, arr), fut in zip(jobs, futures):
+                fut.result()  # in order: every earlier job has finished too
+                done = at + arr.size
+                if on_ready is not None and done - issued >= window:
+                    on_ready(issued, done)
+                    issued = done
+            if on_ready is not None and end > issued:
+                on_ready(issued, end)
+        except BaseException:
+            # no copy may still write into dst once the caller sees the error (it
+            # may hand dst back to a pool): cancel the queued jobs, wait for the rest
+            for fut in futures:
+                fut.cancel()
+            wait(futures)
+            raise
 
