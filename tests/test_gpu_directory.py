@@ -211,3 +211,28 @@ def test_directory_declines_without_the_tile_layout(sz, codebooks):
     torch.cuda.synchronize()
     assert torch.equal(target[:, :3].view(torch.int16), kv[:, :3].view(torch.int16))
     assert bool((target[:, 3] == 1.0).all())
+
+
+def test_unsuitable_workspaces_are_declined(sz, codebooks):
+    """A workspace that is not a contiguous uint8 buffer on the layer's device is
+    declined by the encoders; the attention and histogram wrappers allocate their
+    own in its place."""
+    say("unsuitable workspaces")
+    books = codebooks[:32]
+    batch = sz.PagedBatch([[0, 1], [2]], 2048, "cuda")
+    # no escapes: at most 64 distinct high bytes, so fixed6 takes the words too
+    words = random_words(np.random.default_rng(9), 2 * 4 * 2048, books, 0.0)
+    kv = bf16(words).view(2, 4, 2048)
+    out = batch.new_payload_buffer()
+    ws = batch.new_workspace()
+    for bad in (ws.view(torch.int32), ws[::2], ws.cpu()):
+        assert sz.encode_top16_paged(kv, batch, out, bad, codebooks=books) is None
+    six = batch.new_palette_buffer(6)
+    pws = batch.new_palette_workspace()
+    assert sz.encode_bf16_paged(kv, batch, six, pws.cpu(), bits=6) is None
+    assert sz.encode_top16_paged(kv, batch, out, ws, codebooks=books) == batch.total_encoded_bytes
+    assert sz.encode_bf16_paged(kv, batch, six, pws, bits=6) is not None
+    counts = sz.exponent_histogram_paged(kv, batch, workspace=torch.zeros(8, dtype=torch.int32,
+                                                                          device="cuda"))
+    torch.cuda.synchronize()
+    assert counts is not None and int(counts.sum()) == 2 * 3 * 2048

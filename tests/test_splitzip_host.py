@@ -421,3 +421,10 @@ def test_contiguous_run_and_runs():
     assert splitzip_cuda.contiguous_run([]) is None
     assert _contiguous_runs([]) == ()
     assert _contiguous_runs([3, 4, 5, 9, 10, 2]) == ((3, 3), (9, 2), (2, 1))
+
+
+def test_encoders_reject_a_missing_workspace():
+    with pytest.raises(ValueError, match="workspace"):
+        splitzip_cuda.encode_top16_paged(None, None, None, None)
+    with pytest.raises(ValueError, match="workspace"):
+        splitzip_cuda.encode_bf16_paged(None, None, None, None, bits=6)

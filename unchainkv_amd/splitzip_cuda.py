@@ -678,6 +678,12 @@ def _payloads_fit(source, src_offsets, encoded_bytes, batch: PagedBatch) -> bool
     return all(o + e <= size for o, e in zip(src_offsets, encoded_bytes))
 
 
+def _byte_buffer_ok(buf, device, nbytes: int, torch) -> bool:
+    """A contiguous uint8 tensor on ``device`` holding at least ``nbytes`` bytes."""
+    return buf is not None and buf.dtype == torch.uint8 and buf.is_contiguous() and \
+        buf.device == device and buf.numel() >= nbytes
+
+
 def _directory_ptr(directory, batch: PagedBatch, torch) -> int | None:
     """Device address of an escape directory (0 for none); None when unusable."""
     if directory is None:
@@ -706,6 +712,8 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
     encoded bytes or ``None`` when the codec declines."""
     if palette_info is not None and presence is None:
         raise ValueError("palette_info needs presence")
+    if workspace is None:
+        raise ValueError("encode_top16_paged needs a workspace (batch.workspace())")
     lib = _load()
     name = "kvq_splitzip_bf16_encode_top16_paged" + (
         "_probe" if palette_info is not None else "_presence" if presence is not None else "")
@@ -722,6 +730,8 @@ def encode_top16_paged(kv_layer, batch: PagedBatch, out, workspace, layer_index:
         tables = _resolve_tables(layer_index, codebooks, kv_layer.device, torch)
     dir_ptr = _directory_ptr(directory, batch, torch)
     if tables is None or dir_ptr is None:
+        return None
+    if not _byte_buffer_ok(workspace, kv_layer.device, 1, torch):
         return None
     extra = ()
     if presence is not None:
@@ -880,6 +890,9 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
         raise ValueError("palette_info and info_first go together")
     if palette_info is not None:
         return _encode_bf16_paged_info(kv_layer, batch, out, bits, palette_info, info_first)
+    if workspace is None:
+        raise ValueError("encode_bf16_paged needs a workspace (batch.new_palette_workspace()) "
+                         "unless palette_info is given")
     lib = _load()
     name = "kvq_splitzip_bf16_encode_mode_paged" + ("_presence" if presence is not None else "")
     encode = getattr(lib, name, None) if lib else None
@@ -890,6 +903,8 @@ def encode_bf16_paged(kv_layer, batch: PagedBatch, out, workspace, bits: int = 6
     if not _paged_layout_ok(kv_layer, batch, torch):
         return None
     if out.dtype != torch.uint8 or not out.is_contiguous() or out.device != kv_layer.device:
+        return None
+    if not _byte_buffer_ok(workspace, kv_layer.device, 1, torch):
         return None
     batch.palette_layout(bits)
     offs = batch._palette[bits][3]
@@ -1146,9 +1161,12 @@ def decode_attention_top16(q, payloads, payload_offsets, context_tokens, kv_head
         scale = head_dim ** -0.5
     if out is None:
         out = torch.empty_like(q)
+    elif out.dtype != torch.bfloat16 or not out.is_contiguous() or out.shape != q.shape or \
+            out.device != q.device:
+        return None
     max_ctx = max(int(c) for c in context_tokens)
     need = int(lib.kvq_splitzip_top16_decode_attention_workspace_bytes(batch, kv_heads, max_ctx))
-    if workspace is None or workspace.numel() < need:
+    if not _byte_buffer_ok(workspace, q.device, need, torch):
         workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=q.device)
     offs = (ctypes.c_ulonglong * batch)(*map(int, payload_offsets))
     ctxs = (ctypes.c_ulonglong * batch)(*map(int, context_tokens))
@@ -1239,7 +1257,7 @@ def exponent_histogram_paged(kv_layer, batch: PagedBatch, *, workspace=None, cou
         return None
     count = len(batch.ids)
     need = int(lib.kvq_splitzip_exponent_histogram_workspace_bytes(count, batch.block_words))
-    if workspace is None or workspace.numel() < need:
+    if not _byte_buffer_ok(workspace, kv_layer.device, need, torch):
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=kv_layer.device)
     if counts is None:
         counts = torch.empty((2, 256), dtype=torch.int64, device=kv_layer.device)
