@@ -383,6 +383,79 @@ def test_writeback_skips_a_layer_that_is_not_contiguous():
     assert trace.rows == [("codec_writeback_skip", {"layer": 7, "reason": "layout"})]
 
 
+def test_deferred_writebacks_finish_only_settled_payloads_of_their_layer():
+    """Early-stage writebacks (vllm_connector.py:3565-3718): at the layer's next
+    finish, payloads whose layer is not ready yet, that overflowed, or whose blocks
+    are fragmented are skipped; the rest of one encode group go to one writeback
+    launch; entries of other layers and transfer ids stay until their own finish or
+    a cancel."""
+    from types import SimpleNamespace
+
+    from unchainkv_amd.connector import LayerPayload, PendingLayer
+
+    calls = []
+
+    class FakeLib:
+        @staticmethod
+        def available():
+            return True
+
+        @staticmethod
+        def writeback_top16_paged(out, batch, kv_layer, members):
+            calls.append((out, batch, kv_layer, list(members)))
+            return 700, None
+
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace,
+                               lib=FakeLib())
+    layer = SimpleNamespace(is_contiguous=lambda: True)
+
+    def payload(r, ids, bits=BITS_TOP16):
+        return LayerPayload(r, ids, 2 * MIB, bits, BITS_TOP16, encoded_bytes=300)
+
+    a, b, c, d = payload(0, [4, 5]), payload(1, [7, 9]), payload(2, [11, 12]), payload(3, [20])
+    c.bits, c.fallback = BITS_FIXED6, True          # overflowed -> fixed6 in ready()
+    settled = PendingLayer(3, layer, 16384, [a, b, c, d], ready_done=True)
+    result = ("codec buffer", [0, 300, 600, 900], [300] * 4, "batch")
+    e = payload(0, [30, 31])
+    unsettled = PendingLayer(4, layer, 16384, [e])
+    f = payload(5, [40])
+    other = PendingLayer(3, layer, 16384, [f], ready_done=True)
+    for p in (a, b, c, d, e, f):
+        p.deferred_writeback = True
+    codec._deferred_codec_writebacks.update({
+        ("t0", 3): (settled, a, result, 0), ("t1", 3): (settled, b, result, 1),
+        ("t2", 3): (settled, c, result, 2), ("t3", 3): (settled, d, result, 3),
+        ("t0", 4): (unsettled, e, ("buf", [0], [300], "b4"), 0),
+        ("t5", 3): (other, f, ("buf5", [0], [300], "b5"), 0)})
+
+    assert codec.finish_deferred_writebacks(3, layer, ["t0", "t1", "t2", "t3"]) == 700
+    assert calls == [("codec buffer", "batch", layer, [0, 3])]
+    assert not any(p.deferred_writeback for p in (a, b, c, d))
+    assert trace.rows == [
+        ("codec_writeback_skip", {"layer": 3, "reason": "overflow", "source": "early"}),
+        ("codec_writeback_skip", {"layer": 3, "reason": "fragmented", "segments": 4,
+                                  "source": "early"}),
+        ("codec_writeback_submitted", {"layer": 3, "bytes": 300, "raw_bytes": 2 * MIB,
+                                       "segments": 2, "source": "early"}),
+        ("codec_writeback_submitted", {"layer": 3, "bytes": 300, "raw_bytes": 2 * MIB,
+                                       "segments": 2, "source": "early"})]
+    assert set(codec._deferred_codec_writebacks) == {("t0", 4), ("t5", 3)}
+    trace.rows.clear()
+    calls.clear()
+    # a layer whose ready() has not returned: skipped and dropped, nothing launched
+    assert codec.finish_deferred_writebacks(4, layer) == 0
+    assert calls == [] and not e.deferred_writeback
+    assert trace.rows == [("codec_writeback_skip", {"layer": 4, "reason": "d2h_pending",
+                                                     "source": "early"})]
+    trace.rows.clear()
+    assert codec.cancel_deferred_writebacks(transfer_ids=["t9"]) == 0
+    assert codec.cancel_deferred_writebacks(layer_index=3, reason="metadata_clear") == 1
+    assert codec._deferred_codec_writebacks == {} and not f.deferred_writeback
+    assert trace.rows == [("codec_writeback_skip", {"layer": 3, "reason": "metadata_clear",
+                                                     "source": "early"})]
+
+
 def test_two_chunk_rule_and_kvc2_frames():
     """UNCHAIN_KV_SPLITZIP_CHUNKS=2 (vllm_connector.py:446-447, 2718-2737): only
     with neither Top-16 nor fixed5 enabled, and only for an even number of blocks

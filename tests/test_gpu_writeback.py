@@ -233,3 +233,75 @@ def test_connector_writeback_roundtrip(sz, codebooks):
     got = target.view(torch.int16).cpu().numpy().view(np.uint16).reshape(2, pool, bw)
     for t, rt in zip(tables, recv):
         assert np.array_equal(got[:, rt], original[:, t])
+
+
+def test_connector_deferred_writeback_of_early_saves(sz, codebooks):
+    """Early-stage saves (vllm_connector.py:2148-2165, 3565-3688): no block is
+    overwritten during the early save and its ready; the payloads come from the
+    codec buffer, byte-exact. At the layer's next save hook outside the early stage,
+    finish_deferred_writebacks with the step's active transfer ids moves the settled
+    payloads into their blocks (K run, then V run); the fragmented request and the
+    overflowed one keep their blocks; the new save's own request is encoded from
+    its untouched blocks."""
+    say("connector deferred writeback")
+    books = codebooks[5 * 32:6 * 32]
+    bw, pool = 16384, 112
+    rng = np.random.default_rng(15)
+    words = books_words(rng, books, 2 * pool * bw, 0.0005).reshape(2, pool, bw)
+    tables = [list(range(4, 20)), list(range(30, 48)), [50, 52] + list(range(53, 67)),
+              list(range(70, 86))]
+    hot = 3
+    blk = books_words(rng, books, 2 * 16 * bw, 0.0)
+    outside = np.array(sorted(set(range(256)) - set(books))[:16], np.uint16)
+    hit = rng.random(blk.size) < 0.012
+    blk[hit] = (blk[hit] & 0x807F) | (outside[rng.integers(0, 16, int(hit.sum()))] << 7)
+    words[:, tables[hot]] = blk.reshape(2, 16, bw)
+    # the next step's request: no escapes, so fixed6 (at most 64 high bytes) takes it
+    words[:, 90:106] = books_words(rng, books, 2 * 16 * bw, 0.0).reshape(2, 16, bw)
+    original = words.copy()
+    kv = torch.from_numpy(words.reshape(-1).view(np.int16).copy()).cuda().view(
+        torch.bfloat16).view(2, pool, 16, 8, 128)
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace)
+    ids = ["req-a", "req-b", "req-c", "req-d"]
+    pending = codec.save_kv_layer(5, kv, tables, transfer_ids=ids, early=True)
+    payloads = codec.ready(pending)
+    assert [p.bits for p in payloads] == [BITS_TOP16, BITS_TOP16, BITS_TOP16, BITS_FIXED6]
+    assert not any(p.writeback for p in payloads)
+    tab = oracle.top16_tables(books)
+    for r in range(3):
+        ref = oracle.top16_encode(original[:, tables[r]].reshape(-1), tab)
+        assert bytes(payloads[r].view) == bytes(ref)
+    assert bytes(payloads[hot].view) == bytes(oracle.fixed6_encode(
+        original[:, tables[hot]].reshape(-1)))
+    base = original.reshape(-1).view(np.uint8)
+    torch.cuda.synchronize()
+    assert np.array_equal(layer_bytes(kv), base)
+    assert "codec_writeback_submitted" not in trace.names()
+    sent = [bytes(p.view) for p in payloads]
+    codec.release(pending)
+    # the layer's next save hook outside the early stage: the deferred writebacks of
+    # the step's active transfers, then the save of a new request
+    assert codec.finish_deferred_writebacks(5, kv, ["req-x"]) == 0
+    assert len(codec._deferred_codec_writebacks) == 4   # every Top-16 attempt
+    moved = codec.finish_deferred_writebacks(5, kv, ids + ["req-e"])
+    assert moved == len(sent[0]) + len(sent[1])
+    later = [list(range(90, 106))]
+    out = codec.ready(codec.save_kv_layer(5, kv, later, transfer_ids=["req-e"]))
+    # request d's overflow opened a backoff window on the layer: this save is fixed6
+    assert out[0].bits == BITS_FIXED6
+    same = bytes(out[0].view) == bytes(oracle.fixed6_encode(original[:, later[0]].reshape(-1)))
+    assert same
+    torch.cuda.synchronize()
+    exp = expected_after(base, [np.frombuffer(sent[r], np.uint8) for r in (0,)],
+                         [(tables[0][0], len(tables[0]))], lambda c: 2 * c * bw, 2 * pool * bw,
+                         2 * bw)
+    # request b's table [30..48) is one run as well
+    exp = expected_after(exp, [np.frombuffer(sent[1], np.uint8)], [(30, 18)],
+                         lambda c: 2 * c * bw, 2 * pool * bw, 2 * bw)
+    assert np.array_equal(layer_bytes(kv), exp)
+    early = [(n, f) for n, f in trace.rows if f.get("source") == "early"]
+    assert [n for n, _ in early].count("codec_writeback_submitted") == 2
+    assert [f["reason"] for n, f in early if n == "codec_writeback_skip"] == \
+        ["overflow", "fragmented"]
+    assert codec._deferred_codec_writebacks == {}

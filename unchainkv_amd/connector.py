@@ -18,7 +18,8 @@ This module keeps that codec behaviour and its knobs, batched per layer:
   :3460-3563): a Top-16 payload whose request holds one contiguous run of blocks is
   moved into those blocks (K-plane run, then V-plane run) by one launch per layer
   and copied to the host from there, so the codec buffer is released at once;
-  requests with fragmented block tables are skipped, as in the reference;
+  requests with fragmented block tables are skipped, as in the reference; in the
+  early stage the move is deferred until ``finish_deferred_writebacks`` (:3565-3718);
 * ready (``ready``): after the copy, Top-16 (and fixed5) payloads whose byte 0 is
   255 are re-encoded as fixed6, and fixed6 overflow falls back to raw mode 6
   (``[6] + raw bytes``) (:4526-4665);
@@ -142,6 +143,7 @@ class LayerPayload:
     view: memoryview | None = None
     writeback: bool = False          # moved into its own blocks before the host copy
     writeback_segments: int = 0
+    deferred_writeback: bool = False  # early stage: moved into its blocks at a later save
     _group: int = -1
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
@@ -179,6 +181,7 @@ class PendingLayer:
     deferred: list = field(default_factory=list)
     timing: list = field(default_factory=list)  # ("encode" | "d2h", start, end) GPU events
     d2h_bytes: int = 0       # bytes queued for the host so far (the layer's PCIe traffic)
+    ready_done: bool = False  # ready() has returned: copies complete, overflows settled
 
 
 class SplitzipLayerCodec:
@@ -207,6 +210,9 @@ class SplitzipLayerCodec:
         # batches by block tables: a request keeps its block ids in every layer, so
         # a step's layers share them (built once, ids uploaded once)
         self._batches: dict = {}
+        # early-stage Top-16 payloads whose writeback waits for a later save of their
+        # layer: (transfer id, layer) -> (pending layer, payload, encode result, index)
+        self._deferred_codec_writebacks: dict = {}
 
     # ------------------------------------------------------------------
     # library
@@ -491,12 +497,13 @@ class SplitzipLayerCodec:
         pending.slots.clear()
 
     def _writeback_members(self, members: list, layer_index: int,
-                           payloads: list | None = None) -> list[int]:
+                           payloads: list | None = None, **source) -> list[int]:
         """Indices of the Top-16 members whose blocks are one contiguous run (the
         reference skips fragmented tables, vllm_connector.py:3479-3488) and are not
         blocks of another request of the layer (``payloads``): a block shared with
         another request, as prefix caching shares them, would reach that request's
-        fallback re-encode or raw copy holding payload bytes."""
+        fallback re-encode or raw copy holding payload bytes. ``source`` is added to
+        the skip events (``source="early"`` for deferred writebacks)."""
         owners: dict[int, int] = {}
         for p in payloads if payloads is not None else members:
             for b in p.block_ids:
@@ -506,10 +513,11 @@ class SplitzipLayerCodec:
             runs = _contiguous_runs(p.block_ids)
             if len(runs) != 1:
                 self.trace.event("codec_writeback_skip", layer=layer_index, reason="fragmented",
-                                 segments=len(runs) * 2)
+                                 segments=len(runs) * 2, **source)
                 continue
             if any(owners[b] > 1 for b in p.block_ids):
-                self.trace.event("codec_writeback_skip", layer=layer_index, reason="shared")
+                self.trace.event("codec_writeback_skip", layer=layer_index, reason="shared",
+                                 **source)
                 continue
             if not 0 < p.encoded_bytes < p.raw_bytes:
                 continue
@@ -585,14 +593,28 @@ class SplitzipLayerCodec:
             p._group, p._offset, p.encoded_bytes = group, int(off), int(size)
         return True
 
-    def save_kv_layer(self, layer_index: int, kv_layer, block_tables) -> PendingLayer:
+    def save_kv_layer(self, layer_index: int, kv_layer, block_tables, *, transfer_ids=None,
+                      early: bool = False) -> PendingLayer:
         """Encode every request's blocks of one layer (the save hook's codec step) and
-        start the copies to host. ``ready`` returns the payloads."""
+        start the copies to host. ``ready`` returns the payloads.
+
+        ``transfer_ids``: one id per block table (default: the request's index),
+        which keys the deferred writebacks. ``early``: a save of the early stage,
+        while the forward pass may still read the blocks (vllm_connector.py:2148-2165):
+        with writeback overwrite, no Top-16 payload is moved into its blocks now; it
+        is copied to the host from the codec buffer, and its writeback waits for
+        ``finish_deferred_writebacks``, which the save hook calls outside the early
+        stage with the step's active transfer ids before it saves
+        (vllm_connector.py:2065-2080)."""
         import time
 
         import torch
 
         started = time.perf_counter()
+        if transfer_ids is None:
+            transfer_ids = list(range(len(block_tables)))
+        elif len(transfer_ids) != len(block_tables):
+            raise ValueError("one transfer id per block table")
         block_words = self._layer_geometry(kv_layer, torch)
         payloads = []
         for r, ids in enumerate(block_tables):
@@ -674,12 +696,104 @@ class SplitzipLayerCodec:
                 # a probe of a layer that overflowed before: its payloads cross PCIe
                 # only once their mode bytes show that they fit
                 self._defer_top16(pending, top, top_result, torch)
-            elif not (self.codec_writeback_overwrite
+            elif not (self.codec_writeback_overwrite and not early
                       and self._stage_writeback(pending, top, top_result, torch)):
                 self._assign(pending, top, top_result, torch)
+            if early and self.codec_writeback_overwrite:
+                for i, p in enumerate(top):
+                    if 0 < p.encoded_bytes < p.raw_bytes:
+                        p.deferred_writeback = True
+                        self._deferred_codec_writebacks[(transfer_ids[p.request], layer_index)] \
+                            = (pending, p, top_result, i)
         self.trace.event("codec_encode_submitted", layer=layer_index, requests=len(payloads),
                          raw_bytes=sum(p.raw_bytes for p in payloads))
         return pending
+
+    # ------------------------------------------------------------------
+    # deferred (early-stage) codec writeback (vllm_connector.py:3565-3718)
+
+    def finish_deferred_writebacks(self, layer_index: int, kv_layer, transfer_ids=None) -> int:
+        """Moves the deferred Top-16 payloads of ``layer_index`` (of ``transfer_ids``,
+        the step's active requests; all of the layer's when None) into their blocks
+        of ``kv_layer``, as the reference does at the layer's next save outside the
+        early stage (vllm_connector.py:3565-3688): one writeback launch per encode
+        group on the current stream, K-plane run first, then the V-plane run. The
+        blocks then hold the payloads, so they must not be read as KV again; the
+        entries of a request that has finished (its blocks may be reused) are
+        dropped with ``cancel_deferred_writebacks`` first. A payload is
+        skipped when its layer's ``ready`` has not returned (``d2h_pending``), when
+        it overflowed and went to the fallback (``overflow``), when its blocks are
+        not one contiguous run (``fragmented``) or are shared with another request
+        (``shared``), when the layer is not contiguous (``layout``) or when a run
+        overlaps the codec buffer (``alias``). Every entry of the layer and ids is
+        dropped, and with it the hold on its codec buffer. Returns the bytes
+        moved."""
+        if not self._deferred_codec_writebacks:
+            return 0
+        wanted = None if transfer_ids is None else set(transfer_ids)
+        keys = [k for k in self._deferred_codec_writebacks
+                if k[1] == layer_index and (wanted is None or k[0] in wanted)]
+        groups: dict = {}
+        for key in keys:
+            pending, p, result, i = self._deferred_codec_writebacks.pop(key)
+            p.deferred_writeback = False
+            if not pending.ready_done:
+                self.trace.event("codec_writeback_skip", layer=layer_index, reason="d2h_pending",
+                                 source="early")
+            elif p.bits != BITS_TOP16:
+                self.trace.event("codec_writeback_skip", layer=layer_index, reason="overflow",
+                                 source="early")
+            else:
+                groups.setdefault(id(result), (pending, result, []))[2].append((i, p))
+        moved_total = 0
+        for pending, result, entries in groups.values():
+            out, _, _, batch = result
+            members = [p for _, p in entries]
+            picks = self._writeback_members(members, layer_index, pending.payloads,
+                                            source="early")
+            if not picks:
+                continue
+            if not kv_layer.is_contiguous():
+                for _ in picks:
+                    self.trace.event("codec_writeback_skip", layer=layer_index, reason="layout",
+                                     source="early")
+                continue
+            try:
+                moved, _ = self._lib().writeback_top16_paged(
+                    out, batch, kv_layer, [entries[j][0] for j in picks])
+            except Exception as exc:  # the reference traces the error and goes on
+                self.trace.event("codec_writeback_error", layer=layer_index,
+                                 error=str(exc)[:160], source="early")
+                continue
+            if not moved:
+                for _ in picks:
+                    self.trace.event("codec_writeback_skip", layer=layer_index, reason="alias",
+                                     source="early")
+                continue
+            moved_total += moved
+            for j in picks:
+                p = members[j]
+                self.trace.event("codec_writeback_submitted", layer=layer_index,
+                                 bytes=p.encoded_bytes, raw_bytes=p.raw_bytes, segments=2,
+                                 source="early")
+        return moved_total
+
+    def cancel_deferred_writebacks(self, transfer_ids=None, layer_index: int | None = None,
+                                   reason: str = "cancelled") -> int:
+        """Drops deferred writebacks (of ``transfer_ids`` and ``layer_index`` when
+        given) without moving anything, as the reference does when a request
+        finishes or its metadata is cleared (vllm_connector.py:3690-3718); returns
+        how many were dropped."""
+        wanted = None if transfer_ids is None else set(transfer_ids)
+        keys = [k for k in self._deferred_codec_writebacks
+                if (wanted is None or k[0] in wanted)
+                and (layer_index is None or k[1] == layer_index)]
+        for key in keys:
+            _, p, _, _ = self._deferred_codec_writebacks.pop(key)
+            p.deferred_writeback = False
+            self.trace.event("codec_writeback_skip", layer=key[1], reason=reason,
+                             source="early")
+        return len(keys)
 
     # ------------------------------------------------------------------
     # torch-op formats (vllm_connector.py:3204-3343) and raw passthrough
@@ -881,6 +995,7 @@ class SplitzipLayerCodec:
                 "payload_elapsed_s": time.perf_counter() - pending.started,
             }
         pending.timing.clear()
+        pending.ready_done = True
         self.trace.event("splitzip_payload_ready", layer=layer,
                          raw_bytes=sum(p.raw_bytes for p in pending.payloads),
                          encoded_bytes=sum(p.encoded_bytes for p in pending.payloads), **fields)
