@@ -195,12 +195,15 @@ def test_config_from_environment():
         "UNCHAIN_KV_SPLITZIP_FIXED5": "1",
         "UNCHAIN_KV_SPLITZIP_FIXED5_LAYERS": "1, 3,5",
         "UNCHAIN_KV_SPLITZIP_TOP16_MAX_COOLDOWN": "0",
+        "UNCHAIN_KV_CODEC_MIN_BLOCKS": "64",
     })
-    assert cfg.top16 and cfg.fixed5
+    assert cfg.top16 and cfg.fixed5 and cfg.min_blocks == 64
     assert cfg.fixed5_layers == {1, 3, 5}
     assert cfg.top16_max_cooldown == 1  # clamped to at least 1, as the reference does
     default = CodecConfig.from_env({})
     assert not default.top16 and default.top16_max_cooldown == 32 and not default.fixed5_layers
+    assert default.min_blocks == 0
+    assert CodecConfig.from_env({"UNCHAIN_KV_CODEC_MIN_BLOCKS": "-3"}).min_blocks == 0
     # codec writeback defaults to on with Top-16 (vllm_connector.py:406-412)
     assert cfg.writeback and not default.writeback
     assert not CodecConfig.from_env({"UNCHAIN_KV_SPLITZIP_TOP16": "1",

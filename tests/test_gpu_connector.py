@@ -397,6 +397,14 @@ def test_small_requests_take_the_torchop_formats(sz, codebooks):
             assert np.array_equal(dst[:, recv[name]], host[:, t]), name
     assert [got[name] for name in names] == [(len(t), 4 * BW * len(t)) for t in tables]
     assert results == [(len(t), 4 * BW * len(t)) for t in tables]
+    # UNCHAIN_KV_CODEC_MIN_BLOCKS=3: the requests of fewer blocks get no payload
+    # (vllm_connector.py:5315-5321); the others are the same payloads
+    short = SplitzipLayerCodec(CodecConfig(min_blocks=3), trace=RecordingTrace())
+    pending = short.save_kv_layer(2, kv, tables)
+    kept = short.ready(pending)
+    assert [p.request for p in kept] == [1, 4]
+    assert [bytes(p.view) for p in kept] == [bytes(payloads[1].view), bytes(payloads[4].view)]
+    short.release(pending)
 
 
 # ---------------------------------------------------------------------------

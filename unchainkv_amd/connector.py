@@ -87,6 +87,9 @@ class CodecConfig:
     # GPU event timing of each layer's encodes and copies in the
     # splitzip_payload_ready trace event (vllm_connector.py:473, 4634-4664)
     trace_cuda: bool = False              # UNCHAIN_KV_TRACE_CUDA
+    # requests of fewer blocks bypass the codec: no payload is made for them and the
+    # transport sends their blocks as they are (vllm_connector.py:385, 5315-5321)
+    min_blocks: int = 0                   # UNCHAIN_KV_CODEC_MIN_BLOCKS
 
     @classmethod
     def from_env(cls, env=None) -> "CodecConfig":
@@ -103,6 +106,7 @@ class CodecConfig:
             host_mirror_bytes=max(0, _env_int(env, "UNCHAIN_KV_HOST_MIRROR_BYTES", 0)),
             chunks=2 if _env_int(env, "UNCHAIN_KV_SPLITZIP_CHUNKS", 1) == 2 else 1,
             trace_cuda=_env_int(env, "UNCHAIN_KV_TRACE_CUDA", 0) > 0,
+            min_blocks=max(0, _env_int(env, "UNCHAIN_KV_CODEC_MIN_BLOCKS", 0)),
         )
 
 
@@ -596,7 +600,9 @@ class SplitzipLayerCodec:
     def save_kv_layer(self, layer_index: int, kv_layer, block_tables, *, transfer_ids=None,
                       early: bool = False) -> PendingLayer:
         """Encode every request's blocks of one layer (the save hook's codec step) and
-        start the copies to host. ``ready`` returns the payloads.
+        start the copies to host. ``ready`` returns the payloads. A request with
+        fewer than ``CodecConfig.min_blocks`` blocks bypasses the codec and has no
+        payload (``LayerPayload.request`` names the request of each payload).
 
         ``transfer_ids``: one id per block table (default: the request's index),
         which keys the deferred writebacks. ``early``: a save of the early stage,
@@ -621,6 +627,8 @@ class SplitzipLayerCodec:
             ids = [int(b) for b in ids]
             if not ids:
                 raise ValueError("every request needs at least one block")
+            if len(ids) < self.config.min_blocks:
+                continue  # _use_compressed_native_codec is false for it
             raw = 2 * len(ids) * block_words * 2
             if self._two_chunks(ids):
                 # each half of the blocks is its own payload and frame (fixed6, or a
