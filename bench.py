@@ -537,6 +537,142 @@ def time_writeback(torch, sz, w, reps: int = 10):
             "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "layout": layout}
 
 
+def time_torchop_sender(torch, sz, w, reps: int = 5, cpu_seconds: float = 3.0):
+    """The torch-op sender of requests below 1 MiB (what the reference connector
+    sends without Top-16 native decode: sign/magnitude, else the high-byte palette,
+    else the nibble planes, else raw words): the workload's sender blocks cut into
+    requests of the most whole blocks below 1 MiB, on the first layers. Per layer
+    call: the plan (presence + plan kernels), the encode, and the decode + scatter
+    into the receiver's blocks, each timed with HIP events over back-to-back calls;
+    the host-inclusive sender (plan, host read of the plans, encode) timed by the
+    wall clock. Layer 0's round trip is checked word for word. ``cpu_baseline``: the
+    oracle's numpy restatement of the reference's torch-op encode on a sample of
+    the same requests."""
+    import numpy as np
+
+    send, recv = w["send"], w["recv"]
+    bw, device = send.block_words, w["device"]
+    per = ((1 << 20) - 1) // (4 * bw)   # whole blocks of K and V below 1 MiB
+    if per == 0:
+        return None
+    flat_s = [b for t in send.block_tables for b in t]
+    flat_r = [b for t in recv.block_tables for b in t]
+    count = len(flat_s) // per
+    if count == 0:
+        return None
+    tables = [flat_s[i * per:(i + 1) * per] for i in range(count)]
+    batch = sz.PagedBatch(tables, bw, device)
+    rbatch = sz.PagedBatch([flat_r[i * per:(i + 1) * per] for i in range(count)], bw, device)
+    layers = min(w["layers"], 8)
+    plans, fields, outs, offsets, sizes = [], [], [], [], []
+    for layer in range(layers):
+        plan = sz.plan_torchop_paged(w["kv"][layer], batch)
+        got = sz.read_torchop_plans(plan.cpu().numpy())
+        size = [s for _, s in got]
+        offs = np.concatenate([[0], np.cumsum(size)[:-1]]).astype(np.int64).tolist()
+        out = torch.empty(max(1, sum(size)), dtype=torch.uint8, device=device)
+        if sz.encode_torchop_paged(w["kv"][layer], batch, plan, out, offs, size) != sum(size):
+            raise RuntimeError("torch-op encode failed")
+        plans.append(plan)
+        fields.append(got)
+        outs.append(out)
+        offsets.append(offs)
+        sizes.append(size)
+    if any(s == 0 for size in sizes for s in size):
+        return {"requests": count, "note": "a request no torch-op format compresses (raw "
+                                          "passthrough): not timed"}
+    raw = batch.total_raw_bytes
+    target = w["receiver"][0]
+    if sz.decode_torchop_paged(outs[0], offsets[0], sizes[0], target, rbatch) != raw:
+        raise RuntimeError("torch-op decode failed")
+    ids_s = torch.tensor(flat_s[:count * per], dtype=torch.int64, device=device)
+    ids_r = torch.tensor(flat_r[:count * per], dtype=torch.int64, device=device)
+    if not torch.equal(target.index_select(1, ids_r).view(torch.int16),
+                       w["kv"][0].index_select(1, ids_s).view(torch.int16)):
+        raise RuntimeError("torch-op round trip differs from the sender's words")
+    stream = torch.cuda.current_stream(device)
+
+    def timed(call):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # the wrappers' host work per call exceeds the GPU's: a longer hold keeps
+        # every queued call back to back
+        hold_queue(torch, 30.0)
+        e0.record(stream)
+        for _ in range(reps):
+            for layer in range(layers):
+                call(layer)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * layers)
+
+    plan_ms = timed(lambda l: sz.plan_torchop_paged(w["kv"][l], batch, plans=plans[l]))
+    enc_ms = timed(lambda l: sz.encode_torchop_paged(w["kv"][l], batch, plans[l], outs[l],
+                                                     offsets[l], sizes[l]))
+    dec_ms = timed(lambda l: sz.decode_torchop_paged(outs[l], offsets[l], sizes[l],
+                                                     w["receiver"][l], rbatch))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for layer in range(layers):
+            plan = sz.plan_torchop_paged(w["kv"][layer], batch, plans=plans[layer])
+            size = [s for _, s in sz.read_torchop_plans(plan.cpu().numpy())]
+            sz.encode_torchop_paged(w["kv"][layer], batch, plan, outs[layer], offsets[layer],
+                                    size)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3 / (reps * layers)
+    enc_bytes = sum(sum(size) for size in sizes) / layers
+    modes = {}
+    for got in fields:
+        for mode, _ in got:
+            modes[str(mode)] = modes.get(str(mode), 0) + 1
+
+    def frac(nbytes, ms):
+        return round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
+
+    result = {
+        "requests": count, "blocks_per_request": per,
+        "raw_bytes_per_request": 4 * per * bw, "raw_bytes_per_layer": raw,
+        "modes": modes, "encoded_bytes_per_layer": int(enc_bytes),
+        "compression_ratio": round(raw / enc_bytes, 5),
+        "plan_ms_per_layer_call": round(plan_ms, 5),
+        "encode_ms_per_layer_call": round(enc_ms, 5),
+        "decode_ms_per_layer_call": round(dec_ms, 5),
+        # plan: reads the raw words once; encode: reads them again and writes the
+        # payloads; decode: reads the payloads and writes the raw words
+        "plan_hbm_frac": frac(raw, plan_ms),
+        "encode_hbm_frac": frac(raw + enc_bytes, enc_ms),
+        "decode_hbm_frac": frac(raw + enc_bytes, dec_ms),
+        # the sender's kernels against one read of the words and one write of the
+        # payloads (the reference's choice needs the whole request's statistics
+        # before any byte is written, so the words are read twice)
+        "sender_gpu_hbm_frac": frac(raw + enc_bytes, plan_ms + enc_ms),
+        "sender_host_inclusive_ms_per_layer": round(host_ms, 4),
+        "verified": True,
+    }
+    if cpu_seconds > 0:
+        # CPU baseline: the oracle's numpy torch-op encoder on requests of layer 0
+        # (test infrastructure, timed as the reported baseline only)
+        import oracle
+
+        k = min(count, 16)
+        sample = w["kv"][0].index_select(1, ids_s[:k * per]).view(torch.int16).cpu().numpy()
+        sample = sample.view(np.uint16).reshape(2, k, per * bw)
+        done_bytes, r, t0 = 0, 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds:
+            words = sample[:, r % k].reshape(-1)
+            if oracle.encode_torchop(words) is None:
+                raise RuntimeError("the oracle declined a request the GPU encoded")
+            done_bytes += 2 * words.size
+            r += 1
+        cpu_s = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": round(done_bytes / cpu_s / 1e9, 4), "unit": "GB/s raw bf16 (encode only)",
+            "cores": 1, "kind": "port",
+            "sample": f"{r} requests of layer 0 ({k} distinct), {round(cpu_s, 1)} s, the "
+                      "oracle's numpy torch-op encoder"}
+    return result
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (the oracle's C codec, test infrastructure, timed on this host)
 
@@ -1333,6 +1469,8 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
         torch.cuda.synchronize()
         verify(torch, w)
         time_writeback(torch, sz, w, reps=1)
+        if name == "llama3-8b-paged":
+            time_torchop_sender(torch, sz, w, reps=1, cpu_seconds=0.0)
         calibration_copy(torch, w["device"])
         return {"profile_steps": args.profile_steps, "workload": name,
                 "calibration_copy_bytes": CALIBRATION_BYTES}
@@ -1466,6 +1604,7 @@ def run_codec(args, torch, sz, workloads, name: str, headline: bool = True):
                                                    raw_bytes=raw_layer * layers)
         result["exponent_histogram"] = time_histogram(torch, sz, w)
         result["codec_writeback"] = time_writeback(torch, sz, w)
+        result["torchop_sender"] = time_torchop_sender(torch, sz, w)
         result["dropin_per_request"] = time_dropin(torch, sz, w)
         result["staging_overlap"] = time_overlap(torch, sz, w)
         result["connector_layer"] = time_connector(torch, sz, w)

@@ -96,7 +96,8 @@ __device__ __forceinline__ unsigned int code_at(const unsigned char* sec, unsign
   return ((lo | (hi << 8)) >> (bit & 7)) & ((1u << w) - 1u);
 }
 
-__global__ __launch_bounds__(kThreads) void torchop_decode(LaunchArgs a, TorchopSizes sizes) {
+__global__ __launch_bounds__(kThreads) void torchop_decode_generic(LaunchArgs a,
+                                                                   TorchopSizes sizes) {
   __shared__ unsigned char s_hdr[260];
   const unsigned int tid = threadIdx.x;
   const unsigned int r = blockIdx.y;
@@ -216,9 +217,10 @@ __device__ __forceinline__ unsigned int word_at(const uint32_t (&w)[8], unsigned
   return (w[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
 }
 
-// Workgroup (x, y): tile x of payload y; each thread marks the values of its 16
-// words in LDS byte maps, one ballot per wave turns them into mask bits.
-__global__ __launch_bounds__(kThreads) void torchop_presence(LaunchArgs a) {
+// Any geometry. Workgroup (x, y): tile x of payload y; each thread marks the values
+// of its 16 words in LDS byte maps, one ballot per wave turns them into mask bits.
+__global__ __launch_bounds__(kThreads) void torchop_presence_generic(LaunchArgs a,
+                                                                     unsigned int record_base) {
   __shared__ unsigned char s_high[256];
   __shared__ unsigned char s_nib[64];
   const unsigned int tid = threadIdx.x;
@@ -242,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void torchop_presence(LaunchArgs a) {
   }
   __syncthreads();
   const unsigned int lane = tid & (kWave - 1), wave = tid >> 6;
-  unsigned int* rec = a.workspace + kTorchopRecordWords * (d.tile_begin + blockIdx.x);
+  unsigned int* rec =
+      a.workspace + kTorchopRecordWords * (record_base + d.tile_begin + blockIdx.x);
   const unsigned long long high = __ballot(s_high[tid] != 0);
   if (lane == 0) {
     rec[2 * wave] = (unsigned int)high;
@@ -283,7 +286,8 @@ __device__ __forceinline__ void nibble_masks(const unsigned int (&high)[8], unsi
 
 // One workgroup per payload: OR of its tile records, then the reference's format
 // choice (vllm_connector.py:3210-3213, 3219-3222, 3250-3253, 3279-3290, 3310-3311).
-__global__ __launch_bounds__(kThreads) void torchop_plan(LaunchArgs a, TorchopPlan* plans) {
+__global__ __launch_bounds__(kThreads) void torchop_plan(LaunchArgs a, unsigned int record_base,
+                                                        TorchopPlan* plans) {
   __shared__ unsigned int s_or[9];
   const unsigned int tid = threadIdx.x;
   const PayloadDesc d = a.p[blockIdx.x];
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void torchop_plan(LaunchArgs a, TorchopPl
   __syncthreads();
   unsigned int part[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   for (unsigned int t = tid; t < tiles; t += kThreads) {
-    const unsigned int* rec = a.workspace + kTorchopRecordWords * (d.tile_begin + t);
+    const unsigned int* rec = a.workspace + kTorchopRecordWords * (record_base + d.tile_begin + t);
 #pragma unroll
     for (int k = 0; k < 9; ++k) part[k] |= rec[k];
   }
@@ -391,77 +395,115 @@ __device__ __forceinline__ void put_codes(unsigned char* sec, unsigned long long
     dst[j] = (unsigned char)(j < 8 ? lo >> (8 * j) : hi >> (8 * (j - 8)));
 }
 
-// Workgroup (x, y): words [4096 x, 4096 x + 4096) of payload y, 16 per thread;
-// workgroup x == 0 also writes the header. Payloads whose plan declined, or whose
-// plan size is not the size the host laid out, are skipped.
-__global__ __launch_bounds__(kThreads) void torchop_encode(LaunchArgs a, const TorchopPlan* plans,
-                                                           TorchopSizes sizes) {
+// The plan's fields, the rank tables in LDS (mode 0: high byte -> palette index;
+// mode 1: entry 16q + v -> index of nibble value v in plane q's palette) and, with
+// `header`, the payload's header and palettes (vllm_connector.py:3226-3228,
+// 3259-3261, 3300-3307). `ok`: the plan encodes the payload (a format was chosen,
+// for n words, at the size the host laid out); nothing is written otherwise. The
+// record is read as 16 aligned dwords (scalar loads), and no register array is
+// indexed per thread (such an array would be placed in memory). The caller
+// synchronises before reading s_rank.
+struct EncodeFields {
+  unsigned int mode;
+  unsigned int widths;  // one byte per nibble plane (mode 1); mode 0 and 2: byte 0
+  unsigned int mag_min;
+  bool ok;
+};
+
+__device__ __forceinline__ unsigned int plane_width(const EncodeFields& f, int q) {
+  return (f.widths >> (8 * q)) & 0xFFu;
+}
+
+__device__ __forceinline__ unsigned int pick4(unsigned int i, unsigned int a0, unsigned int a1,
+                                              unsigned int a2, unsigned int a3) {
+  return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
+}
+
+__device__ __forceinline__ EncodeFields encode_prologue(const TorchopPlan* plan,
+                                                        unsigned long long n,
+                                                        unsigned long long size,
+                                                        unsigned char* out,
+                                                        unsigned char* s_rank, bool header) {
+  const unsigned int tid = threadIdx.x;
+  const unsigned int* pw = reinterpret_cast<const unsigned int*>(plan);
+  unsigned int high[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) high[k] = pw[k];
+  const unsigned int nibbles = pw[8], w9 = pw[9], w10 = pw[10];
+  const unsigned long long encoded = pw[12] | ((unsigned long long)pw[13] << 32);
+  const unsigned long long words = pw[14] | ((unsigned long long)pw[15] << 32);
+  EncodeFields f;
+  f.mode = w9 & 0xFFu;                  // byte 36
+  f.widths = (w9 >> 8) | (w10 << 24);   // bytes 37-40
+  f.mag_min = (w10 >> 8) & 0xFFu;       // byte 41
+  f.ok = f.mode != kTorchopNone && encoded == size && words == n;
+  unsigned int nib[4];
+  nibble_masks(high, nibbles, nib);
+  unsigned int rank = 0, present = 0;
+  if (f.mode == 0) {
+    const unsigned int h = tid, hw = h >> 5;
+    unsigned int word = 0, below = 0;
+#pragma unroll
+    for (unsigned int k = 0; k < 8; ++k) {
+      word = k == hw ? high[k] : word;
+      below += k < hw ? (unsigned int)__popc(high[k]) : 0u;
+    }
+    rank = below + (unsigned int)__popc(word & ((1u << (h & 31)) - 1u));
+    present = (word >> (h & 31)) & 1u;
+  } else if (f.mode == 1 && tid < 64) {
+    const unsigned int q = tid >> 4, v = tid & 15;
+    const unsigned int m = pick4(q, nib[0], nib[1], nib[2], nib[3]);
+    rank = (unsigned int)__popc(m & ((1u << v) - 1u));
+    present = (m >> v) & 1u;
+  }
+  s_rank[tid] = (unsigned char)rank;
+  if (header && f.ok) {
+    if (f.mode == 2) {
+      if (tid == 0) out[0] = 2;
+      if (tid == 1) out[1] = (unsigned char)plane_width(f, 0);
+      if (tid == 2) out[2] = (unsigned char)f.mag_min;
+    } else if (f.mode == 0) {
+      unsigned int distinct = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) distinct += (unsigned int)__popc(high[k]);
+      if (tid == 0) {
+        out[0] = 0;
+        out[1] = (unsigned char)plane_width(f, 0);
+      }
+      if (present) out[2 + rank] = (unsigned char)tid;
+      if (tid >= distinct) out[2 + tid] = 0;
+    } else if (tid < 64) {
+      const unsigned int q = tid >> 4, v = tid & 15;
+      const unsigned int m = pick4(q, nib[0], nib[1], nib[2], nib[3]);
+      if (present) out[5 + 16 * q + rank] = (unsigned char)v;
+      if (v >= (unsigned int)__popc(m)) out[5 + 16 * q + v] = 0;
+      if (tid == 0) out[0] = 1;
+      if (tid < 4) out[1 + tid] = (unsigned char)(f.widths >> (8 * tid));
+    }
+  }
+  return f;
+}
+
+// Any geometry. Workgroup (x, y): words [4096 x, 4096 x + 4096) of payload y, 16
+// per thread; workgroup x == 0 also writes the header. Payloads whose plan
+// declined, or whose plan size is not the size the host laid out, are skipped.
+__global__ __launch_bounds__(kThreads) void torchop_encode_generic(LaunchArgs a,
+                                                                   const TorchopPlan* plans,
+                                                                   TorchopSizes sizes) {
   __shared__ unsigned char s_rank[256];
   const unsigned int tid = threadIdx.x;
   const unsigned int r = blockIdx.y;
   const PayloadDesc d = a.p[r];
   const unsigned long long n = payload_words(a, d);
   const unsigned long long tile0 = (unsigned long long)blockIdx.x * kTorchopTile;
-  const TorchopPlan& plan = plans[r];
-  const unsigned int mode = plan.mode;
-  if (tile0 >= n || mode == kTorchopNone || plan.encoded_bytes != sizes.encoded[r] ||
-      plan.words != n)
-    return;  // the whole workgroup
-  unsigned int high[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) high[k] = plan.high[k];
-  unsigned int width[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) width[q] = plan.width[q];
-  const unsigned int mag_min = plan.mag_min;
+  if (tile0 >= n) return;  // the whole workgroup
   unsigned char* out = a.buf + d.buf_offset;
-
-  // rank tables: mode 0, high byte -> palette index; mode 1, entry 16q + v -> index
-  // of nibble value v in plane q's palette
-  unsigned int nib[4];
-  nibble_masks(high, plan.nibbles, nib);
-  {
-    unsigned int rank = 0, present = 0;
-    if (mode == 0) {
-      // (mask words read from the plan in memory: a per-thread index into a
-      // register array would go through scratch)
-      const unsigned int h = tid;
-      const unsigned int word = plan.high[h >> 5];
-      rank = (unsigned int)__popc(word & ((1u << (h & 31)) - 1u));
-#pragma unroll
-      for (unsigned int k = 0; k < 8; ++k) rank += k < (h >> 5) ? (unsigned int)__popc(high[k]) : 0u;
-      present = (word >> (h & 31)) & 1u;
-    } else if (mode == 1 && tid < 64) {
-      const unsigned int q = tid >> 4, v = tid & 15;
-      rank = (unsigned int)__popc(nib[q] & ((1u << v) - 1u));
-      present = (nib[q] >> v) & 1u;
-    }
-    s_rank[tid] = (unsigned char)rank;
-    if (blockIdx.x == 0) {
-      // header (vllm_connector.py:3226-3228, 3259-3261, 3300-3307)
-      if (mode == 2) {
-        if (tid == 0) out[0] = 2;
-        if (tid == 1) out[1] = (unsigned char)width[0];
-        if (tid == 2) out[2] = (unsigned char)mag_min;
-      } else if (mode == 0) {
-        unsigned int distinct = 0;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) distinct += (unsigned int)__popc(high[k]);
-        if (tid == 0) {
-          out[0] = 0;
-          out[1] = (unsigned char)width[0];
-        }
-        if (present) out[2 + rank] = (unsigned char)tid;
-        if (tid >= distinct) out[2 + tid] = 0;
-      } else if (tid < 64) {
-        const unsigned int q = tid >> 4, v = tid & 15;
-        if (present) out[5 + 16 * q + rank] = (unsigned char)v;
-        if (v >= (unsigned int)__popc(nib[q])) out[5 + 16 * q + v] = 0;
-        if (tid == 0) out[0] = 1;
-        if (tid < 4) out[1 + tid] = (unsigned char)width[tid];
-      }
-    }
-  }
+  const EncodeFields f = encode_prologue(plans + r, n, sizes.encoded[r], out, s_rank,
+                                         blockIdx.x == 0);
+  if (!f.ok) return;
+  const unsigned int mode = f.mode, mag_min = f.mag_min;
+  const unsigned int width[4] = {plane_width(f, 0), plane_width(f, 1), plane_width(f, 2),
+                                 plane_width(f, 3)};
   __syncthreads();
   const unsigned long long i0 = tile0 + (unsigned long long)tid * kWordsPerLane;
   if (i0 >= n) return;
@@ -501,10 +543,271 @@ __global__ __launch_bounds__(kThreads) void torchop_encode(LaunchArgs a, const T
   }
 }
 
+// ---------------------------------------------------------------------------
+// tile kernels: block words a multiple of 1024 (a 1024-word wave chunk lies in one
+// block), the layer 16-byte aligned. Workgroup (x, y): words [4096 x, 4096 x +
+// 4096) of payload y; wave w owns the chunk at 4096 x + 1024 w (its block found
+// with scalar loads), lane l the two 8-word runs at 8 l and 512 + 8 l of it. Every
+// section access of a wave instruction is then one contiguous span: the run's 16
+// source bytes, its 8 low bytes, its sign byte and its w code bytes (w-bit codes of
+// 8 words fill whole bytes) at the section offset of word i, w * i / 8. Payload
+// sections start at any byte (global memory takes unaligned accesses).
+
+typedef unsigned short u16_unaligned __attribute__((aligned(1)));
+typedef unsigned int u32_unaligned __attribute__((aligned(1)));
+
+// Little-endian bytes [0, w) at p, 1 <= w <= 7 (w uniform): one access per set bit.
+__device__ __forceinline__ unsigned long long load_bytes(const unsigned char* p, unsigned int w) {
+  unsigned long long v = 0;
+  unsigned int at = 0;
+  if (w & 4) {
+    v = *reinterpret_cast<const u32_unaligned*>(p);
+    at = 4;
+  }
+  if (w & 2) {
+    v |= (unsigned long long)*reinterpret_cast<const u16_unaligned*>(p + at) << (8 * at);
+    at += 2;
+  }
+  if (w & 1) v |= (unsigned long long)p[at] << (8 * at);
+  return v;
+}
+
+__device__ __forceinline__ void store_bytes(unsigned char* p, unsigned long long v,
+                                            unsigned int w) {
+  unsigned int at = 0;
+  if (w & 4) {
+    *reinterpret_cast<u32_unaligned*>(p) = (unsigned int)v;
+    at = 4;
+  }
+  if (w & 2) {
+    *reinterpret_cast<u16_unaligned*>(p + at) = (unsigned short)(v >> (8 * at));
+    at += 2;
+  }
+  if (w & 1) p[at] = (unsigned char)(v >> (8 * at));
+}
+
+// Element offset in the layer of the wave chunk starting at payload word c.
+__device__ __forceinline__ unsigned long long chunk_source(const LaunchArgs& a,
+                                                           const PayloadDesc& d,
+                                                           const EncodeGeom& geo,
+                                                           unsigned long long n,
+                                                           unsigned long long c) {
+  const unsigned long long half = n >> 1;
+  const unsigned int plane = c >= half ? 1u : 0u;
+  const unsigned int in_plane = uniform((unsigned int)(c - plane * half));
+  const unsigned int j = uniform(div_u32(in_plane, geo.bw_magic, geo.bw));
+  const unsigned int within = in_plane - j * geo.bw;
+  const unsigned long long blk = uniform64((unsigned long long)a.ids[d.ids_offset + j]);
+  return uniform64(plane * a.plane_stride + blk * a.block_stride + within);
+}
+
+// Codes k = 0..7 of a run, `width` bits each, LSB-first.
+__device__ __forceinline__ unsigned int run_code(unsigned long long codes, unsigned int width,
+                                                 int k) {
+  return (unsigned int)(codes >> (width * k)) & ((1u << width) - 1u);
+}
+
+__global__ __launch_bounds__(kThreads) void torchop_presence_tile(LaunchArgs a, EncodeGeom geo,
+                                                                  unsigned int record_base) {
+  __shared__ unsigned char s_high[256];
+  __shared__ unsigned int s_nib;
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const unsigned int tile = group_index();
+  const PayloadDesc d = a.p[find_payload(a, tile)];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned long long c = (unsigned long long)(tile - d.tile_begin) * kTorchopTile + wave * 1024ull;
+  const bool active = c < n;
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  if (active) {
+    const uint16_t* src = a.kv + chunk_source(a, d, geo, n, c);
+    v0 = load_stream16(src + 8 * lane);
+    v1 = load_stream16(src + 512 + 8 * lane);
+  }
+  if (tid < 64) reinterpret_cast<unsigned int*>(s_high)[tid] = 0;
+  if (tid == 0) s_nib = 0;
+  __syncthreads();
+  if (active) {
+    const uint32_t x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    unsigned int nib = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      s_high[(x[k] >> 8) & 0xFF] = 1;
+      s_high[x[k] >> 24] = 1;
+      nib |= (1u << (x[k] & 15)) | (1u << (16 + ((x[k] >> 4) & 15)));
+      nib |= (1u << ((x[k] >> 16) & 15)) | (1u << (16 + ((x[k] >> 20) & 15)));
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) nib |= __shfl_xor(nib, off, kWave);
+    if (lane == 0) atomicOr(&s_nib, nib);
+  }
+  __syncthreads();
+  unsigned int* rec = a.workspace + kTorchopRecordWords * (record_base + tile);
+  const unsigned long long high = __ballot(s_high[tid] != 0);
+  if (lane == 0) {
+    rec[2 * wave] = (unsigned int)high;
+    rec[2 * wave + 1] = (unsigned int)(high >> 32);
+  }
+  if (tid == 0) rec[8] = s_nib;
+}
+
+__global__ __launch_bounds__(kThreads) void torchop_encode_tile(LaunchArgs a, EncodeGeom geo,
+                                                                const TorchopPlan* plans,
+                                                                TorchopSizes sizes) {
+  __shared__ unsigned char s_rank[256];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const unsigned int tile = group_index();
+  const unsigned int r = find_payload(a, tile);
+  const PayloadDesc d = a.p[r];
+  const unsigned long long n = payload_words(a, d);
+  const unsigned int local = tile - d.tile_begin;
+  const unsigned long long c = (unsigned long long)local * kTorchopTile + wave * 1024ull;
+  const bool active = c < n;
+  // the words first: the plan's round trip overlaps with theirs
+  u32x4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+  if (active) {
+    const uint16_t* src = a.kv + chunk_source(a, d, geo, n, c);
+    v0 = load_stream16(src + 8 * lane);
+    v1 = load_stream16(src + 512 + 8 * lane);
+  }
+  unsigned char* out = a.buf + d.buf_offset;
+  const EncodeFields f = encode_prologue(plans + r, n, sizes.encoded[r], out, s_rank, local == 0);
+  if (!f.ok) return;  // the whole workgroup
+  __syncthreads();
+  if (!active) return;
+  const uint32_t x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+  for (int run = 0; run < 2; ++run) {
+    const uint32_t* xr = x + 4 * run;
+    const unsigned long long i = c + 512 * run + 8 * lane;  // the run's first word
+    if (f.mode == 1) {
+      unsigned long long at = 69;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned int w = plane_width(f, q);
+        unsigned long long codes = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const unsigned int word = (xr[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+          const unsigned int v = s_rank[16 * q + ((word >> (4 * q)) & 15)] & ((1u << w) - 1u);
+          codes |= (unsigned long long)v << (w * k);
+        }
+        store_bytes(out + at + w * (i >> 3), codes, w);
+        at += n * w / 8;
+      }
+      continue;
+    }
+    // low bytes: bytes 0 and 2 of each dword
+    const u32x2 low = {__builtin_amdgcn_perm(xr[1], xr[0], 0x06040200u),
+                       __builtin_amdgcn_perm(xr[3], xr[2], 0x06040200u)};
+    const unsigned int w = plane_width(f, 0);
+    unsigned long long codes = 0;
+    unsigned int signs = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const unsigned int word = (xr[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+      unsigned int v;
+      if (f.mode == 2) {
+        signs |= (word >> 15) << k;
+        v = ((word >> 8) & 0x7Fu) - f.mag_min;
+      } else {
+        v = s_rank[word >> 8];
+      }
+      codes |= (unsigned long long)(v & ((1u << w) - 1u)) << (w * k);
+    }
+    if (f.mode == 2) {
+      store_stream8(out + 3 + i, low);
+      out[3 + n + (i >> 3)] = (unsigned char)signs;
+      store_bytes(out + 3 + n + n / 8 + w * (i >> 3), codes, w);
+    } else {
+      store_stream8(out + 258 + i, low);
+      store_bytes(out + 258 + n + w * (i >> 3), codes, w);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void torchop_decode_tile(LaunchArgs a, EncodeGeom geo,
+                                                                TorchopSizes sizes) {
+  __shared__ unsigned char s_hdr[260];
+  const unsigned int tid = threadIdx.x;
+  const unsigned int lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const unsigned int tile = group_index();
+  const unsigned int r = find_payload(a, tile);
+  const PayloadDesc d = a.p[r];
+  const unsigned long long n = 2ull * d.block_count * a.block_words;
+  const unsigned long long size = sizes.encoded[r];
+  const unsigned char* payload = a.buf + d.buf_offset;
+  const unsigned long long c =
+      (unsigned long long)(tile - d.tile_begin) * kTorchopTile + wave * 1024ull;
+  const bool active = c < n;
+  // the destination's block (scalar loads) while the header comes in
+  uint16_t* dst = active ? a.kv + chunk_source(a, d, geo, n, c) : nullptr;
+  for (unsigned int k = tid; k < 258; k += kThreads) s_hdr[k] = k < size ? payload[k] : 0;
+  __syncthreads();
+  const TorchopHeader h = parse_header(s_hdr, size, n);
+  if (!h.ok || !active) return;
+  u32x4 o[2];
+#pragma unroll
+  for (int run = 0; run < 2; ++run) {
+    const unsigned long long i = c + 512 * run + 8 * lane;
+    unsigned int word[8];
+    if (h.mode == 1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) word[k] = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const unsigned int w = h.width[q];
+        const unsigned long long codes = load_bytes(payload + h.code_at[q] + w * (i >> 3), w);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          word[k] |= (unsigned int)s_hdr[5 + 16 * q + run_code(codes, w, k)] << (4 * q);
+      }
+    } else {
+      const u32x2 low = load_stream8(payload + h.low_at + i);
+      const unsigned int w = h.width[0];
+      const unsigned long long codes = load_bytes(payload + h.code_at[0] + w * (i >> 3), w);
+      const unsigned int signs = h.mode == 2 ? payload[h.sign_at + (i >> 3)] : 0u;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const unsigned int code = run_code(codes, w, k);
+        const unsigned int hi = h.mode == 2 ? (((signs >> k) & 1u) << 7) | (code + h.mag_min)
+                                            : (unsigned int)s_hdr[2 + code];
+        const unsigned int lo = ((k < 4 ? low.x : low.y) >> (8 * (k & 3))) & 0xFFu;
+        word[k] = (hi << 8) | lo;
+      }
+    }
+    o[run].x = (word[0] & 0xFFFFu) | (word[1] << 16);
+    o[run].y = (word[2] & 0xFFFFu) | (word[3] << 16);
+    o[run].z = (word[4] & 0xFFFFu) | (word[5] << 16);
+    o[run].w = (word[6] & 0xFFFFu) | (word[7] << 16);
+  }
+  // write-through stores after the last load (the compiler's waits do not see them)
+  asm volatile("" ::"v"(o[0]), "v"(o[1]));
+  store_through16(dst + 8 * lane, o[0]);
+  store_through16(dst + 512 + 8 * lane, o[1]);
+}
+
 }  // namespace
 }  // namespace unchainkv
 
 using namespace unchainkv;
+
+namespace {
+
+unsigned long long torchop_tiles(unsigned long long n) {
+  return (n + kTorchopTile - 1) / kTorchopTile;
+}
+
+// The tile kernels' geometry: 1024-word wave chunks inside one block, 16-byte
+// aligned runs of the layer.
+bool torchop_tile_geometry(unsigned long long kv_ptr, unsigned long long plane_stride,
+                           unsigned long long block_stride, unsigned long long block_words) {
+  return block_words % 1024 == 0 && kv_ptr % 16 == 0 && plane_stride % 8 == 0 &&
+         block_stride % 8 == 0;
+}
+
+}  // namespace
 
 // Decodes payload r (src + src_offsets[r], encoded_bytes[r] long; byte 0 is its
 // mode, 0, 1 or 2) and scatters it into blocks ids[block_offsets[r] ..
@@ -528,6 +831,8 @@ extern "C" long long kvq_splitzip_bf16_decode_torchop_paged(
     total += 2 * n;
     max_n = std::max(max_n, n);
   }
+  const bool tiles = torchop_tile_geometry(kv_ptr, plane_stride, block_stride, block_words);
+  const EncodeGeom geo = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
     LaunchArgs a{};
@@ -540,18 +845,29 @@ extern "C" long long kvq_splitzip_bf16_decode_torchop_paged(
     a.block_words = block_words;
     const unsigned int count =
         (unsigned int)std::min<unsigned long long>(kMaxPayloads, payload_count - first);
-    unsigned long long launch_max = 0;
+    unsigned long long launch_max = 0, launch_tiles = 0;
+    bool uniform_size = true;
     for (unsigned int k = 0; k < count; ++k) {
       const unsigned long long r = first + k;
       a.p[k].buf_offset = src_offsets[r];
       a.p[k].ids_offset = block_offsets[r];
       a.p[k].block_count = (unsigned int)(block_offsets[r + 1] - block_offsets[r]);
+      a.p[k].tile_begin = (unsigned int)launch_tiles;
       sizes.encoded[k] = encoded_bytes[r];
-      launch_max = std::max(launch_max, 2ull * a.p[k].block_count * block_words);
+      const unsigned long long n = 2ull * a.p[k].block_count * block_words;
+      launch_max = std::max(launch_max, n);
+      launch_tiles += torchop_tiles(n);
+      uniform_size = uniform_size && a.p[k].block_count == a.p[0].block_count;
     }
     a.payload_count = count;
     const dim3 grid((unsigned int)((launch_max + kTorchopTile - 1) / kTorchopTile), count);
-    hipLaunchKernelGGL(torchop_decode, grid, dim3(kThreads), 0, stream, a, sizes);
+    if (tiles && launch_tiles <= 0xFFFFFFFFULL) {
+      a.total_tiles = (unsigned int)launch_tiles;
+      a.uniform_tiles = uniform_size ? (unsigned int)(launch_tiles / count) : 0;
+      hipLaunchKernelGGL(torchop_decode_tile, dim3(a.total_tiles), dim3(kThreads), 0, stream, a,
+                         geo, sizes);
+    } else
+      hipLaunchKernelGGL(torchop_decode_generic, grid, dim3(kThreads), 0, stream, a, sizes);
     const hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_decode", st);
   }
@@ -560,14 +876,12 @@ extern "C" long long kvq_splitzip_bf16_decode_torchop_paged(
 
 namespace {
 
-// Tile records of a launch's payloads (first, first + count) start at their
-// payloads' tile prefix over the whole call.
-unsigned long long torchop_tiles(unsigned long long n) {
-  return (n + kTorchopTile - 1) / kTorchopTile;
-}
 
-// Fills the launch arguments of payloads [first, first + count); false when a
-// payload's word count is past the kernels' limit.
+// Fills the launch arguments of payloads [first, first + count): descriptors with
+// their first tile within the launch, the launch's tile count and, when every
+// payload has the same size, its tiles per payload. The launch's tile records
+// start at record tile_prefix. False when a word or tile count is past the
+// kernels' limits.
 bool torchop_args(LaunchArgs& a, unsigned long long kv_ptr, unsigned long long plane_stride,
                   unsigned long long block_stride, unsigned long long block_words,
                   unsigned long long block_ids_ptr, const unsigned long long* block_offsets,
@@ -581,18 +895,23 @@ bool torchop_args(LaunchArgs& a, unsigned long long kv_ptr, unsigned long long p
   a.block_words = block_words;
   a.payload_count = count;
   max_n = 0;
-  unsigned long long tile = tile_prefix;
+  unsigned long long tile = 0;  // tiles of the launch before payload k
+  bool uniform_size = true;
   for (unsigned int k = 0; k < count; ++k) {
     const unsigned long long r = first + k;
     const unsigned long long blocks = block_offsets[r + 1] - block_offsets[r];
     const unsigned long long n = 2 * blocks * block_words;
-    if (n > 0x7FFFFFFFULL || tile > 0xFFFFFFFFULL) return false;
+    if (n > 0x7FFFFFFFULL || tile_prefix + tile > 0xFFFFFFFFULL) return false;
     a.p[k].ids_offset = block_offsets[r];
     a.p[k].block_count = (unsigned int)blocks;
     a.p[k].tile_begin = (unsigned int)tile;
     tile += torchop_tiles(n);
     max_n = std::max(max_n, n);
+    uniform_size = uniform_size && blocks == block_offsets[first + 1] - block_offsets[first];
   }
+  if (tile > 0xFFFFFFFFULL) return false;
+  a.total_tiles = (unsigned int)tile;
+  a.uniform_tiles = uniform_size ? (unsigned int)(tile / count) : 0;
   return true;
 }
 
@@ -638,6 +957,8 @@ extern "C" long long kvq_splitzip_bf16_plan_torchop_paged(
   const unsigned long long need =
       kvq_splitzip_torchop_workspace_bytes(block_words, block_offsets, payload_count);
   if (need == 0 || workspace_bytes < need) return 0;
+  const bool tiles = torchop_tile_geometry(kv_ptr, plane_stride, block_stride, block_words);
+  const EncodeGeom geo = make_geom(block_words);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   unsigned long long tile_prefix = 0;
   for (unsigned long long first = 0; first < payload_count; first += kMaxPayloads) {
@@ -649,16 +970,20 @@ extern "C" long long kvq_splitzip_bf16_plan_torchop_paged(
                       block_offsets, first, count, tile_prefix, max_n))
       return 0;
     a.workspace = reinterpret_cast<unsigned int*>(workspace_ptr);
-    hipLaunchKernelGGL(torchop_presence, dim3((unsigned int)torchop_tiles(max_n), count),
-                       dim3(kThreads), 0, stream, a);
+    const unsigned int base = (unsigned int)tile_prefix;
+    if (tiles)
+      hipLaunchKernelGGL(torchop_presence_tile, dim3(a.total_tiles), dim3(kThreads), 0, stream, a,
+                         geo, base);
+    else
+      hipLaunchKernelGGL(torchop_presence_generic, dim3((unsigned int)torchop_tiles(max_n), count),
+                         dim3(kThreads), 0, stream, a, base);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_presence", st);
-    hipLaunchKernelGGL(torchop_plan, dim3(count), dim3(kThreads), 0, stream, a,
+    hipLaunchKernelGGL(torchop_plan, dim3(count), dim3(kThreads), 0, stream, a, base,
                        reinterpret_cast<TorchopPlan*>(plans_ptr) + first);
     st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_plan", st);
-    for (unsigned int k = 0; k < count; ++k)
-      tile_prefix += torchop_tiles(2ull * a.p[k].block_count * block_words);
+    tile_prefix += a.total_tiles;
   }
   return (long long)payload_count;
 }
@@ -674,6 +999,8 @@ extern "C" long long kvq_splitzip_bf16_encode_torchop_paged(
       plans_ptr == 0 || plans_ptr % 8 != 0 || out_ptr == 0 || out_offsets == nullptr ||
       encoded_bytes == nullptr)
     return 0;
+  const bool tiles = torchop_tile_geometry(kv_ptr, plane_stride, block_stride, block_words);
+  const EncodeGeom geo = make_geom(block_words);
   unsigned long long total = 0;
   for (unsigned long long r = 0; r < payload_count; ++r) {
     const unsigned long long n = 2 * (block_offsets[r + 1] - block_offsets[r]) * block_words;
@@ -698,9 +1025,13 @@ extern "C" long long kvq_splitzip_bf16_encode_torchop_paged(
       a.p[k].buf_offset = out_offsets[first + k];
       sizes.encoded[k] = encoded_bytes[first + k];
     }
-    hipLaunchKernelGGL(torchop_encode, dim3((unsigned int)torchop_tiles(max_n), count),
-                       dim3(kThreads), 0, stream, a,
-                       reinterpret_cast<const TorchopPlan*>(plans_ptr) + first, sizes);
+    const dim3 grid((unsigned int)torchop_tiles(max_n), count);
+    const TorchopPlan* plans = reinterpret_cast<const TorchopPlan*>(plans_ptr) + first;
+    if (tiles)
+      hipLaunchKernelGGL(torchop_encode_tile, dim3(a.total_tiles), dim3(kThreads), 0, stream, a,
+                         geo, plans, sizes);
+    else
+      hipLaunchKernelGGL(torchop_encode_generic, grid, dim3(kThreads), 0, stream, a, plans, sizes);
     const hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_encode", st);
   }
