@@ -51,8 +51,12 @@ struct TorchopHeader {
   bool ok;
 };
 
-__device__ TorchopHeader parse_header(const unsigned char* h, unsigned long long size,
+// From the payload's first eight bytes (little-endian in `first8`).
+__device__ TorchopHeader parse_header(unsigned long long first8, unsigned long long size,
                                       unsigned long long n) {
+  unsigned int h[5];
+#pragma unroll
+  for (int k = 0; k < 5; ++k) h[k] = (unsigned int)(first8 >> (8 * k)) & 0xFFu;
   TorchopHeader t{};
   t.mode = h[0];
   t.ok = false;
@@ -108,7 +112,10 @@ __global__ __launch_bounds__(kThreads) void torchop_decode_generic(LaunchArgs a,
   // palettes and widths, from the first bytes of the payload
   for (unsigned int k = tid; k < 258; k += kThreads) s_hdr[k] = k < size ? payload[k] : 0;
   __syncthreads();
-  const TorchopHeader h = parse_header(s_hdr, size, n);
+  unsigned long long first8 = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) first8 |= (unsigned long long)s_hdr[k] << (8 * k);
+  const TorchopHeader h = parse_header(first8, size, n);
   if (!h.ok) return;
   const unsigned long long i0 =
       (unsigned long long)blockIdx.x * kTorchopTile + (unsigned long long)tid * kWordsPerLane;
@@ -729,7 +736,7 @@ __global__ __launch_bounds__(kThreads) void torchop_encode_tile(LaunchArgs a, En
 
 __global__ __launch_bounds__(kThreads) void torchop_decode_tile(LaunchArgs a, EncodeGeom geo,
                                                                 TorchopSizes sizes) {
-  __shared__ unsigned char s_hdr[260];
+  __shared__ unsigned char s_pal[256];
   const unsigned int tid = threadIdx.x;
   const unsigned int lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const unsigned int tile = group_index();
@@ -740,40 +747,68 @@ __global__ __launch_bounds__(kThreads) void torchop_decode_tile(LaunchArgs a, En
   const unsigned char* payload = a.buf + d.buf_offset;
   const unsigned long long c =
       (unsigned long long)(tile - d.tile_begin) * kTorchopTile + wave * 1024ull;
+  // a payload of these kernels holds at least 2048 words; a shorter size fails its
+  // header check below, and the header reads stay inside 16 bytes of the payload
+  if (size < 16) return;
+  // header bytes 0-7 from the aligned dwords that cover them (scalar loads, in
+  // parallel with the destination block's)
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(payload);
+  const unsigned int* hw = reinterpret_cast<const unsigned int*>(addr & ~(uintptr_t)3);
+  const unsigned int sh = (unsigned int)(addr & 3) * 8;
+  const unsigned long long lo64 = hw[0] | ((unsigned long long)hw[1] << 32);
+  const unsigned long long first8 =
+      sh ? (lo64 >> sh) | ((unsigned long long)hw[2] << (64 - sh)) : lo64;
   const bool active = c < n;
-  // the destination's block (scalar loads) while the header comes in
   uint16_t* dst = active ? a.kv + chunk_source(a, d, geo, n, c) : nullptr;
-  for (unsigned int k = tid; k < 258; k += kThreads) s_hdr[k] = k < size ? payload[k] : 0;
+  const TorchopHeader h = parse_header(first8, size, n);
+  if (!h.ok) return;  // the whole workgroup
+  // the palette bytes first, then every section load of both runs, so that the
+  // palette's LDS write waits for its own load only
+  unsigned int pal = 0;
+  if (h.mode == 0) pal = payload[2 + tid];
+  else if (h.mode == 1 && tid < 64) pal = payload[5 + tid];
+  u32x2 low[2] = {{0, 0}, {0, 0}};
+  unsigned long long codes[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+  unsigned int signs[2] = {0, 0};
+  if (active) {
+#pragma unroll
+    for (int run = 0; run < 2; ++run) {
+      const unsigned long long i = c + 512 * run + 8 * lane;
+      if (h.mode == 1) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          codes[run][q] = load_bytes(payload + h.code_at[q] + h.width[q] * (i >> 3), h.width[q]);
+      } else {
+        low[run] = load_stream8(payload + h.low_at + i);
+        codes[run][0] = load_bytes(payload + h.code_at[0] + h.width[0] * (i >> 3), h.width[0]);
+        if (h.mode == 2) signs[run] = payload[h.sign_at + (i >> 3)];
+      }
+    }
+  }
+  if (h.mode != 2) s_pal[tid] = (unsigned char)pal;
   __syncthreads();
-  const TorchopHeader h = parse_header(s_hdr, size, n);
-  if (!h.ok || !active) return;
+  if (!active) return;
   u32x4 o[2];
 #pragma unroll
   for (int run = 0; run < 2; ++run) {
-    const unsigned long long i = c + 512 * run + 8 * lane;
     unsigned int word[8];
     if (h.mode == 1) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) word[k] = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const unsigned int w = h.width[q];
-        const unsigned long long codes = load_bytes(payload + h.code_at[q] + w * (i >> 3), w);
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-          word[k] |= (unsigned int)s_hdr[5 + 16 * q + run_code(codes, w, k)] << (4 * q);
-      }
+          word[k] |= (unsigned int)s_pal[16 * q + run_code(codes[run][q], h.width[q], k)]
+                     << (4 * q);
     } else {
-      const u32x2 low = load_stream8(payload + h.low_at + i);
-      const unsigned int w = h.width[0];
-      const unsigned long long codes = load_bytes(payload + h.code_at[0] + w * (i >> 3), w);
-      const unsigned int signs = h.mode == 2 ? payload[h.sign_at + (i >> 3)] : 0u;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const unsigned int code = run_code(codes, w, k);
-        const unsigned int hi = h.mode == 2 ? (((signs >> k) & 1u) << 7) | (code + h.mag_min)
-                                            : (unsigned int)s_hdr[2 + code];
-        const unsigned int lo = ((k < 4 ? low.x : low.y) >> (8 * (k & 3))) & 0xFFu;
+        const unsigned int code = run_code(codes[run][0], h.width[0], k);
+        const unsigned int hi = h.mode == 2
+                                    ? (((signs[run] >> k) & 1u) << 7) | (code + h.mag_min)
+                                    : (unsigned int)s_pal[code];
+        const unsigned int lo = ((k < 4 ? low[run].x : low[run].y) >> (8 * (k & 3))) & 0xFFu;
         word[k] = (hi << 8) | lo;
       }
     }
