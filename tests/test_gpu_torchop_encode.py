@@ -211,3 +211,18 @@ def test_llama3_8b_small_requests(sz):
         assert expected is not None
         assert fields[r] == (int(expected[0]), expected.size)
         assert bytes(host[offsets[r]:offsets[r] + sizes[r]]) == expected.tobytes()
+
+
+def test_more_than_256_requests(sz):
+    """300 one-block requests (five presence launches of at most 64 payloads, two
+    plan launches of at most 256): every plan and payload is the oracle's."""
+    say("torchop encode 300 requests")
+    rng = np.random.default_rng(300)
+    bw = 1024
+    words_list = []
+    for r in range(300):
+        mode = (2, 0, 1)[r % 3]
+        width = 1 + r % (6 if mode == 2 else 7 if mode == 0 else 4)
+        words_list.append(words_for(rng, 2 * bw, mode, width))
+    fields, *_ = check_against_oracle(sz, words_list, bw, 310, seed=3)
+    assert {m for m, _ in fields} <= {0, 1, 2, 255}

@@ -293,18 +293,28 @@ __device__ __forceinline__ void nibble_masks(const unsigned int (&high)[8], unsi
 
 // One workgroup per payload: OR of its tile records, then the reference's format
 // choice (vllm_connector.py:3210-3213, 3219-3222, 3250-3253, 3279-3290, 3310-3311).
-__global__ __launch_bounds__(kThreads) void torchop_plan(LaunchArgs a, unsigned int record_base,
-                                                        TorchopPlan* plans) {
+// Payloads of one plan launch: each payload's first tile record and its blocks per
+// plane (the presence launches cover at most kMaxPayloads payloads each; one plan
+// launch follows all of them).
+constexpr unsigned int kPlanPayloads = 256;
+struct PlanArgs {
+  const unsigned int* workspace;
+  unsigned long long block_words;
+  unsigned int record_begin[kPlanPayloads];
+  unsigned int blocks[kPlanPayloads];
+};
+
+__global__ __launch_bounds__(kThreads) void torchop_plan(PlanArgs a, TorchopPlan* plans) {
   __shared__ unsigned int s_or[9];
   const unsigned int tid = threadIdx.x;
-  const PayloadDesc d = a.p[blockIdx.x];
-  const unsigned long long n = payload_words(a, d);
+  const unsigned long long n = 2ull * a.blocks[blockIdx.x] * a.block_words;
+  const unsigned int record0 = a.record_begin[blockIdx.x];
   const unsigned int tiles = (unsigned int)((n + kTorchopTile - 1) / kTorchopTile);
   if (tid < 9) s_or[tid] = 0;
   __syncthreads();
   unsigned int part[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
   for (unsigned int t = tid; t < tiles; t += kThreads) {
-    const unsigned int* rec = a.workspace + kTorchopRecordWords * (record_base + d.tile_begin + t);
+    const unsigned int* rec = a.workspace + kTorchopRecordWords * (record0 + t);
 #pragma unroll
     for (int k = 0; k < 9; ++k) part[k] |= rec[k];
   }
@@ -1012,13 +1022,28 @@ extern "C" long long kvq_splitzip_bf16_plan_torchop_paged(
     else
       hipLaunchKernelGGL(torchop_presence_generic, dim3((unsigned int)torchop_tiles(max_n), count),
                          dim3(kThreads), 0, stream, a, base);
-    hipError_t st = hipGetLastError();
+    const hipError_t st = hipGetLastError();
     if (st != hipSuccess) return fail("torchop_presence", st);
-    hipLaunchKernelGGL(torchop_plan, dim3(count), dim3(kThreads), 0, stream, a, base,
-                       reinterpret_cast<TorchopPlan*>(plans_ptr) + first);
-    st = hipGetLastError();
-    if (st != hipSuccess) return fail("torchop_plan", st);
     tile_prefix += a.total_tiles;
+  }
+  // one plan launch for up to kPlanPayloads payloads, after every presence launch
+  unsigned long long record = 0;
+  for (unsigned long long first = 0; first < payload_count; first += kPlanPayloads) {
+    const unsigned int count =
+        (unsigned int)std::min<unsigned long long>(kPlanPayloads, payload_count - first);
+    PlanArgs pa{};
+    pa.workspace = reinterpret_cast<const unsigned int*>(workspace_ptr);
+    pa.block_words = block_words;
+    for (unsigned int k = 0; k < count; ++k) {
+      const unsigned long long blocks = block_offsets[first + k + 1] - block_offsets[first + k];
+      pa.record_begin[k] = (unsigned int)record;
+      pa.blocks[k] = (unsigned int)blocks;
+      record += torchop_tiles(2 * blocks * block_words);
+    }
+    hipLaunchKernelGGL(torchop_plan, dim3(count), dim3(kThreads), 0, stream, pa,
+                       reinterpret_cast<TorchopPlan*>(plans_ptr) + first);
+    const hipError_t st = hipGetLastError();
+    if (st != hipSuccess) return fail("torchop_plan", st);
   }
   return (long long)payload_count;
 }
