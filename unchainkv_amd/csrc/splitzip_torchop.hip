@@ -23,9 +23,13 @@
 // codes LSB-first with zero padding bits). The host reads the plans' sizes between
 // the plan and the encode to lay the payloads out.
 //
-// Workgroup (x, y): payload y of the launch, words [4096 x, 4096 x + 4096); a thread
-// decodes 16 consecutive words. Byte-granular reads (these are fallback formats),
-// 16-byte stores when a thread's words lie in one block.
+// Kernels: `*_tile` for layers whose block words are a multiple of 1024 (a
+// 1024-word wave chunk lies in one block; one workgroup per 4096-word tile of the
+// launch, XCD-remapped, lanes own two 8-word runs so that every section access of
+// a wave instruction is one contiguous span), `*_generic` for any other geometry
+// (workgroup (x, y): words [4096 x, 4096 x + 4096) of payload y, 16 consecutive
+// words per thread, byte-granular section accesses). A launch covers at most 64
+// payloads; the plan kernel runs once for up to 256 after all presence launches.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
