@@ -245,7 +245,7 @@ def test_connector_deferred_writeback_of_early_saves(sz, codebooks):
     its untouched blocks."""
     say("connector deferred writeback")
     books = codebooks[5 * 32:6 * 32]
-    bw, pool = 16384, 112
+    bw, pool = 16384, 128
     rng = np.random.default_rng(15)
     words = books_words(rng, books, 2 * pool * bw, 0.0005).reshape(2, pool, bw)
     tables = [list(range(4, 20)), list(range(30, 48)), [50, 52] + list(range(53, 67)),
@@ -305,3 +305,21 @@ def test_connector_deferred_writeback_of_early_saves(sz, codebooks):
     assert [f["reason"] for n, f in early if n == "codec_writeback_skip"] == \
         ["overflow", "fragmented"]
     assert codec._deferred_codec_writebacks == {}
+    # the layer's next Top-16 attempt is the backoff's probe (a Top-16 encode that
+    # records presence masks, its payload copied once its mode byte shows it fits):
+    # deferred in the early stage too, and moved once its layer is ready
+    pend = codec.save_kv_layer(5, kv, [list(range(112, 128))], transfer_ids=["req-f"],
+                               early=True)
+    assert pend.presence is not None and pend.payloads[0].probe
+    got = codec.ready(pend)
+    assert got[0].bits == BITS_TOP16
+    probe_payload = bytes(got[0].view)
+    assert probe_payload == bytes(oracle.top16_encode(original[:, 112:128].reshape(-1), tab))
+    torch.cuda.synchronize()
+    assert np.array_equal(layer_bytes(kv), exp)
+    assert codec.finish_deferred_writebacks(5, kv, ["req-f"]) == len(probe_payload)
+    exp = expected_after(exp, [np.frombuffer(probe_payload, np.uint8)], [(112, 16)],
+                         lambda c: 2 * c * bw, 2 * pool * bw, 2 * bw)
+    torch.cuda.synchronize()
+    assert np.array_equal(layer_bytes(kv), exp)
+    codec.release(pend)
