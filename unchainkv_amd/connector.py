@@ -147,7 +147,7 @@ class LayerPayload:
     view: memoryview | None = None
     writeback: bool = False          # moved into its own blocks before the host copy
     writeback_segments: int = 0
-    deferred_writeback: bool = False  # early stage: moved into its blocks at a later save
+    deferred_writeback: bool = False  # early stage: moved by finish_deferred_writebacks
     _group: int = -1
     _offset: int = 0
     _status: int = -1                # index of its mode byte in the group's status copy
@@ -214,8 +214,9 @@ class SplitzipLayerCodec:
         # batches by block tables: a request keeps its block ids in every layer, so
         # a step's layers share them (built once, ids uploaded once)
         self._batches: dict = {}
-        # early-stage Top-16 payloads whose writeback waits for a later save of their
-        # layer: (transfer id, layer) -> (pending layer, payload, encode result, index)
+        # early-stage Top-16 payloads whose writeback waits for
+        # finish_deferred_writebacks: (transfer id, layer) -> (pending layer, payload,
+        # encode result, index in the encode group)
         self._deferred_codec_writebacks: dict = {}
 
     # ------------------------------------------------------------------
