@@ -1404,9 +1404,14 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   const bool large = max_tiles >= kFinLargeTiles;
   // a presence-mask encode (a layer that overflowed before: dense tiles
   // everywhere) spreads its placement over 32 groups per payload: 1 % outlier
-  // layer encode call 109.2 -> 105.8 us (16 groups: 106.5 us)
-  const dim3 fin_grid(a.payload_count *
-                          (a.presence && !a.inbody_slots ? kFinPresenceGroups : large ? 16 : 8) +
+  // layer encode call 109.2 -> 105.8 us (16 groups: 106.5 us). So does an encode of
+  // one or two payloads (the drop-in per-request call), whose escapes would
+  // otherwise be placed by 8 workgroups: 8.4 M-word request with an escape every
+  // 200 words 32.3 -> 20.2 us, with the benchmark's natural escapes 14.9 -> 15.5 us.
+  const bool few = a.payload_count <= 2;
+  const dim3 fin_grid(a.payload_count * ((a.presence || few) && !a.inbody_slots
+                                             ? kFinPresenceGroups
+                                             : large ? 16 : 8) +
                       (a.palette_info ? a.payload_count : 0));
   if (a.inbody_slots) {
     if (large)
@@ -1420,6 +1425,9 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
                        fin_grid, block, 0, stream, a);
   } else if (a.presence) {
     hipLaunchKernelGGL((top16_encode_finalize<kFinPresenceGroups, false, kDenseItemsDense>),
+                       fin_grid, block, 0, stream, a);
+  } else if (few) {
+    hipLaunchKernelGGL((top16_encode_finalize<kFinPresenceGroups, false, kDenseItemsSparse>),
                        fin_grid, block, 0, stream, a);
   } else if (large) {
     hipLaunchKernelGGL((top16_encode_finalize<16, false, kDenseItemsSparse>), fin_grid, block, 0,
