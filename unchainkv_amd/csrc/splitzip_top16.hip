@@ -67,6 +67,7 @@ namespace {
 // workgroups: Llama-3-70B TP8 encode call 73.5 -> 72.9 us with 8 for its largest
 // payloads of 2048 tiles)
 constexpr unsigned int kFinLargeTiles = 4096;
+constexpr unsigned int kFinFewTiles = 1024;
 constexpr int kFinPresenceGroups = 32;
 constexpr int kFinPreload = 8;                         // staged escapes loaded with the counts
 // Dense tiles (more staged escapes than the preload) placed per wave pass by the
@@ -1405,10 +1406,12 @@ long long launch_encode(LaunchArgs& a, const EncodeGeom& g, const Plan& p, hipSt
   // a presence-mask encode (a layer that overflowed before: dense tiles
   // everywhere) spreads its placement over 32 groups per payload: 1 % outlier
   // layer encode call 109.2 -> 105.8 us (16 groups: 106.5 us). So does an encode of
-  // one or two payloads (the drop-in per-request call), whose escapes would
-  // otherwise be placed by 8 workgroups: 8.4 M-word request with an escape every
-  // 200 words 32.3 -> 20.2 us, with the benchmark's natural escapes 14.9 -> 15.5 us.
-  const bool few = a.payload_count <= 2;
+  // one or two payloads of at least 1024 tiles (the drop-in per-request call),
+  // whose escapes would otherwise be placed by 8 workgroups: 8.4 M-word request with
+  // an escape every 200 words 32.3 -> 20.2 us, with the benchmark's natural escapes
+  // 14.9 -> 15.5 us. (A 1 M-word layer with natural escapes, a launch-bound call,
+  // keeps 8 groups: 8.3 us, 9.3 us with 32.)
+  const bool few = a.payload_count <= 2 && max_tiles >= kFinFewTiles;
   const dim3 fin_grid(a.payload_count * ((a.presence || few) && !a.inbody_slots
                                              ? kFinPresenceGroups
                                              : large ? 16 : 8) +
