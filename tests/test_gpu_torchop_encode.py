@@ -226,3 +226,45 @@ def test_more_than_256_requests(sz):
         words_list.append(words_for(rng, 2 * bw, mode, width))
     fields, *_ = check_against_oracle(sz, words_list, bw, 310, seed=3)
     assert {m for m, _ in fields} <= {0, 1, 2, 255}
+
+
+def test_misaligned_layer_takes_the_generic_kernels(sz):
+    """Block words a multiple of 1024 but the layer 2 bytes off 16-byte alignment:
+    plan, encode and decode take the generic kernels and still give the oracle's
+    payloads and an exact round trip."""
+    say("torchop misaligned layer")
+    rng = np.random.default_rng(77)
+    bw, pool = 2048, 12
+    words_list = [words_for(rng, 2 * 3 * bw, 2, 4), words_for(rng, 2 * 2 * bw, 0, 5),
+                  words_for(rng, 2 * 4 * bw, 1, 2)]
+    tables = [[1, 7, 3], [10, 0], [2, 4, 5, 9]]
+    host = rng.integers(0, 1 << 16, (2, pool, bw)).astype(np.uint16)
+    for words, t in zip(words_list, tables):
+        host[:, t] = words.reshape(2, len(t), bw)
+    backing = torch.zeros(2 * pool * bw + 1, dtype=torch.int16, device="cuda")
+    backing[1:] = torch.from_numpy(host.reshape(-1).view(np.int16)).cuda()
+    layer = backing[1:].view(torch.bfloat16).view(2, pool, bw)
+    assert layer.data_ptr() % 16 == 2
+    batch = sz.PagedBatch(tables, bw, "cuda")
+    plans = sz.plan_torchop_paged(layer, batch)
+    fields = sz.read_torchop_plans(plans.cpu().numpy())
+    sizes = [s for _, s in fields]
+    offsets = np.cumsum([0] + sizes)[:-1].tolist()
+    out = torch.zeros(sum(sizes), dtype=torch.uint8, device="cuda")
+    assert sz.encode_torchop_paged(layer, batch, plans, out, offsets, sizes) == sum(sizes)
+    got = out.cpu().numpy()
+    for r, words in enumerate(words_list):
+        expected = oracle.encode_torchop(words)
+        assert fields[r] == (int(expected[0]), expected.size)
+        assert bytes(got[offsets[r]:offsets[r] + sizes[r]]) == expected.tobytes(), r
+    # decode into a misaligned receiver through other blocks
+    recv_backing = torch.zeros_like(backing)
+    target = recv_backing[1:].view(torch.bfloat16).view(2, pool, bw)
+    recv_tables = [[11, 6, 8], [3, 1], [0, 2, 4, 5]]
+    recv = sz.PagedBatch(recv_tables, bw, "cuda")
+    assert sz.decode_torchop_paged(out, offsets, sizes, target, recv) == \
+        sum(2 * w.size for w in words_list)
+    torch.cuda.synchronize()
+    res = target.view(torch.int16).cpu().numpy().view(np.uint16).reshape(2, pool, bw)
+    for words, t in zip(words_list, recv_tables):
+        assert np.array_equal(res[:, t].reshape(-1), words)
