@@ -323,3 +323,15 @@ def test_connector_deferred_writeback_of_early_saves(sz, codebooks):
     torch.cuda.synchronize()
     assert np.array_equal(layer_bytes(kv), exp)
     codec.release(pend)
+    # with preserve_source (prefix caching or chunked prefill may reuse the blocks)
+    # an early save defers nothing and nothing is ever written into the blocks
+    keep = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True, preserve_source=True),
+                              trace=RecordingTrace())
+    pend = keep.save_kv_layer(5, kv, [list(range(96, 112))], transfer_ids=["req-g"],
+                              early=True)
+    assert keep.ready(pend)[0].bits == BITS_TOP16
+    assert keep._deferred_codec_writebacks == {}
+    assert keep.finish_deferred_writebacks(5, kv) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(layer_bytes(kv), exp)
+    keep.release(pend)
