@@ -1,8 +1,8 @@
 """CPU oracle for the splitzip bf16 KV-cache codec.
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
-CPU-baseline leg of ``bench.py`` may import this package, and only as the
-checker (or, for the baseline, as the timed CPU restatement). The product
+CPU-baseline leg of ``bench.py`` may import this package, and only to check
+results against (or, for the baseline, as the timed CPU restatement). The product
 package ``unchainkv_amd`` never imports it; its codec runs on the HIP library
 and fails loudly when that library is missing.
 

@@ -4,7 +4,8 @@
  * TEST INFRASTRUCTURE ONLY. This file restates, in plain C, the algorithm of the
  * reference codec so the HIP kernels can be checked against it. Only tests/,
  * __graft_entry__.smoke() and the CPU-baseline leg of bench.py may load the
- * library built from it, and only as the checker or as the timed CPU baseline.
+ * library built from it, and only to check results against or as the timed CPU
+ * baseline.
  * The product path (unchainkv_amd) never links, imports or calls it.
  *
  * Canonical form. The reference encoder places escape entries with a global
