@@ -584,3 +584,30 @@ def test_payload_ready_carries_gpu_timing_under_trace_cuda():
         else:
             assert set(row) == {"layer", "raw_bytes", "encoded_bytes"}
         assert not pending.timing
+
+
+def test_save_needs_one_transfer_id_per_block_table():
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True))
+    with pytest.raises(ValueError, match="transfer id"):
+        codec.save_kv_layer(0, object(), [[1], [2]], transfer_ids=["only-one"], early=True)
+
+
+def test_cancel_deferred_writebacks_by_transfer_and_layer():
+    from unchainkv_amd.connector import LayerPayload
+
+    trace = RecordingTrace()
+    codec = SplitzipLayerCodec(CodecConfig(top16=True, writeback=True), trace=trace)
+    entries = {}
+    for tid in ("a", "b"):
+        for layer in (1, 2):
+            p = LayerPayload(0, [layer], 2 * MIB, BITS_TOP16, BITS_TOP16, encoded_bytes=9)
+            p.deferred_writeback = True
+            entries[(tid, layer)] = (None, p, None, 0)
+    codec._deferred_codec_writebacks.update(entries)
+    assert codec.cancel_deferred_writebacks(["a"], reason="request_finished") == 2
+    assert set(codec._deferred_codec_writebacks) == {("b", 1), ("b", 2)}
+    assert not entries[("a", 1)][1].deferred_writeback
+    assert codec.cancel_deferred_writebacks(layer_index=2) == 1
+    assert set(codec._deferred_codec_writebacks) == {("b", 1)}
+    assert [f["reason"] for _, f in trace.rows] == ["request_finished"] * 2 + ["cancelled"]
+    assert all(f["source"] == "early" for _, f in trace.rows)
